@@ -1,0 +1,110 @@
+"""ctypes binding of libbcm_event_scan.so, the C ABI declared in
+include/bcm_event_scan.h.
+
+torch is imported first on purpose: the library links the HIP runtime by
+SONAME, so loading it after torch binds it to the runtime torch already uses
+(one set of streams, one device-pointer space). There is no CPU fallback:
+if the library is missing, every entry point raises.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("BCM_LIB_PATH", os.path.join(_HERE, "lib", "libbcm_event_scan.so"))
+
+F32, F16, BF16, U8 = 0, 1, 2, 3
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: U8, torch.uint8: U8}
+
+c_i32, c_i64, c_f32, c_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+
+class ScanArgs(ctypes.Structure):
+    """Mirror of bcm_scan_args (field order and types must match the header)."""
+
+    _fields_ = [
+        ("n_events", c_i64), ("n_channels", c_i32), ("dim", c_i32), ("dstate", c_i32),
+        ("max_seqlen", c_i32), ("n_chunks", c_i32), ("dtype", c_i32),
+        ("u", c_p), ("k", c_p), ("cu_seqlens", c_p), ("dt_idle", c_p), ("dt_active", c_p),
+        ("A", c_p), ("W_B", c_p), ("W_C", c_p), ("D", c_p), ("z", c_p),
+        ("out", c_p), ("out_z", c_p), ("x", c_p),
+        ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
+        ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
+        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p),
+    ]
+
+
+# name -> (restype, argtypes); exactly the functions declared in the header.
+SIGNATURES = {
+    "bcm_abi_version": (c_i32, []),
+    "bcm_last_error": (ctypes.c_char_p, []),
+    "bcm_bitmask_words": (c_i64, [c_i64]),
+    "bcm_tile_count": (c_i64, [c_i64]),
+    "bcm_zero": (c_i32, [c_p, c_i64, c_p]),
+    "bcm_extract_count": (c_i32, [c_p, c_i32, c_i64, c_i64, c_f32, c_p, c_p, c_p]),
+    "bcm_extract_scan": (c_i32, [c_p, c_i64, c_p, c_p, c_p]),
+    "bcm_extract_fill": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
+    "bcm_expand_events": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_p]),
+    "bcm_seqlen_max": (c_i32, [c_p, c_i64, c_p, c_p]),
+    "bcm_gather_fwd": (c_i32, [c_p, c_i32, c_i64, c_i64, c_p, c_p, c_i64, c_p, c_p]),
+    "bcm_gather_bwd": (c_i32, [c_p, c_i32, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p]),
+    "bcm_gather_bwd_rows": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p]),
+    "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_build_event_index": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_i64, c_p]),
+    "bcm_restore_fwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p]),
+    "bcm_restore_bwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load (once) and return the native library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"bc_mamba_amd: native library {LIB_PATH} is not built "
+                "(run `python -m bc_mamba_amd.build`); there is no CPU fallback")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.bcm_abi_version() != 1:
+            raise RuntimeError("bc_mamba_amd: ABI version mismatch")
+        _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Call a C-ABI entry point and turn a non-zero status into RuntimeError."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise RuntimeError(lib().bcm_last_error().decode())
+
+
+def ptr(t):
+    return None if t is None else c_p(t.data_ptr())
+
+
+def dtype_code(dtype):
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise RuntimeError(f"bc_mamba_amd: unsupported dtype {dtype}") from None
+
+
+def stream_of(t):
+    """The current torch stream of t's device as a hipStream_t."""
+    return c_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def bitmask_words(L):
+    return (L + 1023) // 1024 * 32
+
+
+def tile_count(L):
+    return (L + 63) // 64

@@ -1,0 +1,118 @@
+// Shared device and host helpers of libbcm_event_scan (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "bcm_event_scan.h"
+
+namespace bcm {
+
+constexpr int kWave = 64;
+// Sequence steps per restore / gather tile (one 64-bit mask per tile).
+constexpr int kTile = 64;
+
+// ---------------------------------------------------------------- errors
+// Defined in abi.hip; thread-local so concurrent callers do not clobber it.
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* fn);
+// Zero fill with a kernel (abi.hip).
+int zero_bytes(void* ptr, int64_t bytes, hipStream_t s, const char* fn);
+
+inline int64_t bitmask_words(int64_t L) { return ((L + 1023) / 1024) * 32; }
+inline int64_t tile_count(int64_t L) { return (L + kTile - 1) / kTile; }
+inline hipStream_t hs(bcm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- dtypes
+using bf16 = __hip_bfloat16;
+using f16 = __half;
+
+template <typename T> __device__ __forceinline__ float to_f(T v);
+template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f<uint8_t>(uint8_t v) { return (float)v; }
+template <> __device__ __forceinline__ float to_f<f16>(f16 v) { return __half2float(v); }
+template <> __device__ __forceinline__ float to_f<bf16>(bf16 v) { return __bfloat162float(v); }
+
+template <typename T> __device__ __forceinline__ T from_f(float v);
+template <> __device__ __forceinline__ float from_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16 from_f<f16>(float v) { return __float2half_rn(v); }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float v) { return __float2bfloat16(v); }
+
+inline size_t dtype_size(int dt) { return dt == BCM_F32 ? 4 : (dt == BCM_U8 ? 1 : 2); }
+inline bool dtype_ok(int dt) { return dt == BCM_F32 || dt == BCM_F16 || dt == BCM_BF16; }
+
+// Calls fn(T{}) with the C++ type of a dtype code.
+template <typename F> inline void dispatch_dtype(int dt, F&& fn) {
+  if (dt == BCM_F32) fn(float{});
+  else if (dt == BCM_F16) fn(f16{});
+  else fn(bf16{});
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// Orders LDS traffic between the lanes of one wave (no block barrier).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_incl_sum(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Inclusive prefix max over the 64 lanes.
+__device__ __forceinline__ int wave_incl_max(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v = max(v, o);
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Sum over aligned groups of G lanes (result in every lane of the group).
+template <int G> __device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, G);
+  return v;
+}
+
+// 64-bit event mask of one 64-step tile (bitmask words 2j and 2j+1).
+__device__ __forceinline__ uint64_t tile_mask(const uint32_t* row, int64_t j) {
+  const uint2 w = *reinterpret_cast<const uint2*>(row + 2 * j);
+  return (uint64_t)w.x | ((uint64_t)w.y << 32);
+}
+
+// exp2 of a clamped exponent: the decay of the reference scan
+// (selective_scan_common.h:45-52 clamps Δ·A·log2e to [-126, 126]).
+__device__ __forceinline__ float decay(float e) {
+  return __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(e, -126.0f, 126.0f));
+}
+
+}  // namespace bcm

@@ -1,0 +1,454 @@
+// Stage 1: event extraction, expansion and the event gather (fwd / bwd).
+//
+// Reference behaviour: csrc/extract/extract_events_cuda.cu
+//   count_base_kernel :192-208, DeviceScan :361-372, fill_base_kernel
+//   :226-312, build_logical_cu_kernel :449-467, expand_events_direct_kernel
+//   :482-509, gather_events_fwd2_kernel :629-642, scatter_events_bwd2 :649-662.
+//
+// MI355X design: one wave per membrane row. The count pass reads the
+// membrane once with 16-byte loads and packs the threshold bits into a
+// bitmask (1 bit per step, 1/32 of an fp32 membrane); the fill pass reads
+// only that bitmask, turns each lane's 32-step word into events with popcount
+// and a wave prefix sum, stages the segment's event times in LDS and writes
+// ch / t / k (and, fused, the gathered x values and the tile table) with
+// coalesced stores.
+#include "bcm_common.hpp"
+
+#include <type_traits>
+
+namespace bcm {
+
+// ------------------------------------------------------------------ count
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t n_rows, int64_t L, float thr,
+                                               uint32_t* __restrict__ bitmask, int64_t W,
+                                               int32_t* __restrict__ counts) {
+  constexpr int PER = 16 / sizeof(T);  // steps per lane per group
+  constexpr int GS = kWave * PER;      // steps per group
+  constexpr int LPW = 32 / PER;        // lanes per 32-bit word
+  constexpr int WPG = GS / 32;         // words per group
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const T* xr = x + row * L;
+  uint32_t* br = bitmask + row * W;
+  int cnt = 0;
+  const int64_t ng = (L + GS - 1) / GS;
+#pragma unroll 4
+  for (int64_t g = 0; g < ng; ++g) {
+    const int64_t t0 = g * GS + (int64_t)lane * PER;
+    uint32_t bits = 0;
+    if (VEC && t0 + PER <= L) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(xr + t0);
+      const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) bits |= (uint32_t)(to_f(v[i]) > thr) << i;
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        if (t0 + i < L) bits |= (uint32_t)(to_f(xr[t0 + i]) > thr) << i;
+    }
+    cnt += __popc(bits);
+    uint32_t w = bits << (PER * (lane % LPW));
+#pragma unroll
+    for (int m = 1; m < LPW; m <<= 1) w |= __shfl_xor(w, m, kWave);
+    if (lane % LPW == 0) br[g * WPG + lane / LPW] = w;
+  }
+  cnt = wave_sum(cnt);
+  if (lane == 0) counts[row] = cnt;
+}
+
+// ------------------------------------------------------------------- scan
+// One block: exclusive offsets of the per-row counts, total and maximum.
+__global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict__ counts, int64_t n,
+                                                      int32_t* __restrict__ cu, int32_t* __restrict__ meta) {
+  constexpr int ITEMS = 8;
+  __shared__ int s_wsum[16];
+  __shared__ int s_wmax[16];
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+  const int nw = blockDim.x / kWave;
+  int carry = 0, mx = 0;
+  for (int64_t base = 0; base < n; base += (int64_t)blockDim.x * ITEMS) {
+    int v[ITEMS];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int64_t idx = base + (int64_t)tid * ITEMS + i;
+      v[i] = idx < n ? counts[idx] : 0;
+      s += v[i];
+      mx = max(mx, v[i]);
+    }
+    const int incl = wave_incl_sum(s);
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    int woff = 0, total = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int x = s_wsum[w];
+      if (w < wave) woff += x;
+      total += x;
+    }
+    __syncthreads();
+    int run = carry + woff + incl - s;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      run += v[i];
+      const int64_t idx = base + (int64_t)tid * ITEMS + i;
+      if (idx < n) cu[idx + 1] = run;
+    }
+    carry += total;
+  }
+  mx = wave_max(mx);
+  if (lane == 0) s_wmax[wave] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    int m = 0;
+    for (int w = 0; w < nw; ++w) m = max(m, s_wmax[w]);
+    cu[0] = 0;
+    meta[0] = carry;
+    meta[1] = m;
+  }
+}
+
+// ------------------------------------------------------------------- fill
+constexpr int kFillSeg = 64 * 32;  // steps per segment (one word per lane)
+
+template <typename T, bool GATHER, bool TILES>
+__global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitmask, int64_t W,
+                                              const int32_t* __restrict__ base_cu, int64_t n_rows, int64_t L,
+                                              int expand, const T* __restrict__ x, int32_t* __restrict__ ch_ids,
+                                              int32_t* __restrict__ t_steps, int32_t* __restrict__ k_flat,
+                                              T* __restrict__ x_ev, int32_t* __restrict__ tile_start, int64_t nT,
+                                              int32_t* __restrict__ head_flags) {
+  __shared__ int32_t s_t[4][kFillSeg];
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int64_t c = (int64_t)blockIdx.x * 4 + wave;
+  if (c >= n_rows) return;
+  const int32_t cu0 = base_cu[c];
+  const int32_t n = base_cu[c + 1] - cu0;
+  if (TILES && lane == 0) {
+    for (int r = 0; r < expand; ++r)
+      tile_start[(c * expand + r) * (nT + 1) + nT] = cu0 * expand + r * n + n;
+  }
+  if (n <= 0 && !TILES) return;
+  const uint32_t* br = bitmask + c * W;
+  const int64_t nwords = (L + 31) / 32;
+  int32_t* st = s_t[wave];
+  int prev_t = -1;
+  int off = 0;
+  for (int64_t w0 = 0; w0 < nwords; w0 += kWave) {
+    const int64_t w = w0 + lane;
+    const uint32_t word = w < nwords ? br[w] : 0u;
+    const int pc = __popc(word);
+    const int incl = wave_incl_sum(pc);
+    const int excl = incl - pc;
+    const int seg_cnt = __shfl(incl, kWave - 1, kWave);
+    const int last_t = word ? (int)(32 * w + 31 - __clz((int)word)) : -1;
+    const int seg_last = wave_max(last_t);
+    if (TILES && (w % 2 == 0) && (w / 2 < nT)) {
+      for (int r = 0; r < expand; ++r)
+        tile_start[(c * expand + r) * (nT + 1) + w / 2] = cu0 * expand + r * n + off + excl;
+    }
+    uint32_t ww = word;
+    int pos = excl;
+    while (ww) {
+      const int b = __ffs((int)ww) - 1;
+      ww &= ww - 1;
+      st[pos++] = (int)(32 * w + b);
+    }
+    wave_sync();
+    for (int r = 0; r < expand; ++r) {
+      const int64_t lc = c * expand + r;
+      const int64_t obase = (int64_t)cu0 * expand + (int64_t)r * n + off;
+      for (int i = lane; i < seg_cnt; i += kWave) {
+        const int t = st[i];
+        const int tp = i > 0 ? st[i - 1] : prev_t;
+        ch_ids[obase + i] = (int32_t)lc;
+        t_steps[obase + i] = t;
+        k_flat[obase + i] = tp < 0 ? t + 1 : t - tp;
+        if (head_flags) head_flags[obase + i] = tp < 0 ? 1 : 0;
+        if (GATHER) x_ev[obase + i] = x[lc * L + t];
+      }
+    }
+    wave_sync();
+    prev_t = max(prev_t, seg_last);
+    off += seg_cnt;
+  }
+}
+
+// ----------------------------------------------------------------- expand
+__global__ __launch_bounds__(256) void k_expand_cu(const int32_t* __restrict__ base_cu, int64_t n_rows, int expand,
+                                                   int32_t* __restrict__ cu) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c > n_rows) return;
+  if (c < n_rows) {
+    const int32_t s = base_cu[c];
+    const int32_t cnt = base_cu[c + 1] - s;
+    for (int r = 0; r < expand; ++r) cu[c * expand + r] = s * expand + r * cnt;
+  } else {
+    cu[n_rows * expand] = base_cu[n_rows] * expand;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_expand_events(const int32_t* __restrict__ bch, const int32_t* __restrict__ bt,
+                                                       const int32_t* __restrict__ bk,
+                                                       const int32_t* __restrict__ base_cu, int64_t n_rows,
+                                                       int64_t E_base, int expand, int32_t* __restrict__ ch,
+                                                       int32_t* __restrict__ t, int32_t* __restrict__ k) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= E_base) return;
+  const int32_t c = bch[i];
+  if (c < 0 || c >= n_rows) return;
+  const int32_t s = base_cu[c];
+  const int32_t cnt = base_cu[c + 1] - s;
+  const int64_t off = i - s;
+  if (off < 0 || off >= cnt) return;
+  const int32_t tv = bt[i], kv = bk[i];
+  for (int r = 0; r < expand; ++r) {
+    const int64_t pos = (int64_t)s * expand + (int64_t)r * cnt + off;
+    ch[pos] = c * expand + r;
+    t[pos] = tv;
+    k[pos] = kv;
+  }
+}
+
+__global__ __launch_bounds__(1024) void k_seqlen_max(const int32_t* __restrict__ cu, int64_t n,
+                                                     int32_t* __restrict__ out) {
+  __shared__ int s_m[16];
+  int m = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) m = max(m, cu[i + 1] - cu[i]);
+  m = wave_max(m);
+  if (lane_id() == 0) s_m[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int r = 0;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) r = max(r, s_m[w]);
+    out[0] = r;
+  }
+}
+
+// ----------------------------------------------------------------- gather
+template <typename T>
+__global__ __launch_bounds__(256) void k_gather_fwd(const T* __restrict__ x, int64_t n_rows, int64_t L,
+                                                    const int32_t* __restrict__ ch, const int32_t* __restrict__ t,
+                                                    int64_t E, T* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int32_t c = ch[e], s = t[e];
+  const bool ok = c >= 0 && c < n_rows && s >= 0 && s < L;
+  out[e] = ok ? x[(int64_t)c * L + s] : from_f<T>(0.0f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_scatter(const T* __restrict__ g, const int32_t* __restrict__ ch,
+                                                 const int32_t* __restrict__ t, int64_t E, int64_t n_rows, int64_t L,
+                                                 T* __restrict__ dx) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int32_t c = ch[e], s = t[e];
+  if (c >= 0 && c < n_rows && s >= 0 && s < L) dx[(int64_t)c * L + s] = g[e];
+}
+
+// Row-wise gather backward: one wave per (row, 256-step segment); lane l
+// owns steps 4l..4l+3 of the segment and reads its events' gradients at
+// tile_start + rank (rank from the tile's bitmask).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void k_gather_bwd_rows(const T* __restrict__ g, const uint32_t* __restrict__ bitmask,
+                                                         int64_t W, int64_t mrd,
+                                                         const int32_t* __restrict__ tile_start, int64_t nT,
+                                                         int64_t n_rows, int64_t L, int64_t n_seg,
+                                                         T* __restrict__ dx) {
+  const int lane = lane_id();
+  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (wid >= n_rows * n_seg) return;
+  const int64_t row = wid / n_seg, seg = wid - row * n_seg;
+  const int64_t t0 = seg * 256 + 4 * lane;
+  if (t0 >= L) return;
+  const int64_t j = t0 / kTile;
+  const uint64_t m = tile_mask(bitmask + (row / mrd) * W, j);
+  const int off = (int)(t0 - j * kTile);
+  int e = tile_start[row * (nT + 1) + j] + __popcll(m & ((1ull << off) - 1ull));
+  const uint32_t nib = (uint32_t)(m >> off) & 0xFu;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = 0.0f;
+    if ((nib >> i) & 1u) v[i] = to_f(g[e++]);
+  }
+  T* dr = dx + row * L;
+  if (VEC && t0 + 4 <= L) {
+    T o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = from_f<T>(v[i]);
+    if (sizeof(T) == 4) *reinterpret_cast<uint4*>(dr + t0) = *reinterpret_cast<uint4*>(o);
+    else *reinterpret_cast<uint2*>(dr + t0) = *reinterpret_cast<uint2*>(o);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (t0 + i < L) dr[t0 + i] = from_f<T>(v[i]);
+  }
+}
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+static unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace bcm
+
+using namespace bcm;
+
+extern "C" {
+
+int bcm_extract_count(const void* membrane, int dtype, int64_t n_rows, int64_t L, float threshold,
+                      uint32_t* bitmask, int32_t* counts, bcm_stream_t stream) {
+  const char* fn = "bcm_extract_count";
+  if (!dtype_ok(dtype) && dtype != BCM_U8) return set_error(BCM_EINVAL, "%s: membrane must be fp32, fp16, bf16 or u8", fn);
+  if (n_rows < 0 || L < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  if (n_rows == 0) return BCM_OK;
+  if (L == 0) return zero_bytes(counts, n_rows * 4, hs(stream), fn);
+  if (!membrane || !bitmask || !counts) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_rows * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: n_rows * L must fit in int32", fn);
+  const int64_t W = bitmask_words(L);
+  const bool vec = aligned(membrane, 16) && ((L * (int64_t)dtype_size(dtype)) % 16 == 0);
+  const dim3 grid(blocks_for(n_rows, 4)), block(256);
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    const T* x = static_cast<const T*>(membrane);
+    if (vec) hipLaunchKernelGGL((k_count<T, true>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W, counts);
+    else hipLaunchKernelGGL((k_count<T, false>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W, counts);
+  };
+  if (dtype == BCM_U8) go(uint8_t{});
+  else dispatch_dtype(dtype, go);
+  return check_launch(fn);
+}
+
+int bcm_extract_scan(const int32_t* counts, int64_t n_rows, int32_t* cu_seqlens, int32_t* meta,
+                     bcm_stream_t stream) {
+  const char* fn = "bcm_extract_scan";
+  if (n_rows < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  if (!cu_seqlens || !meta || (n_rows > 0 && !counts)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
+  return check_launch(fn);
+}
+
+int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_rows, int64_t L, int64_t expand,
+                     const void* x, int x_dtype, int32_t* ch_ids, int32_t* t_steps, int32_t* k_flat, void* x_events,
+                     int32_t* tile_start, int32_t* head_flags, bcm_stream_t stream) {
+  const char* fn = "bcm_extract_fill";
+  if (n_rows < 0 || L < 0 || expand < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (n_rows == 0 || L == 0) return BCM_OK;
+  if (!bitmask || !base_cu) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if ((x == nullptr) != (x_events == nullptr))
+    return set_error(BCM_EINVAL, "%s: x and x_events must both be given or both be NULL", fn);
+  if (x && !dtype_ok(x_dtype)) return set_error(BCM_EINVAL, "%s: x must be fp32, fp16 or bf16", fn);
+  if (n_rows * expand * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: rows * expand * L must fit in int32", fn);
+  if (tile_start && !aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  const int64_t W = bitmask_words(L), nT = tile_count(L);
+  const dim3 grid(blocks_for(n_rows, 4)), block(256);
+  const int ex = (int)expand;
+  auto launch = [&](auto tag, auto gather, auto tiles) {
+    using T = decltype(tag);
+    constexpr bool G = decltype(gather)::value;
+    constexpr bool TT = decltype(tiles)::value;
+    hipLaunchKernelGGL((k_fill<T, G, TT>), grid, block, 0, hs(stream), bitmask, W, base_cu, n_rows, L, ex,
+                       static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
+                       head_flags);
+  };
+  using Y = std::true_type;
+  using N = std::false_type;
+  if (!ch_ids || !t_steps || !k_flat) return set_error(BCM_EINVAL, "%s: null output pointer", fn);
+  if (x) {
+    dispatch_dtype(x_dtype, [&](auto tag) {
+      if (tile_start) launch(tag, Y{}, Y{});
+      else launch(tag, Y{}, N{});
+    });
+  } else {
+    if (tile_start) launch(float{}, N{}, Y{});
+    else launch(float{}, N{}, N{});
+  }
+  return check_launch(fn);
+}
+
+int bcm_expand_events(const int32_t* base_ch, const int32_t* base_t, const int32_t* base_k, const int32_t* base_cu,
+                      int64_t n_rows, int64_t E_base, int64_t expand, int32_t* ch_ids, int32_t* t_steps,
+                      int32_t* k_flat, int32_t* cu_seqlens, bcm_stream_t stream) {
+  const char* fn = "bcm_expand_events";
+  if (n_rows < 0 || E_base < 0 || expand < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (!base_cu || !cu_seqlens) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if ((n_rows + 1) * expand > INT32_MAX || E_base * expand > INT32_MAX)
+    return set_error(BCM_EINVAL, "%s: expanded sizes must fit in int32", fn);
+  hipLaunchKernelGGL(k_expand_cu, dim3(blocks_for(n_rows + 1, 256)), dim3(256), 0, hs(stream), base_cu, n_rows,
+                     (int)expand, cu_seqlens);
+  int rc = check_launch(fn);
+  if (rc || E_base == 0) return rc;
+  if (!base_ch || !base_t || !base_k || !ch_ids || !t_steps || !k_flat)
+    return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_expand_events, dim3(blocks_for(E_base, 256)), dim3(256), 0, hs(stream), base_ch, base_t,
+                     base_k, base_cu, n_rows, E_base, (int)expand, ch_ids, t_steps, k_flat);
+  return check_launch(fn);
+}
+
+int bcm_seqlen_max(const int32_t* cu_seqlens, int64_t n, int32_t* out, bcm_stream_t stream) {
+  const char* fn = "bcm_seqlen_max";
+  if (n < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  if (!out || (n > 0 && !cu_seqlens)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  hipLaunchKernelGGL(k_seqlen_max, dim3(1), dim3(1024), 0, hs(stream), cu_seqlens, n, out);
+  return check_launch(fn);
+}
+
+int bcm_gather_fwd(const void* x, int dtype, int64_t n_rows, int64_t L, const int32_t* ch_ids,
+                   const int32_t* t_steps, int64_t E, void* out, bcm_stream_t stream) {
+  const char* fn = "bcm_gather_fwd";
+  if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: x must be fp32, fp16 or bf16", fn);
+  if (E < 0 || n_rows < 0 || L < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  if (E == 0) return BCM_OK;
+  if (!x || !ch_ids || !t_steps || !out) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL(k_gather_fwd<T>, dim3(blocks_for(E, 256)), dim3(256), 0, hs(stream),
+                       static_cast<const T*>(x), n_rows, L, ch_ids, t_steps, E, static_cast<T*>(out));
+  });
+  return check_launch(fn);
+}
+
+int bcm_gather_bwd(const void* g, int dtype, const int32_t* ch_ids, const int32_t* t_steps, int64_t E,
+                   int64_t n_rows, int64_t L, void* dx, bcm_stream_t stream) {
+  const char* fn = "bcm_gather_bwd";
+  if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: grad must be fp32, fp16 or bf16", fn);
+  if (E < 0 || n_rows < 0 || L < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  int rc = zero_bytes(dx, n_rows * L * (int64_t)dtype_size(dtype), hs(stream), fn);
+  if (rc || E == 0) return rc;
+  if (!g || !ch_ids || !t_steps) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL(k_scatter<T>, dim3(blocks_for(E, 256)), dim3(256), 0, hs(stream), static_cast<const T*>(g),
+                       ch_ids, t_steps, E, n_rows, L, static_cast<T*>(dx));
+  });
+  return check_launch(fn);
+}
+
+int bcm_gather_bwd_rows(const void* g, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
+                        const int32_t* tile_start, int64_t n_rows, int64_t L, void* dx, bcm_stream_t stream) {
+  const char* fn = "bcm_gather_bwd_rows";
+  if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: grad must be fp32, fp16 or bf16", fn);
+  if (n_rows < 0 || L < 0 || mask_row_div < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (n_rows == 0 || L == 0) return BCM_OK;
+  if (!bitmask || !tile_start || !dx) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  const int64_t W = bitmask_words(L), nT = tile_count(L);
+  const int64_t n_seg = (L + 255) / 256;
+  const size_t es = dtype_size(dtype);
+  const bool vec = aligned(dx, 4 * es) && ((L * (int64_t)es) % (4 * es) == 0);
+  const dim3 grid(blocks_for(n_rows * n_seg, 4)), block(256);
+  dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    if (vec)
+      hipLaunchKernelGGL((k_gather_bwd_rows<T, true>), grid, block, 0, hs(stream), static_cast<const T*>(g), bitmask,
+                         W, mask_row_div, tile_start, nT, n_rows, L, n_seg, static_cast<T*>(dx));
+    else
+      hipLaunchKernelGGL((k_gather_bwd_rows<T, false>), grid, block, 0, hs(stream), static_cast<const T*>(g),
+                         bitmask, W, mask_row_div, tile_start, nT, n_rows, L, n_seg, static_cast<T*>(dx));
+  });
+  return check_launch(fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,290 @@
+"""Drop-in for the event-path pieces of the reference's spike_mamba/e_model.py:
+`RestoreDenseFn` / `restore_dense_fn` (:123-161), `GatherEventsFn` (:167-193),
+`TwoLevelDelta` (:210-230), `SpikeSamplerSurrogate` (:233-254) and the
+`Mamba` block (:258-506) with `extract_events_1d` (:361-409).
+
+The block runs the same composition as the reference: dense in_proj GEMM,
+depthwise causal conv + SiLU (PyTorch-ROCm), then the event path on the HIP
+kernels (extraction, gather, flat selective scan, zero-order-hold restore),
+then out_proj. With `fused_event_path=True` (default) the block calls the
+fused entry points: one extraction pass that also gathers x_conv at the
+events and builds the event index, the restore and the gather backward read
+that index instead of rebuilding it, and the per-block host syncs drop from
+two to one. Results are identical to the unfused composition.
+
+The decode `step` / inference cache of the reference are not part of the
+event path (the reference's own `step` reads an undefined `self.pw_B`).
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from einops import rearrange, repeat
+
+try:
+    from . import _native as _nat
+    from . import extract_events_cuda as _ee_cuda
+    from . import restore_dense_cuda_nodecay
+    from .runtime_breakdown import cuda_stage
+    from .selective_scan_interface import selective_scan_flat_ch_fn
+except ImportError:  # imported with this directory on sys.path
+    import _native as _nat
+    import extract_events_cuda as _ee_cuda
+    import restore_dense_cuda_nodecay
+    from runtime_breakdown import cuda_stage
+    from selective_scan_interface import selective_scan_flat_ch_fn
+
+_HAS_EE_CUDA = True
+_HAS_GATHER_CUDA = True
+
+
+class RestoreDenseFn(torch.autograd.Function):
+    """Zero-order-hold restore. forward(y_flat, time_steps_i32, cu_seqlens,
+    dim, seqlen) -> (B, L, D); backward -> (dy_flat, None, None, None, None)."""
+
+    @staticmethod
+    def forward(ctx, y_flat, time_steps_i32, cu_seqlens, dim: int, seqlen: int):
+        out = restore_dense_cuda_nodecay.restore_dense_fwd(y_flat, time_steps_i32, cu_seqlens, dim, seqlen)
+        ctx.save_for_backward(time_steps_i32, cu_seqlens)
+        ctx.dim, ctx.seqlen = dim, seqlen
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        time_steps_i32, cu_seqlens = ctx.saved_tensors
+        with cuda_stage("restore_backward"):
+            dy = restore_dense_cuda_nodecay.restore_dense_bwd(dout.contiguous(), time_steps_i32, cu_seqlens,
+                                                              ctx.dim, ctx.seqlen)
+        return dy, None, None, None, None
+
+
+def restore_dense_fn(y_flat, time_steps_i32, cu_seqlens, dim: int, seqlen: int):
+    return RestoreDenseFn.apply(y_flat, time_steps_i32, cu_seqlens, dim, seqlen)
+
+
+class GatherEventsFn(torch.autograd.Function):
+    """Differentiable gather of x_conv [B, D, L] at (channel_ids, time_steps);
+    backward scatters into a dense zero tensor."""
+
+    @staticmethod
+    def forward(ctx, x_conv, channel_ids_i32, time_steps_i32):
+        x_c = x_conv.contiguous()
+        out_x = _ee_cuda.gather_events_fwd(x_c, channel_ids_i32, time_steps_i32)[0]
+        ctx.save_for_backward(channel_ids_i32, time_steps_i32)
+        ctx.shape = x_c.shape
+        return out_x
+
+    @staticmethod
+    def backward(ctx, grad_x):
+        channel_ids_i32, time_steps_i32 = ctx.saved_tensors
+        B, D, L = ctx.shape
+        with cuda_stage("gather_scatter_backward"):
+            dx_flat = _ee_cuda.gather_events_bwd(grad_x.contiguous(), channel_ids_i32, time_steps_i32, B * D, L)[0]
+        return dx_flat.view(B, D, L), None, None
+
+
+def _gather_events_cuda(x_conv, channel_ids_i32, time_steps_i32):
+    return GatherEventsFn.apply(x_conv, channel_ids_i32, time_steps_i32)
+
+
+_gather_events_fn = _gather_events_cuda
+
+
+class _IndexedGatherFn(torch.autograd.Function):
+    """x_conv values already gathered by the fused extraction; the backward
+    writes the dense gradient row by row from the event index."""
+
+    @staticmethod
+    def forward(ctx, x_conv, payload, event_index):
+        # payload = (x_events,): kept out of the autograd inputs on purpose
+        ctx.event_index = event_index
+        ctx.shape = x_conv.shape
+        return payload[0]
+
+    @staticmethod
+    def backward(ctx, grad_x):
+        B, D, L = ctx.shape
+        bitmask, tile_start, expand = ctx.event_index
+        g = grad_x.contiguous()
+        dx = torch.empty((B, D, L), dtype=g.dtype, device=g.device)
+        with cuda_stage("gather_scatter_backward"):
+            _nat.call("bcm_gather_bwd_rows", _nat.ptr(g), _nat.dtype_code(g.dtype), _nat.ptr(bitmask), int(expand),
+                      _nat.ptr(tile_start), B * D, L, _nat.ptr(dx), _nat.stream_of(g))
+        return dx, None, None
+
+
+class _IndexedRestoreFn(torch.autograd.Function):
+    """Zero-order-hold restore reading the event index of the fused
+    extraction (same result as RestoreDenseFn)."""
+
+    @staticmethod
+    def forward(ctx, y_flat, event_index, n_ch: int, dim: int, seqlen: int):
+        ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen = event_index, n_ch, dim, seqlen
+        ctx.n_events = int(y_flat.size(0))
+        return restore_dense_cuda_nodecay.restore_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen)
+
+    @staticmethod
+    def backward(ctx, dout):
+        dout = dout.contiguous()
+        dy = torch.empty(ctx.n_events, dtype=torch.float32, device=dout.device)
+        with cuda_stage("restore_backward"):
+            _nat.call("bcm_zero", _nat.ptr(dy), 4 * ctx.n_events, _nat.stream_of(dout))
+            restore_dense_cuda_nodecay.restore_bwd_indexed(dout, ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen, dy)
+        return dy, None, None, None, None
+
+
+class TwoLevelDelta(nn.Module):
+    """Per-channel idle / active steps: dt = softplus(a) + eps (e_model.py:210-230)."""
+
+    def __init__(self, d_inner: int, dt_min=0.001, dt_max=0.1, dt_init_floor=1e-4, eps=1e-6, device=None):
+        super().__init__()
+        self.eps = eps
+        scale = math.log(dt_max) - math.log(dt_min)
+        rand0 = torch.rand(d_inner, device=device) * scale + math.log(dt_min)
+        rand1 = torch.rand(d_inner, device=device) * scale + math.log(dt_min)
+        dt0 = torch.exp(rand0).clamp(min=dt_init_floor)
+        dt1 = torch.exp(rand1).clamp(min=dt_init_floor)
+
+        def inv_sp(y, eps=1e-6):
+            y = y.clamp_min(eps)
+            return torch.log(torch.expm1(y))
+
+        self.a0 = nn.Parameter(inv_sp(dt0))
+        self.a1 = nn.Parameter(inv_sp(dt1))
+
+    def levels(self):
+        return F.softplus(self.a0) + self.eps, F.softplus(self.a1) + self.eps
+
+
+class SpikeSamplerSurrogate(nn.Module):
+    """Bernoulli / threshold spike sampler with a straight-through gradient
+    (e_model.py:233-254)."""
+
+    def __init__(self, mode: str = "ste", sample_inference: bool = False, threshold: float = 0.5):
+        super().__init__()
+        assert mode in ("prob", "ste")
+        self.mode, self.sample_inference, self.threshold = mode, sample_inference, threshold
+
+    def forward(self, p):
+        if self.mode == "prob":
+            if self.training:
+                s = torch.bernoulli(p)
+                return s.detach() + p - p.detach()
+            if self.sample_inference:
+                return torch.bernoulli(p)
+            return (p >= self.threshold).to(dtype=p.dtype)
+        s = (p >= self.threshold).to(dtype=p.dtype)
+        return s.detach() + p - p.detach()
+
+
+class Mamba(nn.Module):
+    """Event-driven Mamba block (e_model.py:258-506), same parameters and
+    initialisation as the reference."""
+
+    def __init__(self, d_model, d_state=16, d_conv=4, expand=2, dt_rank="auto", dt_min=0.001, dt_max=0.1,
+                 dt_init="random", dt_scale=1.0, dt_init_floor=1e-4, conv_bias=True, bias=False,
+                 use_fast_path=False, spiking=True, spike_mode="ste", prob_activation="sigmoid",
+                 sample_inference=False, threshold=0.5, layer_idx=None, device=None, dtype=None,
+                 fused_event_path=True):
+        factory_kwargs = {"device": device, "dtype": dtype}
+        super().__init__()
+        self.d_model, self.d_state, self.d_conv, self.expand = d_model, d_state, d_conv, expand
+        self.d_inner = int(self.expand * self.d_model)
+        self.dt_rank = math.ceil(self.d_model / 16) if dt_rank == "auto" else dt_rank
+        self.use_fast_path = use_fast_path
+        self.layer_idx = layer_idx
+        self.spiking = spiking
+        assert spike_mode in ("ste", "prob")
+        assert prob_activation in ("sigmoid", "clamp")
+        self.spike_mode, self.prob_activation = spike_mode, prob_activation
+        self.sample_inference, self.threshold = sample_inference, threshold
+        self.scan_impl = "flat_ch"
+        self.fused_event_path = fused_event_path
+
+        self.in_proj = nn.Linear(self.d_model, self.d_inner, bias=bias, **factory_kwargs)
+        self.conv1d = nn.Conv1d(in_channels=self.d_inner, out_channels=self.d_inner, bias=conv_bias,
+                                kernel_size=d_conv, groups=self.d_inner, padding=d_conv - 1, **factory_kwargs)
+        self.activation = "silu"
+        self.act = nn.SiLU()
+        fp32_kwargs = {"device": device, "dtype": torch.float32}
+        self.W_BC = nn.Parameter(torch.empty(self.d_inner, self.d_state * 2, **fp32_kwargs))
+        nn.init.normal_(self.W_BC, std=0.02)
+        self.D = nn.Parameter(torch.ones(self.d_inner, **fp32_kwargs))
+        self.D._no_weight_decay = True
+        A = repeat(torch.arange(1, self.d_state + 1, dtype=torch.float32, device=device), "n -> d n",
+                   d=self.d_inner).contiguous()
+        self.A_log = nn.Parameter(torch.log(A))
+        self.A_log._no_weight_decay = True
+        self.out_proj = nn.Linear(self.d_inner, self.d_model, bias=bias, **factory_kwargs)
+        self.prob_head = nn.Linear(self.d_model, self.d_model, bias=True, **factory_kwargs)
+        self.spike_sampler = SpikeSamplerSurrogate(mode=self.spike_mode, sample_inference=self.sample_inference,
+                                                   threshold=self.threshold)
+        self.delta_gen = TwoLevelDelta(self.d_inner, dt_min=dt_min, dt_max=dt_max, dt_init_floor=dt_init_floor,
+                                       device=device)
+
+    def to_spike(self, out):
+        logits = self.prob_head(out)
+        p = torch.sigmoid(logits) if self.prob_activation == "sigmoid" else torch.clamp(logits, 0.0, 1.0)
+        return self.spike_sampler(p)
+
+    def _to_spike(self, out):
+        return self.to_spike(out) if self.spiking else out
+
+    def extract_events_1d(self, hidden_states, x_conv, threshold: float):
+        """Reference composition (e_model.py:361-409): base extraction,
+        expansion, host read of max_seqlen, differentiable gather."""
+        B, L, d_model = hidden_states.shape
+        assert d_model == self.d_model, f"hidden_states last dim {d_model} != self.d_model {self.d_model}"
+        base_input = rearrange(hidden_states, "b l d -> b d l").contiguous()
+        with cuda_stage("routing_index_extraction"):
+            base_ch_ids, base_t_steps, base_k_flat, base_cu_seqlens, _counts, _ms = \
+                _ee_cuda.extract_base_events(base_input, threshold)
+        with cuda_stage("active_token_packing"):
+            channel_ids, time_steps, k_flat, cu_seqlens, max_seqlen_t = _ee_cuda.expand_base_events(
+                base_ch_ids, base_t_steps, base_k_flat, base_cu_seqlens, B, self.d_model, self.expand)
+            max_seqlen = int(max_seqlen_t.item())
+        with cuda_stage("active_gather_forward"):
+            x_conv_flat = _gather_events_fn(x_conv, channel_ids, time_steps)
+        return channel_ids, time_steps, k_flat, cu_seqlens, max_seqlen, x_conv_flat
+
+    def _conv(self, x, seqlen):
+        return self.act(self.conv1d(x)[..., :seqlen])
+
+    def forward(self, hidden_states, inference_params=None):
+        if inference_params is not None:
+            raise RuntimeError("Mamba: the decode / inference-cache path is not part of the event-path build")
+        batch, seqlen, dim = hidden_states.shape
+        x = rearrange(self.in_proj.weight @ rearrange(hidden_states, "b l d -> d (b l)"), "d (b l) -> b d l",
+                      l=seqlen)
+        if self.in_proj.bias is not None:
+            x = x + rearrange(self.in_proj.bias.to(dtype=x.dtype), "d -> d 1")
+        x = self._conv(x, seqlen).contiguous()
+
+        dt_idle, dt_active = self.delta_gen.levels()
+        A = -torch.exp(self.A_log)
+        W_B = self.W_BC[:, :self.d_state].contiguous()
+        W_C = self.W_BC[:, self.d_state:].contiguous()
+        n_ch = batch * self.d_inner
+
+        if self.fused_event_path:
+            base_input = rearrange(hidden_states.detach(), "b l d -> b d l").contiguous()
+            with cuda_stage("routing_index_extraction"):
+                _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_ev, event_index = \
+                    _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach())
+            with cuda_stage("active_gather_forward"):
+                x_conv_flat = _IndexedGatherFn.apply(x, (x_ev,), event_index)
+        else:
+            _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_conv_flat = self.extract_events_1d(
+                hidden_states, x, self.threshold)
+
+        with cuda_stage("sparse_scan_forward"):
+            y_flat, _ = selective_scan_flat_ch_fn(x_conv_flat, k_flat, cu_seqlens, int(max_seqlen), dt_idle,
+                                                  dt_active, A, W_B, W_C, self.D, None, tile_offsets=None,
+                                                  tile_chunk_size=0, is_depthwise_bc=True, pw_B=None, pw_C=None)
+        with cuda_stage("dense_restoration_forward"):
+            if self.fused_event_path:
+                y_dense = _IndexedRestoreFn.apply(y_flat, event_index, n_ch, self.d_inner, seqlen)
+            else:
+                y_dense = restore_dense_fn(y_flat, time_steps.to(torch.int32), cu_seqlens, self.d_inner, seqlen)
+        return self.out_proj(y_dense)

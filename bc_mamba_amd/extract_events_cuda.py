@@ -1,0 +1,197 @@
+"""Drop-in for the reference extension module `extract_events_cuda`
+(csrc/extract/extract_events_cuda.cu, bindings :759-798), backed by the HIP
+kernels of libbcm_event_scan.so.
+
+Same function names, argument order, return lists, dtypes and error style
+as the reference; every check raises RuntimeError with the reference's
+message. Outputs are allocated with torch on the input's device and filled
+by the native library on the current stream.
+"""
+import torch
+
+try:
+    from . import _native as _nat
+except ImportError:  # imported with this directory on sys.path
+    import _native as _nat
+
+__all__ = ["extract_events", "extract_base_events", "expand_base_events",
+           "gather_events_fwd", "gather_events_bwd", "extract_events_indexed"]
+
+_I32 = torch.int32
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _empty_i32(n, dev):
+    return torch.empty(n, dtype=_I32, device=dev)
+
+
+def _count_scan(x2d, dtype_code, threshold):
+    """Passes 1-2: bitmask, counts, cu_seqlens, meta=(E, max) on the device."""
+    NC, L = x2d.shape
+    dev = x2d.device
+    bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
+    counts = _empty_i32(NC, dev)
+    cu = _empty_i32(NC + 1, dev)
+    meta = _empty_i32(2, dev)
+    s = _nat.stream_of(x2d)
+    _nat.call("bcm_extract_count", _nat.ptr(x2d), dtype_code, NC, L, float(threshold),
+              _nat.ptr(bitmask), _nat.ptr(counts), s)
+    _nat.call("bcm_extract_scan", _nat.ptr(counts), NC, _nat.ptr(cu), _nat.ptr(meta), s)
+    return bitmask, counts, cu, meta
+
+
+def extract_base_events(base_input, threshold):
+    """base_input [B, d_model, L] fp32/fp16/bf16 -> [ch_ids, t_steps, k_flat,
+    cu_seqlens, counts, max_seqlen] (extract_events_cuda.cu:324-418).
+
+    An event is float(base_input[b, d, t]) > float(threshold); events are
+    channel-major (channel = b*d_model + d), time-ascending; k = t+1 for a
+    channel's first event, else the gap to the previous one. One host sync
+    reads the total event count to size the outputs, like the reference."""
+    _check(base_input.is_cuda, "base_input must be CUDA")
+    _check(base_input.is_contiguous(), "base_input must be contiguous")
+    _check(base_input.dim() == 3, "base_input must be 3-D [B, d_model, L]")
+    _check(base_input.dtype in (torch.float32, torch.float16, torch.bfloat16),
+           "base_input must be fp32, fp16 or bf16")
+    B, Dm, L = base_input.shape
+    dev = base_input.device
+    with torch.cuda.device(dev):
+        x2d = base_input.view(B * Dm, L)
+        bitmask, counts, cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold)
+        E = int(meta[0].item())
+        if E == 0:
+            ei = torch.zeros(0, dtype=_I32, device=dev)
+            return [ei, ei, ei, cu, counts, torch.zeros(1, dtype=_I32, device=dev)]
+        ch, t, k = _empty_i32(E, dev), _empty_i32(E, dev), _empty_i32(E, dev)
+        _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(cu), B * Dm, L, 1, None, 0,
+                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), None, None, None, _nat.stream_of(x2d))
+        return [ch, t, k, cu, counts, meta[1].clone()]
+
+
+def expand_base_events(base_ch_ids, base_t_steps, base_k_flat, base_cu_seqlens, B, d_model, expand):
+    """Replicate base channel c into logical channels c*expand + r
+    (repeat_interleave order) -> [channel_ids, time_steps, k_flat,
+    cu_seqlens, max_seqlen] (extract_events_cuda.cu:529-603)."""
+    _check(base_ch_ids.is_cuda, "base_ch_ids must be CUDA")
+    _check(base_ch_ids.is_contiguous(), "base_ch_ids must be contiguous")
+    NC_base = int(B) * int(d_model)
+    NC_inner = NC_base * int(expand)
+    E_base = int(base_ch_ids.size(0))
+    dev = base_ch_ids.device
+    with torch.cuda.device(dev):
+        if E_base == 0:
+            ei = torch.zeros(0, dtype=_I32, device=dev)
+            return [ei, ei, ei, torch.zeros(NC_inner + 1, dtype=_I32, device=dev),
+                    torch.zeros(1, dtype=_I32, device=dev)]
+        for name, tns in (("base_t_steps", base_t_steps), ("base_k_flat", base_k_flat),
+                          ("base_cu_seqlens", base_cu_seqlens)):
+            _check(tns.is_cuda and tns.dtype == _I32 and tns.is_contiguous(),
+                   f"{name} must be a contiguous int32 CUDA tensor")
+        _check(base_ch_ids.dtype == _I32, "base_ch_ids must be int32")
+        _check(base_cu_seqlens.numel() >= NC_base + 1, "base_cu_seqlens must have B*d_model+1 entries")
+        E = E_base * int(expand)
+        ch, t, k = _empty_i32(E, dev), _empty_i32(E, dev), _empty_i32(E, dev)
+        cu = _empty_i32(NC_inner + 1, dev)
+        s = _nat.stream_of(base_ch_ids)
+        _nat.call("bcm_expand_events", _nat.ptr(base_ch_ids), _nat.ptr(base_t_steps), _nat.ptr(base_k_flat),
+                  _nat.ptr(base_cu_seqlens), NC_base, E_base, int(expand), _nat.ptr(ch), _nat.ptr(t),
+                  _nat.ptr(k), _nat.ptr(cu), s)
+        ms = torch.empty((), dtype=_I32, device=dev)
+        _nat.call("bcm_seqlen_max", _nat.ptr(base_cu_seqlens), NC_base, _nat.ptr(ms), s)
+        return [ch, t, k, cu, ms]
+
+
+def extract_events(mask):
+    """LEGACY: bool mask [B, D, L] -> [ch_ids, t_steps, k_flat, cu_seqlens,
+    max_seqlen, head_flags] (extract_events_cuda.cu:117-179)."""
+    _check(mask.is_cuda, "mask must be a CUDA tensor")
+    _check(mask.is_contiguous(), "mask must be contiguous")
+    _check(mask.dtype == torch.bool, "mask must be bool")
+    B, D, L = mask.shape
+    dev = mask.device
+    with torch.cuda.device(dev):
+        x2d = mask.view(B * D, L)
+        bitmask, counts, cu, meta = _count_scan(x2d, _nat.U8, 0.5)
+        E = int(meta[0].item())
+        if E == 0:
+            ei = torch.zeros(0, dtype=_I32, device=dev)
+            return [ei, ei, ei, cu, torch.zeros(1, dtype=_I32, device=dev), ei]
+        ch, t, k, hf = (_empty_i32(E, dev) for _ in range(4))
+        _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(cu), B * D, L, 1, None, 0,
+                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), None, None, _nat.ptr(hf), _nat.stream_of(x2d))
+        return [ch, t, k, cu, meta[1].clone(), hf]
+
+
+def gather_events_fwd(x, channel_ids, time_steps):
+    """out_x[e] = x.view(NC, L)[channel_ids[e], time_steps[e]] -> [out_x]
+    (extract_events_cuda.cu:670-708)."""
+    _check(x.is_cuda, "gather_events_fwd: x must be a CUDA tensor")
+    _check(x.is_contiguous(), "gather_events_fwd: x must be contiguous")
+    _check(channel_ids.dtype == _I32, "gather_events_fwd: channel_ids must be int32")
+    _check(time_steps.dtype == _I32, "gather_events_fwd: time_steps must be int32")
+    _check(x.dim() == 3, "gather_events_fwd: x must be 3-D [B, D, L]")
+    B, D, L = x.shape
+    E = int(channel_ids.size(0))
+    out = torch.empty(E, dtype=x.dtype, device=x.device)
+    if E == 0:
+        return [out]
+    with torch.cuda.device(x.device):
+        _nat.call("bcm_gather_fwd", _nat.ptr(x), _nat.dtype_code(x.dtype), B * D, L,
+                  _nat.ptr(channel_ids.contiguous()), _nat.ptr(time_steps.contiguous()), E,
+                  _nat.ptr(out), _nat.stream_of(x))
+    return [out]
+
+
+def gather_events_bwd(grad_x, channel_ids, time_steps, NC, L):
+    """dx [NC, L] = 0 except dx[channel_ids[e], time_steps[e]] = grad_x[e]
+    -> [dx] (extract_events_cuda.cu:717-754). (ch, t) pairs must be unique."""
+    _check(grad_x.is_cuda, "gather_events_bwd: grad tensor must be CUDA")
+    _check(channel_ids.dtype == _I32, "gather_events_bwd: channel_ids must be int32")
+    _check(time_steps.dtype == _I32, "gather_events_bwd: time_steps must be int32")
+    NC, L = int(NC), int(L)
+    dx = torch.empty((NC, L), dtype=grad_x.dtype, device=grad_x.device)
+    with torch.cuda.device(grad_x.device):
+        g = grad_x.contiguous()
+        _nat.call("bcm_gather_bwd", _nat.ptr(g), _nat.dtype_code(g.dtype), _nat.ptr(channel_ids.contiguous()),
+                  _nat.ptr(time_steps.contiguous()), int(g.size(0)), NC, L, _nat.ptr(dx), _nat.stream_of(g))
+    return [dx]
+
+
+def extract_events_indexed(base_input, threshold, expand=1, x=None):
+    """Fused extraction for the block forward (no reference counterpart; the
+    reference composes extract_base_events + expand_base_events +
+    gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
+    max_seqlen as a Python int, x_events or None, event_index) where
+    event_index = (bitmask, tile_start, expand) feeds the restore and the
+    row-wise gather backward. One host sync (E and max_seqlen together)."""
+    _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
+           "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
+    B, Dm, L = base_input.shape
+    expand = int(expand)
+    dev = base_input.device
+    with torch.cuda.device(dev):
+        x2d = base_input.view(B * Dm, L)
+        bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold)
+        E_base, max_seqlen = (int(v) for v in meta.tolist())
+        NCi = B * Dm * expand
+        cu = base_cu if expand == 1 else _empty_i32(NCi + 1, dev)
+        s = _nat.stream_of(x2d)
+        if expand != 1:
+            _nat.call("bcm_expand_events", None, None, None, _nat.ptr(base_cu), B * Dm, 0, expand,
+                      None, None, None, _nat.ptr(cu), s)
+        E = E_base * expand
+        ch, t, k = _empty_i32(E, dev), _empty_i32(E, dev), _empty_i32(E, dev)
+        tile_start = torch.empty((NCi, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
+        xe = None
+        if x is not None:
+            _check(x.is_cuda and x.is_contiguous() and tuple(x.shape) == (B, Dm * expand, L),
+                   "x must be a contiguous CUDA tensor [B, d_model*expand, L]")
+            xe = torch.empty(E, dtype=x.dtype, device=dev)
+        _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(base_cu), B * Dm, L, expand,
+                  _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(ch), _nat.ptr(t),
+                  _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), None, s)
+        return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)

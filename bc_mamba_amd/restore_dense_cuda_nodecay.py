@@ -1,0 +1,117 @@
+"""Drop-in for the reference extension module `restore_dense_cuda_nodecay`
+(csrc/r_nodecay/restore_dense.cpp, bindings :207-226), backed by the HIP
+restore kernels of libbcm_event_scan.so.
+
+restore_dense_fwd(y_flat, time_steps, cu_seqlens, dim, seqlen, out_dtype=None)
+    -> (B, L, D): out[b, t, d] = y of the last event of channel b*dim+d at or
+       before t (zero-order hold), 0 before the channel's first event.
+restore_dense_bwd(dout, time_steps, cu_seqlens, dim, seqlen)
+    -> dy (E,) float32: sum of dout over the steps each event holds.
+
+time_steps must be strictly increasing inside each channel (as produced by
+extraction). Unlike the reference (exact up to 4095 events per channel),
+every channel length is exact.
+"""
+import torch
+
+try:
+    from . import _native as _nat
+except ImportError:  # imported with this directory on sys.path
+    import _native as _nat
+
+__all__ = ["restore_dense_fwd", "restore_dense_bwd", "build_event_index", "restore_fwd_indexed",
+           "restore_bwd_indexed"]
+
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _check(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def build_event_index(time_steps, cu_seqlens, seqlen, zero_f32=None):
+    """(bitmask, tile_start) of per-channel sorted time steps; optionally
+    zero-fills the float32 tensor zero_f32 in the same launch."""
+    n_ch = int(cu_seqlens.size(0)) - 1
+    dev = time_steps.device
+    bitmask = torch.empty((n_ch, _nat.bitmask_words(seqlen)), dtype=torch.int32, device=dev)
+    tile_start = torch.empty((n_ch, _nat.tile_count(seqlen) + 1), dtype=torch.int32, device=dev)
+    _nat.call("bcm_build_event_index", _nat.ptr(time_steps), _nat.ptr(cu_seqlens), n_ch, int(seqlen),
+              _nat.ptr(bitmask), _nat.ptr(tile_start), _nat.ptr(zero_f32),
+              int(zero_f32.numel()) if zero_f32 is not None else 0, _nat.stream_of(time_steps))
+    return bitmask, tile_start
+
+
+def restore_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen, out_dtype=None):
+    """Restore forward from an event index (bitmask, tile_start, expand)."""
+    bitmask, tile_start, mrd = event_index
+    out_dtype = y_flat.dtype if out_dtype is None else out_dtype
+    out = torch.empty((n_ch // dim, seqlen, dim), dtype=out_dtype, device=y_flat.device)
+    _nat.call("bcm_restore_fwd", _nat.ptr(y_flat), _nat.dtype_code(y_flat.dtype), _nat.ptr(bitmask), int(mrd),
+              _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(out), _nat.dtype_code(out_dtype),
+              _nat.stream_of(y_flat))
+    return out
+
+
+def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy):
+    """Restore backward from an event index into a zeroed float32 dy."""
+    bitmask, tile_start, mrd = event_index
+    _nat.call("bcm_restore_bwd", _nat.ptr(dout), _nat.dtype_code(dout.dtype), _nat.ptr(bitmask), int(mrd),
+              _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), _nat.stream_of(dout))
+    return dy
+
+
+def restore_dense_fwd(y_flat, time_steps, cu_seqlens, dim, seqlen, out_dtype=None):
+    """Zero-order-hold restore forward (restore_dense.cpp:43-130)."""
+    fn = "restore_dense_fwd"
+    _check(y_flat.dtype in _FLOATS, f"{fn}: y_flat must be fp32, fp16, or bf16")
+    _check(time_steps.dtype == torch.int32, f"{fn}: time_steps must be int32 (torch.int32)")
+    _check(cu_seqlens.dtype == torch.int32, f"{fn}: cu_seqlens must be int32 (torch.int32)")
+    _check(y_flat.is_cuda and time_steps.is_cuda and cu_seqlens.is_cuda, f"{fn}: all tensors must be on CUDA")
+    _check(y_flat.is_contiguous() and time_steps.is_contiguous() and cu_seqlens.is_contiguous(),
+           f"{fn}: all tensors must be contiguous")
+    _check(y_flat.dim() == 1, f"{fn}: y_flat must be 1-D")
+    _check(time_steps.shape == y_flat.shape, f"{fn}: time_steps shape must equal y_flat shape")
+    _check(cu_seqlens.dim() == 1, f"{fn}: cu_seqlens must be 1-D")
+    dim, seqlen = int(dim), int(seqlen)
+    _check(dim >= 1, f"{fn}: dim must be >= 1")
+    _check(seqlen >= 1, f"{fn}: seqlen must be >= 1")
+    n_ch = int(cu_seqlens.size(0)) - 1
+    _check(n_ch >= 1, f"{fn}: cu_seqlens must have at least 2 elements")
+    _check(n_ch % dim == 0, f"{fn}: n_channels (B*D) must be divisible by dim")
+    out_dtype = y_flat.dtype if out_dtype is None else out_dtype
+    _check(out_dtype in _FLOATS, f"{fn}: out_dtype must be fp32, fp16, or bf16")
+    if y_flat.dtype == torch.float16:
+        _check(out_dtype == torch.float16, f"{fn}: fp16 input only supports fp16 output")
+    if y_flat.dtype == torch.bfloat16:
+        _check(out_dtype == torch.bfloat16, f"{fn}: bf16 input only supports bf16 output")
+    with torch.cuda.device(y_flat.device):
+        bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen)
+        return restore_fwd_indexed(y_flat, (bitmask, tile_start, 1), n_ch, dim, seqlen, out_dtype)
+
+
+def restore_dense_bwd(dout, time_steps, cu_seqlens, dim, seqlen):
+    """Zero-order-hold restore backward -> dy (E,) float32
+    (restore_dense.cpp:138-202)."""
+    fn = "restore_dense_bwd"
+    _check(dout.dtype in _FLOATS, f"{fn}: dout must be fp32/fp16/bf16")
+    _check(time_steps.dtype == torch.int32, f"{fn}: time_steps must be int32")
+    _check(cu_seqlens.dtype == torch.int32, f"{fn}: cu_seqlens must be int32")
+    _check(dout.is_cuda and time_steps.is_cuda and cu_seqlens.is_cuda, f"{fn}: all tensors must be on CUDA")
+    _check(dout.is_contiguous() and time_steps.is_contiguous() and cu_seqlens.is_contiguous(),
+           f"{fn}: all tensors must be contiguous")
+    dim, seqlen = int(dim), int(seqlen)
+    _check(dim >= 1, f"{fn}: dim must be >= 1")
+    _check(seqlen >= 1, f"{fn}: seqlen must be >= 1")
+    n_ch = int(cu_seqlens.size(0)) - 1
+    _check(dout.dim() == 3, f"{fn}: dout must be 3-D (B, L, D)")
+    _check(dout.size(1) == seqlen, f"{fn}: dout.size(1) must equal seqlen")
+    _check(dout.size(2) == dim, f"{fn}: dout.size(2) must equal dim (D)")
+    _check(dout.size(0) * dim == n_ch, f"{fn}: dout.size(0)*dim must equal n_channels")
+    dy = torch.empty(int(time_steps.size(0)), dtype=torch.float32, device=dout.device)
+    with torch.cuda.device(dout.device):
+        bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen, zero_f32=dy)
+        if n_ch > 0:
+            restore_bwd_indexed(dout, (bitmask, tile_start, 1), n_ch, dim, seqlen, dy)
+    return dy

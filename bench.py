@@ -1,0 +1,285 @@
+"""Benchmark of the event-sparse path on one MI355X.
+
+One step = one fwd+bwd pass of the whole path over the config's synthetic
+batch, inputs resident in HBM:
+  forward : extract (count -> offsets -> host read of E -> fill, with x_conv
+            gathered at the events and the event index built in the same
+            pass) -> flat selective scan -> zero-order-hold restore
+  backward: restore backward -> selective scan backward -> gather backward
+All stages run in libbcm_event_scan.so on torch's current stream. Prints one
+JSON line (metric / value / roofline / cpu_baseline ...).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--cfg 1] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd events/s & achieved HBM GB/s, B32 D256 L2048 N16 at 15% density"
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
+    """Compulsory traffic of the path's API contract, each tensor once
+    (x_conv read and dx written dense)."""
+    M = B * D * L
+    NC = B * D
+    n_ch = max(1, -(-max_seqlen // 2048))
+    st = NC * n_ch * N * 8
+    return {
+        "fwd_extract_gather": M // expand * s_m + M * s_u + 3 * E * 4 + E * s_u + 4 * (NC + 1),
+        "fwd_scan": E * s_u + E * 4 + E * s_u + st,
+        "fwd_restore": E * s_u + E * 4 + M * s_o,
+        "bwd_restore": M * s_o + E * 4 + E * 4,
+        "bwd_scan": E * s_u + E * 4 + E * s_u + st + E * s_u,
+        "bwd_gather": E * s_u + 2 * E * 4 + M * s_u,
+    }
+
+
+class Path:
+    """The fwd+bwd path driven through the C ABI with reusable buffers."""
+
+    KERNELS = ["count", "offsets", "fill", "scan_fwd", "restore_fwd", "zero_dy", "restore_bwd", "scan_bwd",
+               "gather_bwd"]
+
+    def __init__(self, w, dev):
+        import torch
+        from bc_mamba_amd import _native as nat
+        self.t, self.nat, self.w, self.dev = torch, nat, w, dev
+        B, D, L = w.B, w.D, w.L
+        self.NC = B * D
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.bitmask = torch.empty((self.NC, nat.bitmask_words(L)), **i32)
+        self.counts = torch.empty(self.NC, **i32)
+        self.cu = torch.empty(self.NC + 1, **i32)
+        self.meta = torch.empty(2, **i32)
+        self.meta_h = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
+        self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
+        self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
+        self.E = -1
+        self.events = {}
+
+    def _alloc(self, E, ms):
+        t, dev, w = self.t, self.dev, self.w
+        i32 = dict(dtype=t.int32, device=dev)
+        self.E, self.ms = E, ms
+        self.ch, self.ts, self.k = (t.empty(E, **i32) for _ in range(3))
+        self.u = t.empty(E, dtype=w.dtype, device=dev)
+        self.y = t.empty(E, dtype=w.dtype, device=dev)
+        self.dy32 = t.empty(E, dtype=t.float32, device=dev)
+        self.du = t.empty(E, dtype=w.dtype, device=dev)
+        self.n_chunks = max(1, -(-ms // 2048))
+        self.x = t.empty((self.NC, self.n_chunks, 2 * w.N), dtype=t.float32, device=dev)
+        f32 = dict(dtype=t.float32, device=dev)
+        self.grads = [t.empty((w.D, w.N), **f32) for _ in range(3)] + [t.empty(w.D, **f32) for _ in range(3)]
+
+    def _scan_args(self):
+        nat, w = self.nat, self.w
+        a = nat.ScanArgs()
+        a.n_events, a.n_channels, a.dim, a.dstate = self.E, self.NC, w.D, w.N
+        a.max_seqlen, a.n_chunks, a.dtype = self.ms, self.n_chunks, nat.dtype_code(w.dtype)
+        a.u, a.k, a.cu_seqlens = self.u.data_ptr(), self.k.data_ptr(), self.cu.data_ptr()
+        a.dt_idle, a.dt_active = w.dt_idle.data_ptr(), w.dt_active.data_ptr()
+        a.A, a.W_B, a.W_C, a.D = w.A.data_ptr(), w.W_B.data_ptr(), w.W_C.data_ptr(), w.D_skip.data_ptr()
+        a.out, a.x = self.y.data_ptr(), self.x.data_ptr()
+        a.dout, a.x_saved, a.du = self.dy.data_ptr(), self.x.data_ptr(), self.du.data_ptr()
+        a.dA, a.dW_B, a.dW_C, a.ddt_idle, a.ddt_active, a.dD = (g.data_ptr() for g in self.grads)
+        return a
+
+    def step(self, timed=()):
+        """One fwd+bwd. Kernels named in `timed` get HIP events around them."""
+        t, nat, w = self.t, self.nat, self.w
+        s = nat.stream_of(self.counts)
+        P = nat.ptr
+        ev = self.events
+
+        def mark(name, fn):
+            if name in timed:
+                a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                a.record()
+                fn()
+                b.record()
+                ev.setdefault(name, []).append((a, b))
+            else:
+                fn()
+
+        B, D, L = w.B, w.D, w.L
+        mark("count", lambda: nat.call("bcm_extract_count", P(w.membrane), nat.dtype_code(w.membrane.dtype),
+                                       self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), s))
+        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta), s))
+        self.meta_h.copy_(self.meta, non_blocking=True)
+        t.cuda.current_stream().synchronize()
+        E, ms = int(self.meta_h[0]), int(self.meta_h[1])
+        if E != self.E or ms != getattr(self, "ms", -1):
+            self._alloc(E, ms)
+            self.dy = self.dy32 if w.dtype == t.float32 else t.empty(E, dtype=w.dtype, device=self.dev)
+            self.args = self._scan_args()
+        mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
+                                      nat.dtype_code(w.dtype), P(self.ch), P(self.ts), P(self.k), P(self.u),
+                                      P(self.tile_start), None, s))
+        mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
+        mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), P(self.bitmask), 1,
+                                             P(self.tile_start), self.NC, D, L, P(self.dense),
+                                             nat.dtype_code(w.dtype), s))
+        mark("zero_dy", lambda: nat.call("bcm_zero", P(self.dy32), 4 * E, s))
+        mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), nat.dtype_code(w.dtype), P(self.bitmask),
+                                             1, P(self.tile_start), self.NC, D, L, P(self.dy32), s))
+        if self.dy is not self.dy32:
+            self.dy.copy_(self.dy32)
+        mark("scan_bwd", lambda: nat.call("bcm_scan_bwd", self.args, s))
+        mark("gather_bwd", lambda: nat.call("bcm_gather_bwd_rows", P(self.du), nat.dtype_code(w.dtype),
+                                            P(self.bitmask), 1, P(self.tile_start), self.NC, L, P(self.dx), s))
+
+    def kernel_ms(self, name):
+        self.t.cuda.synchronize()
+        v = [a.elapsed_time(b) for a, b in self.events.get(name, [])]
+        return sum(v) / len(v) if v else float("nan")
+
+
+def cpu_baseline(cfg, batches, reps=3):
+    """The torch CPU restatement of the path (oracle/torch_path.py) on a
+    bounded sample of the workload: `batches` of the config's B batches."""
+    import torch
+    from bc_mamba_amd.workloads import CONFIGS, make_workload
+    from oracle import torch_path as tp
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    w = make_workload(cfg, B=batches)
+    args = (w.membrane, w.x_conv.float(), w.dout.float(), w.threshold, w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C,
+            w.D_skip)
+    tp.path_fwd_bwd(*args)  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        _, _, E = tp.path_fwd_bwd(*args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": E / med, "unit": "events/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config {cfg} with B={batches} of its {CONFIGS[cfg]['B']} batches "
+                      f"(E={E} events), torch fp32 restatement (oracle/torch_path.py), median of {reps} "
+                      f"fwd+bwd reps, {cpu}", "seconds_per_rep": med}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cfg", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-batches", type=int, default=4)
+    ap.add_argument("--api", action="store_true", help="also time the drop-in Python API path (autograd)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the path shards by batch with no exchange; "
+              "multi-GPU runs are not part of it)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from bc_mamba_amd import _native
+    from bc_mamba_amd.workloads import make_workload
+    _native.lib()
+    dev = torch.device("cuda:0")
+    w = make_workload(args.cfg).to(dev)
+    path = Path(w, dev)
+
+    # untimed pre-pass: per-kernel durations pick the dominant kernel
+    for _ in range(max(args.warmup, 1)):
+        path.step(timed=Path.KERNELS)
+    per_kernel = {n: path.kernel_ms(n) for n in Path.KERNELS}
+    dominant = max(per_kernel, key=per_kernel.get)
+    path.events.clear()
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        path.step(timed=(dominant,))
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    dom_ms = path.kernel_ms(dominant)
+
+    E, ms = path.E, path.ms
+    su = torch.tensor([], dtype=w.dtype).element_size()
+    alg = algorithmic_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su)
+    total_bytes = sum(alg.values())
+    # algorithmic bytes of one launch of each kernel (its share of the API-contract traffic)
+    kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC, "offsets": 8 * path.NC,
+                    "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
+                    "restore_fwd": alg["fwd_restore"], "zero_dy": 4 * E, "restore_bwd": alg["bwd_restore"],
+                    "scan_bwd": alg["bwd_scan"], "gather_bwd": alg["bwd_gather"]}
+    dom_gbs = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": E / (ms_per_step * 1e-3),
+        "unit": "events/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[w.dtype],
+        "data": "synthetic",
+        "config": {"workload": f"config {args.cfg}: extract+gather -> flat scan -> ZOH restore, fwd+bwd",
+                   "B": w.B, "D": w.D, "L": w.L, "N": w.N, "events": E, "density": E / (w.B * w.D * w.L),
+                   "max_seqlen": ms},
+        "achieved_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
+        "algorithmic_bytes": total_bytes,
+        "path_frac_of_hbm_peak": total_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_ms": per_kernel,
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None, "launch_ms": dom_ms,
+                     "bytes_per_launch": kernel_bytes[dominant]},
+    }
+    if args.api:
+        result["api_ms_per_step"] = api_path_ms(w, dev, args.steps, args.warmup)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cfg, args.cpu_batches)
+    print(json.dumps(result), flush=True)
+
+
+def api_path_ms(w, dev, steps, warmup):
+    """ms per fwd+bwd through the drop-in Python modules with autograd."""
+    import torch
+    from bc_mamba_amd import e_model
+    from bc_mamba_amd import extract_events_cuda as ee
+    from bc_mamba_amd.selective_scan_interface import selective_scan_flat_ch_fn
+    params = [p.detach().requires_grad_(True) for p in (w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, w.D_skip)]
+    x_conv = w.x_conv.detach().requires_grad_(True)
+
+    def one():
+        ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+        u = e_model.GatherEventsFn.apply(x_conv, ch, t)
+        y, _ = selective_scan_flat_ch_fn(u, k, cu, int(ms), *params[:5], D=params[5], is_depthwise_bc=True)
+        e_model.restore_dense_fn(y, t, cu, w.D, w.L).backward(w.dout)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+if __name__ == "__main__":
+    main()

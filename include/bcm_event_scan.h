@@ -1,0 +1,206 @@
+/*
+ * bcm_event_scan.h - C ABI of the MI355X (gfx950) event-sparse selective-scan
+ * library (libbcm_event_scan.so).
+ *
+ * The library implements BC_mamba's event path in three stages, each with a
+ * forward and a backward:
+ *   1. event extraction  : dense membrane -> per-channel event streams
+ *   2. flat selective scan over the packed events (depthwise B/C mode)
+ *   3. zero-order-hold restore of event outputs to a dense (B, L, D) tensor
+ *
+ * Conventions (all entry points):
+ *   - every pointer is a device pointer unless stated otherwise; the caller
+ *     allocates every input, output and workspace buffer; the library never
+ *     allocates device memory and holds no state other than a thread-local
+ *     error string, so calls on different streams may run concurrently;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream) of
+ *     the current device; no entry point synchronises the host;
+ *   - the return value is BCM_OK or an error code; bcm_last_error() returns
+ *     a message that starts with the entry point's name;
+ *   - dtype codes: BCM_F32 / BCM_F16 / BCM_BF16 (the reference accepts the
+ *     same three for u / z / out / dout / membrane / restore in and out);
+ *   - index tensors (channel ids, time steps, gaps k, cu_seqlens) are int32,
+ *     channel-major (channel = b * D + d), time-ascending inside a channel.
+ *
+ * Internal event index (produced by bcm_extract_fill or
+ * bcm_build_event_index, consumed by restore and the row-wise gather
+ * backward): a bitmask [rows, bcm_bitmask_words(L)] of uint32 words (bit t%32
+ * of word t/32 set iff an event at step t) and a tile table
+ * [channels, bcm_tile_count(L) + 1] of int32 holding, for every 64-step tile,
+ * the absolute index of the channel's first event at or after the tile start.
+ */
+#ifndef BCM_EVENT_SCAN_H
+#define BCM_EVENT_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BCM_ABI_VERSION 1
+
+typedef struct ihipStream_t* bcm_stream_t; /* == hipStream_t */
+
+enum bcm_dtype { BCM_F32 = 0, BCM_F16 = 1, BCM_BF16 = 2, BCM_U8 = 3 /* bool / byte membrane only */ };
+enum bcm_status { BCM_OK = 0, BCM_EINVAL = 1, BCM_EHIP = 2 };
+
+/* ---- library ------------------------------------------------------------ */
+int bcm_abi_version(void);
+const char* bcm_last_error(void);
+/* words per bitmask row for sequence length L (a multiple of 32) */
+int64_t bcm_bitmask_words(int64_t L);
+/* number of 64-step tiles per row: ceil(L / 64) */
+int64_t bcm_tile_count(int64_t L);
+/* zero `bytes` bytes at `ptr` with a fill kernel (no hipMemset: graph-safe) */
+int bcm_zero(void* ptr, int64_t bytes, bcm_stream_t stream);
+
+/* ---- (1) event extraction ----------------------------------------------- */
+/* Pass 1 of extract_base_events (csrc/extract/extract_events_cuda.cu:192-208
+ * count_base_kernel): event = float(membrane[row, t]) > threshold (strict).
+ * membrane [n_rows, L] of `dtype` (BCM_U8 reads a bool/byte mask, used by the
+ * legacy extract_events with threshold 0.5); writes bitmask [n_rows, words]
+ * and counts [n_rows]. */
+int bcm_extract_count(const void* membrane, int dtype, int64_t n_rows,
+                      int64_t L, float threshold, uint32_t* bitmask,
+                      int32_t* counts, bcm_stream_t stream);
+
+/* Pass 2 (extract_events_cuda.cu:361-372, DeviceScan + cu[0]=0 + counts.max):
+ * cu_seqlens[0] = 0, cu_seqlens[i+1] = sum(counts[0..i]);
+ * meta[0] = total events E, meta[1] = max(counts) (0 when n_rows == 0). */
+int bcm_extract_scan(const int32_t* counts, int64_t n_rows,
+                     int32_t* cu_seqlens, int32_t* meta, bcm_stream_t stream);
+
+/* Pass 3 (extract_events_cuda.cu:226-312 fill_base_kernel, fused with
+ * expand_events_direct_kernel :482-509 and gather_events_fwd2_kernel
+ * :629-642). Emits the events of every base row c into the `expand` logical
+ * channels c*expand + r at positions base_cu[c]*expand + r*count_c + i:
+ * ch_ids, t_steps, k_flat (k = t+1 for a channel's first event, else the gap
+ * to the previous event). Optional (NULL to skip): x [n_rows*expand, L] of
+ * x_dtype gathered at the events into x_events [E*expand]; tile_start
+ * [n_rows*expand, tile_count+1]; head_flags [E*expand] (1 at a channel's
+ * first event, else 0: the legacy extract_events output, :102-114). */
+int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu,
+                     int64_t n_rows, int64_t L, int64_t expand,
+                     const void* x, int x_dtype, int32_t* ch_ids,
+                     int32_t* t_steps, int32_t* k_flat, void* x_events,
+                     int32_t* tile_start, int32_t* head_flags,
+                     bcm_stream_t stream);
+
+/* expand_base_events (extract_events_cuda.cu:529-603): logical cu_seqlens
+ * [n_rows*expand+1] and expanded streams [E_base*expand]. */
+int bcm_expand_events(const int32_t* base_ch, const int32_t* base_t,
+                      const int32_t* base_k, const int32_t* base_cu,
+                      int64_t n_rows, int64_t E_base, int64_t expand,
+                      int32_t* ch_ids, int32_t* t_steps, int32_t* k_flat,
+                      int32_t* cu_seqlens, bcm_stream_t stream);
+
+/* out[0] = max_i (cu[i+1] - cu[i]) over n channels (extract_events_cuda.cu
+ * :598-600 diff.max()); 0 when n == 0. */
+int bcm_seqlen_max(const int32_t* cu_seqlens, int64_t n, int32_t* out,
+                   bcm_stream_t stream);
+
+/* gather_events_fwd (extract_events_cuda.cu:670-708):
+ * out[e] = x[ch_ids[e] * L + t_steps[e]], x viewed as [rows, L]. */
+int bcm_gather_fwd(const void* x, int dtype, int64_t n_rows, int64_t L,
+                   const int32_t* ch_ids, const int32_t* t_steps, int64_t E,
+                   void* out, bcm_stream_t stream);
+
+/* gather_events_bwd (extract_events_cuda.cu:717-754): dx [n_rows, L] = 0
+ * except dx[ch_ids[e], t_steps[e]] = g[e]; (ch, t) pairs must be unique. */
+int bcm_gather_bwd(const void* g, int dtype, const int32_t* ch_ids,
+                   const int32_t* t_steps, int64_t E, int64_t n_rows,
+                   int64_t L, void* dx, bcm_stream_t stream);
+
+/* Same result as bcm_gather_bwd for channel-major sorted streams, written
+ * row by row from the event index (no zero pass, no scatter). The bitmask
+ * row of channel ch is ch / mask_row_div. */
+int bcm_gather_bwd_rows(const void* g, int dtype, const uint32_t* bitmask,
+                        int64_t mask_row_div, const int32_t* tile_start,
+                        int64_t n_rows, int64_t L, void* dx,
+                        bcm_stream_t stream);
+
+/* ---- (2) flat per-channel selective scan -------------------------------- */
+/* Argument block of the depthwise flat_ch scan; mirrors SSMParamsFlatSeg /
+ * SSMParamsFlatSegBwd (csrc/selective_scan/selective_scan.h:151-283) minus
+ * the fields that the flat_ch path never reads. Set unused pointers to NULL.
+ *   Δ_i   = dt_idle[d]*(k_i-1) + dt_active[d],  d = ch % dim
+ *   a_i,s = exp2(clamp(Δ_i*A[d,s]*log2(e), -126, 126))
+ *   h_i,s = a_i,s*h_{i-1},s + Δ_i*u_i*(u_i*W_B[d,s])
+ *   y_i   = D[d]*u_i + sum_s h_i,s*(u_i*W_C[d,s]);  out_z = y*silu(z)   */
+typedef struct bcm_scan_args {
+  int64_t n_events;    /* E */
+  int32_t n_channels;  /* NC = len(cu_seqlens) - 1 */
+  int32_t dim;         /* A.shape[0] */
+  int32_t dstate;      /* A.shape[1], <= 256 */
+  int32_t max_seqlen;  /* max events per channel */
+  int32_t n_chunks;    /* max(1, ceil(max_seqlen / 2048)) */
+  int32_t dtype;       /* dtype of u, z, out, out_z, dout, du, dz */
+  const void* u;               /* [E] */
+  const int32_t* k;            /* [E] */
+  const int32_t* cu_seqlens;   /* [NC + 1] */
+  const float* dt_idle;        /* [dim] */
+  const float* dt_active;      /* [dim] */
+  const float* A;              /* [dim, dstate] */
+  const float* W_B;            /* [dim, dstate] */
+  const float* W_C;            /* [dim, dstate] */
+  const float* D;              /* [dim] or NULL */
+  const void* z;               /* [E] or NULL */
+  /* forward outputs */
+  void* out;                   /* [E] ungated y */
+  void* out_z;                 /* [E] y * silu(z), when z != NULL */
+  float* x;                    /* [NC, n_chunks, 2*dstate]: (prod a, h) */
+  /* backward inputs */
+  const void* dout;            /* [E] */
+  const float* x_saved;        /* [NC, n_chunks, 2*dstate] from forward */
+  const void* out_saved;       /* [E] ungated forward output (z only) */
+  /* backward outputs (fully written, no zero-init needed) */
+  void* du;                    /* [E] */
+  float* dA;                   /* [dim, dstate] */
+  float* dW_B;                 /* [dim, dstate] */
+  float* dW_C;                 /* [dim, dstate] */
+  float* ddt_idle;             /* [dim] */
+  float* ddt_active;           /* [dim] */
+  float* dD;                   /* [dim] or NULL */
+  void* dz;                    /* [E] when z != NULL */
+} bcm_scan_args;
+
+/* selective_scan_fwd_flat_ch, depthwise mode (selective_scan.cpp:674-884,
+ * selective_scan_fwd_kernel.cuh:403-728). */
+int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream);
+/* selective_scan_bwd_flat_ch, depthwise mode (selective_scan.cpp:890-1153,
+ * selective_scan_bwd_kernel.cuh:635-1169). */
+int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream);
+
+/* ---- (3) zero-order-hold restore ---------------------------------------- */
+/* Event index of sorted per-channel time steps (the restore kernels' input
+ * when the caller has no bitmask): bitmask [n_rows, words], tile_start
+ * [n_rows, tiles+1]. Steps outside [0, L) are ignored. If zero_f32 != NULL,
+ * zero_f32[0 .. n_zero) is set to 0 (zero-init of the restore backward). */
+int bcm_build_event_index(const int32_t* t_steps, const int32_t* cu_seqlens,
+                          int64_t n_rows, int64_t L, uint32_t* bitmask,
+                          int32_t* tile_start, float* zero_f32,
+                          int64_t n_zero, bcm_stream_t stream);
+
+/* restore_dense_fwd (csrc/r_nodecay/restore_dense.cpp:43-130,
+ * restore_dense_fwd_kernel.cuh:38-114): out[b, t, d] = y[e] for the last
+ * event e of channel b*dim+d with t_e <= t, 0 before the first event.
+ * out (n_rows/dim, L, dim) of out_dtype, fully written. */
+int bcm_restore_fwd(const void* y, int y_dtype, const uint32_t* bitmask,
+                    int64_t mask_row_div, const int32_t* tile_start,
+                    int64_t n_rows, int64_t dim, int64_t L, void* out,
+                    int out_dtype, bcm_stream_t stream);
+
+/* restore_dense_bwd (restore_dense.cpp:138-202,
+ * restore_dense_bwd_kernel.cuh:42-112): dy[e] += sum of dout[b, t, d] over
+ * t in [t_e, t_next). dy [E] float32 must be zero on entry. */
+int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask,
+                    int64_t mask_row_div, const int32_t* tile_start,
+                    int64_t n_rows, int64_t dim, int64_t L, float* dy,
+                    bcm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BCM_EVENT_SCAN_H */

@@ -1,0 +1,75 @@
+"""The C-ABI library loads and exports exactly what include/bcm_event_scan.h
+declares; host-side argument checks report errors without touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+import bc_mamba_amd._native as nat
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "bcm_event_scan.h")
+
+
+def _header_text():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return re.sub(r"//[^\n]*", "", txt)
+
+
+def header_functions():
+    return set(re.findall(r"\b(bcm_[a-z0-9_]+)\s*\(", _header_text()))
+
+
+def header_struct_fields():
+    body = re.search(r"typedef struct bcm_scan_args \{(.*?)\} bcm_scan_args;", _header_text(), re.S).group(1)
+    return [m.group(1) for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*;", body)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(nat.LIB_PATH):
+        from bc_mamba_amd import build
+        build.build()
+    return nat.lib()
+
+
+def test_header_declares_exactly_the_bound_functions():
+    assert header_functions() == set(nat.SIGNATURES)
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_scan_args_layout_matches_header():
+    assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 24 pointers
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 24 * 8
+
+
+def test_host_helpers(lib):
+    assert lib.bcm_abi_version() == 1
+    assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64
+    assert lib.bcm_bitmask_words(1) == 32 and lib.bcm_bitmask_words(1025) == 64
+    assert lib.bcm_tile_count(2048) == nat.tile_count(2048) == 32
+    assert lib.bcm_tile_count(65) == 2
+
+
+def test_invalid_arguments_are_rejected_before_launch(lib):
+    rc = lib.bcm_extract_count(None, 7, 4, 16, 0.5, None, None, None)
+    assert rc == 1 and lib.bcm_last_error().decode().startswith("bcm_extract_count")
+    assert lib.bcm_scan_fwd(None, None) == 1
+    assert lib.bcm_last_error().decode().startswith("bcm_scan_fwd")
+    a = nat.ScanArgs()
+    a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 4, 2, 300, 10, 1, 0
+    assert lib.bcm_scan_bwd(a, None) == 1 and "dstate" in lib.bcm_last_error().decode()
+    a.dstate, a.n_chunks = 16, 2
+    assert lib.bcm_scan_fwd(a, None) == 1 and "n_chunks" in lib.bcm_last_error().decode()
+    assert lib.bcm_restore_fwd(None, 0, None, 1, None, 10, 3, 8, None, 0, None) == 1
+    assert "divisible" in lib.bcm_last_error().decode()
+    assert lib.bcm_restore_fwd(None, 1, None, 1, None, 8, 4, 8, None, 0, None) == 1
+    assert "fp16 input only supports fp16 output" in lib.bcm_last_error().decode()

@@ -1,0 +1,157 @@
+"""GPU parity of stage 2 (flat per-channel selective scan, depthwise mode)
+against the CPU oracle: forward out / out_z / saved state x and every
+gradient, within rtol 1e-4 for fp32 inputs and 2e-2 for bf16/fp16 inputs."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from bc_mamba_amd import selective_scan_cuda as ssc
+from bc_mamba_amd import selective_scan_interface as ssi
+from conftest import assert_close
+from oracle import event_path as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3)}
+
+
+def _case(B, D, L, p, N, dtype, seed, with_z=False, with_D=True, empty_every=0, dim=None):
+    g = torch.Generator().manual_seed(seed)
+    mem = (torch.rand(B, D, L, generator=g) < p).float()
+    if empty_every:
+        mem.view(B * D, L)[::empty_every] = 0.0
+    ch, t, k, cu, counts, ms = orc.extract_base_events(mem.numpy(), 0.5)
+    dim = D if dim is None else dim
+    E = len(ch)
+    u = torch.randn(E, generator=g).to(dtype)
+    dout = torch.randn(E, generator=g).to(dtype)
+    z = torch.randn(E, generator=g).to(dtype) if with_z else None
+    dt_i = torch.nn.functional.softplus(torch.randn(dim, generator=g) - 2.0)
+    dt_a = torch.nn.functional.softplus(torch.randn(dim, generator=g) - 2.0)
+    A = -torch.exp(torch.rand(dim, N, generator=g) * math.log(16.0))
+    WB = torch.randn(dim, N, generator=g) / math.sqrt(N)
+    WC = torch.randn(dim, N, generator=g) / math.sqrt(N)
+    Dv = torch.randn(dim, generator=g) if with_D else None
+    return dict(ch=ch, k=k, cu=cu, ms=ms, u=u, dout=dout, z=z, dt_i=dt_i, dt_a=dt_a, A=A, WB=WB, WC=WC, D=Dv)
+
+
+def _run_and_check(c, dtype, dev):
+    f32 = lambda x: None if x is None else x.float().numpy()
+    cud = lambda x: None if x is None else x.to(dev)
+    k_t = torch.from_numpy(c["k"]).to(dev)
+    cu_t = torch.from_numpy(c["cu"]).to(dev)
+    args = (cud(c["u"]), k_t, cu_t, c["ms"], cud(c["dt_i"]), cud(c["dt_a"]), cud(c["A"]), cud(c["WB"]), cud(c["WC"]))
+    res = ssc.fwd_flat_ch(*args, D=cud(c["D"]), z=cud(c["z"]), is_depthwise_bc=True)
+    ref = orc.scan_fwd(f32(c["u"]), c["k"], c["cu"], c["ms"], f32(c["dt_i"]), f32(c["dt_a"]), f32(c["A"]),
+                       f32(c["WB"]), f32(c["WC"]), f32(c["D"]), f32(c["z"]))
+    rtol, atol = TOL[dtype]
+    assert res[0].dtype == dtype and res[1].dtype == torch.float32
+    assert_close(res[0].float().cpu(), ref[0], rtol, atol, "out")
+    assert_close(res[1].cpu(), ref[1], rtol, atol, "x")
+    if c["z"] is not None:
+        assert_close(res[2].float().cpu(), ref[2], rtol, atol, "out_z")
+    gb = ssc.bwd_flat_ch(*args, cud(c["dout"]), res[1], D=cud(c["D"]), z=cud(c["z"]),
+                         out=res[0] if c["z"] is not None else None, is_depthwise_bc=True)
+    # the backward's z-gate reads the stored (rounded) forward output
+    out_used = res[0].float().cpu().numpy() if c["z"] is not None else None
+    gref = orc.scan_bwd(f32(c["u"]), c["k"], c["cu"], c["ms"], f32(c["dt_i"]), f32(c["dt_a"]), f32(c["A"]),
+                        f32(c["WB"]), f32(c["WC"]), f32(c["dout"]), f32(c["D"]), f32(c["z"]), out_used)
+    names = ["du", "dA", "dW_B", "dW_C", "ddt_idle", "ddt_active"]
+    for i, n in enumerate(names):
+        assert_close(gb[i].float().cpu(), gref[i], rtol, atol, n)
+    i = 6
+    if c["D"] is not None:
+        assert_close(gb[i].cpu(), gref[6], rtol, atol, "dD")
+        i += 1
+    if c["z"] is not None:
+        assert_close(gb[i].float().cpu(), gref[7], rtol, atol, "dz")
+    return res, gb
+
+
+SHAPES = [  # B, D, L, density, N  (max_seqlen lands in each kernel-shape bucket)
+    (2, 8, 100, 0.5, 16),     # <= 64
+    (2, 8, 230, 0.5, 16),     # <= 128
+    (2, 8, 450, 0.5, 16),     # <= 256
+    (2, 8, 2048, 0.15, 16),   # <= 384 (config-1 density)
+    (2, 4, 900, 0.5, 16),     # <= 512
+    (1, 4, 1900, 0.5, 16),    # <= 1024
+    (1, 3, 3000, 0.6, 16),    # <= 2048
+    (1, 2, 6000, 0.7, 8),     # > 2048: three 2048-event chunks
+    (2, 4, 300, 0.5, 1),
+    (2, 4, 300, 0.5, 7),
+    (2, 4, 700, 0.4, 64),
+    (1, 4, 700, 0.4, 65),
+    (1, 2, 300, 0.5, 256),
+]
+
+
+@pytest.mark.parametrize("B,D,L,p,N", SHAPES)
+def test_scan_fp32(cuda_device, B, D, L, p, N):
+    print(f"scan case B={B} D={D} L={L} p={p} N={N}", flush=True)
+    _run_and_check(_case(B, D, L, p, N, torch.float32, seed=L + N), torch.float32, cuda_device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_z", [False, True])
+def test_scan_half_inputs(cuda_device, dtype, with_z):
+    _run_and_check(_case(2, 8, 1200, 0.2, 16, dtype, seed=3, with_z=with_z), dtype, cuda_device)
+
+
+@pytest.mark.parametrize("with_D", [False, True])
+def test_scan_z_gate_fp32(cuda_device, with_D):
+    _run_and_check(_case(2, 6, 600, 0.3, 16, torch.float32, seed=5, with_z=True, with_D=with_D),
+                   torch.float32, cuda_device)
+
+
+def test_scan_empty_channels(cuda_device):
+    _run_and_check(_case(2, 8, 500, 0.3, 16, torch.float32, seed=6, empty_every=3), torch.float32, cuda_device)
+
+
+def test_scan_no_events(cuda_device):
+    c = _case(1, 4, 50, 0.0, 16, torch.float32, seed=7)
+    assert len(c["ch"]) == 0
+    res, gb = _run_and_check(c, torch.float32, cuda_device)
+    assert torch.count_nonzero(res[1]) == 0 and all(torch.count_nonzero(g) == 0 for g in gb[1:])
+
+
+def test_scan_channels_not_multiple_of_dim(cuda_device):
+    c = _case(1, 10, 300, 0.3, 16, torch.float32, seed=8, dim=4)  # 10 channels, d = ch % 4
+    _run_and_check(c, torch.float32, cuda_device)
+
+
+def test_scan_clamped_decays(cuda_device):
+    c = _case(2, 4, 1500, 0.05, 16, torch.float32, seed=9)
+    c["A"] = c["A"] * 600.0  # long gaps: Δ·A·log2e far below -126
+    _run_and_check(c, torch.float32, cuda_device)
+
+
+def test_autograd_function_matches_raw(cuda_device):
+    c = _case(2, 8, 800, 0.2, 16, torch.float32, seed=10, with_z=True)
+    dev = cuda_device
+    leaves = {n: c[n].to(dev).requires_grad_(True) for n in ("u", "dt_i", "dt_a", "A", "WB", "WC", "D", "z")}
+    k_t, cu_t = torch.from_numpy(c["k"]).to(dev), torch.from_numpy(c["cu"]).to(dev)
+    out, x = ssi.selective_scan_flat_ch_fn(leaves["u"], k_t, cu_t, c["ms"], leaves["dt_i"], leaves["dt_a"],
+                                           leaves["A"], leaves["WB"], leaves["WC"], D=leaves["D"], z=leaves["z"],
+                                           is_depthwise_bc=True)
+    assert not x.requires_grad
+    out.backward(c["dout"].to(dev))
+    raw = ssc.fwd_flat_ch(*(leaves[n].detach() for n in ("u",)), k_t, cu_t, c["ms"],
+                          *(leaves[n].detach() for n in ("dt_i", "dt_a", "A", "WB", "WC")),
+                          D=leaves["D"].detach(), z=leaves["z"].detach(), is_depthwise_bc=True)
+    assert torch.equal(out.detach(), raw[2])
+    gb = ssc.bwd_flat_ch(leaves["u"].detach(), k_t, cu_t, c["ms"],
+                         *(leaves[n].detach() for n in ("dt_i", "dt_a", "A", "WB", "WC")),
+                         c["dout"].to(dev), raw[1], D=leaves["D"].detach(), z=leaves["z"].detach(), out=raw[0],
+                         is_depthwise_bc=True)
+    for name, g in zip(("u", "A", "WB", "WC", "dt_i", "dt_a", "D", "z"), (gb[0], gb[1], gb[2], gb[3], gb[4], gb[5],
+                                                                         gb[6], gb[7])):
+        assert torch.equal(leaves[name].grad, g), name
+
+
+def test_scan_is_deterministic(cuda_device):
+    c = _case(4, 8, 1000, 0.2, 16, torch.float32, seed=11)
+    r1, g1 = _run_and_check(c, torch.float32, cuda_device)
+    r2, g2 = _run_and_check(c, torch.float32, cuda_device)
+    assert all(torch.equal(a, b) for a, b in zip(r1, r2)) and all(torch.equal(a, b) for a, b in zip(g1, g2))

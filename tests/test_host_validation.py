@@ -1,0 +1,97 @@
+"""The drop-in modules reject bad inputs with the reference's messages
+(RuntimeError, message naming the entry point) before any device work."""
+import pytest
+import torch
+
+from bc_mamba_amd import extract_events_cuda as ee
+from bc_mamba_amd import restore_dense_cuda_nodecay as rd
+from bc_mamba_amd import selective_scan_cuda as ssc
+from bc_mamba_amd import selective_scan_interface as ssi
+
+i32 = torch.int32
+
+
+@pytest.fixture
+def fake_cuda(monkeypatch):
+    """Lets host tensors pass the device check so the later checks are
+    reached; every case below fails before any device work."""
+    monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
+
+
+def _scan_inputs(E=5, NC=2, dim=2, N=4):
+    return dict(u_flat=torch.randn(E), k_flat=torch.ones(E, dtype=i32), cu_seqlens=torch.tensor([0, 2, 5], dtype=i32),
+                max_seqlen=3, dt_idle=torch.rand(dim), dt_active=torch.rand(dim), A=-torch.rand(dim, N),
+                B=torch.randn(dim, N), C=torch.randn(dim, N))
+
+
+def test_scan_rejects_host_tensors():
+    with pytest.raises(RuntimeError, match="selective_scan_fwd_flat_ch: all tensors must be CUDA tensors"):
+        ssc.fwd_flat_ch(**_scan_inputs(), is_depthwise_bc=True)
+
+
+@pytest.mark.parametrize("field,bad,msg", [
+    ("k_flat", torch.ones(5, dtype=torch.int64), "k_flat must be int32"),
+    ("A", -torch.rand(2, 4, dtype=torch.float64), "A must be float32"),
+    ("u_flat", torch.randn(5, dtype=torch.float64), "u_flat must be fp16/bf16/fp32"),
+    ("A", -torch.rand(2, 300), "dstate must be <= 256"),
+])
+def test_scan_dtype_and_shape_checks(field, bad, msg, fake_cuda):
+    args = _scan_inputs()
+    args[field] = bad
+    with pytest.raises(RuntimeError, match=msg):
+        ssc.fwd_flat_ch(**args, is_depthwise_bc=True)
+
+
+def test_scan_unsupported_modes_raise(fake_cuda):
+    a = _scan_inputs()
+    with pytest.raises(RuntimeError, match="only the depthwise B/C mode"):
+        ssc.fwd_flat_ch(**a, is_depthwise_bc=False)
+    with pytest.raises(RuntimeError, match="pointwise"):
+        ssc.fwd_flat_ch(**a, is_depthwise_bc=True, pw_B=torch.eye(2), pw_C=torch.eye(2))
+
+
+def test_bwd_checks_x_chunks():
+    args = _scan_inputs()
+    with pytest.raises(RuntimeError, match="selective_scan_bwd_flat_ch"):
+        ssc.bwd_flat_ch(**args, dout_flat=torch.randn(5, dtype=torch.float16), x=torch.zeros(2, 1, 8),
+                        is_depthwise_bc=True)
+
+
+def test_restore_checks():
+    y, t, cu = torch.randn(4), torch.tensor([0, 3, 1, 2], dtype=i32), torch.tensor([0, 2, 4], dtype=i32)
+    with pytest.raises(RuntimeError, match="restore_dense_fwd: all tensors must be on CUDA"):
+        rd.restore_dense_fwd(y, t, cu, 1, 8)
+    with pytest.raises(RuntimeError, match="restore_dense_fwd: time_steps must be int32"):
+        rd.restore_dense_fwd(y, t.long(), cu, 1, 8)
+    with pytest.raises(RuntimeError, match="restore_dense_fwd: y_flat must be fp32, fp16, or bf16"):
+        rd.restore_dense_fwd(y.double(), t, cu, 1, 8)
+    with pytest.raises(RuntimeError, match="restore_dense_bwd: all tensors must be on CUDA"):
+        rd.restore_dense_bwd(torch.zeros(2, 8), t, cu, 1, 8)
+
+
+def test_restore_shape_checks(fake_cuda):
+    t, cu = torch.tensor([0, 3, 1, 2], dtype=i32), torch.tensor([0, 2, 4], dtype=i32)
+    with pytest.raises(RuntimeError, match="restore_dense_bwd: dout must be 3-D"):
+        rd.restore_dense_bwd(torch.zeros(2, 8), t, cu, 1, 8)
+    with pytest.raises(RuntimeError, match="restore_dense_fwd: n_channels \\(B\\*D\\) must be divisible by dim"):
+        rd.restore_dense_fwd(torch.zeros(4), t, cu, 3, 8)
+    with pytest.raises(RuntimeError, match="bf16 input only supports bf16 output"):
+        rd.restore_dense_fwd(torch.zeros(4, dtype=torch.bfloat16), t, cu, 1, 8, torch.float32)
+
+
+def test_extract_checks():
+    with pytest.raises(RuntimeError, match="base_input must be CUDA"):
+        ee.extract_base_events(torch.zeros(1, 2, 3), 0.5)
+    with pytest.raises(RuntimeError, match="mask must be a CUDA tensor"):
+        ee.extract_events(torch.zeros(1, 2, 3, dtype=torch.bool))
+    with pytest.raises(RuntimeError, match="gather_events_fwd: x must be a CUDA tensor"):
+        ee.gather_events_fwd(torch.zeros(1, 2, 3), torch.zeros(1, dtype=i32), torch.zeros(1, dtype=i32))
+    with pytest.raises(RuntimeError, match="gather_events_bwd: grad tensor must be CUDA"):
+        ee.gather_events_bwd(torch.zeros(1), torch.zeros(1, dtype=i32), torch.zeros(1, dtype=i32), 1, 3)
+
+
+def test_interface_exports_reference_names():
+    assert callable(ssi.selective_scan_flat_ch_fn)
+    assert issubclass(ssi.SelectiveScanFlatChFn, torch.autograd.Function)
+    with pytest.raises(RuntimeError, match="not part of"):
+        ssi.selective_scan_depthwise_bc_fn()

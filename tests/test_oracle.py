@@ -1,0 +1,273 @@
+"""Pins the CPU oracle (oracle/event_path.py) against independent
+formulations, closed forms, brute force and invariants. No GPU needed."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close
+from oracle import event_path as orc
+from oracle import torch_path as tp
+
+RNG = np.random.default_rng(1234)
+
+
+def _params(D, N, rng):
+    f32 = np.float32
+    dt_i = np.log1p(np.exp(rng.standard_normal(D) - 2.0)).astype(f32)
+    dt_a = np.log1p(np.exp(rng.standard_normal(D) - 2.0)).astype(f32)
+    A = (-np.exp(rng.random((D, N)) * math.log(16.0))).astype(f32)
+    WB = (rng.standard_normal((D, N)) / math.sqrt(N)).astype(f32)
+    WC = (rng.standard_normal((D, N)) / math.sqrt(N)).astype(f32)
+    Dv = rng.standard_normal(D).astype(f32)
+    return dt_i, dt_a, A, WB, WC, Dv
+
+
+def _stream(B, D, L, p, rng):
+    mem = (rng.random((B, D, L)) < p).astype(np.float32)
+    ch, t, k, cu, counts, ms = orc.extract_base_events(mem, 0.5)
+    return mem, ch, t, k, cu, ms
+
+
+# ------------------------------------------------------------- extraction
+def test_extract_brute_force():
+    x = RNG.standard_normal((2, 3, 37)).astype(np.float32)
+    ch, t, k, cu, counts, ms = orc.extract_base_events(x, 0.25)
+    exp_ch, exp_t, exp_k = [], [], []
+    for c in range(6):
+        prev = -1
+        for s in range(37):
+            if x.reshape(6, 37)[c, s] > np.float32(0.25):
+                exp_ch.append(c)
+                exp_t.append(s)
+                exp_k.append(s + 1 if prev < 0 else s - prev)
+                prev = s
+    assert ch.tolist() == exp_ch and t.tolist() == exp_t and k.tolist() == exp_k
+    assert cu[0] == 0 and cu[-1] == len(exp_t)
+    assert ms == max(np.bincount(np.array(exp_ch), minlength=6))
+
+
+def test_extract_strict_threshold_and_invariants():
+    x = np.array([[[0.5, 0.5000001, 0.4999, 1.0, 0.5]]], dtype=np.float32)
+    ch, t, k, cu, counts, ms = orc.extract_base_events(x, 0.5)
+    assert t.tolist() == [1, 3] and k.tolist() == [2, 2]
+    mem, ch, t, k, cu, ms = _stream(3, 5, 200, 0.2, RNG)
+    assert np.all(np.diff(cu) >= 0) and np.all(np.diff(ch) >= 0)
+    for c in range(15):
+        s, e = cu[c], cu[c + 1]
+        assert np.array_equal(np.cumsum(k[s:e]) - 1, t[s:e])  # gaps rebuild the times
+        assert np.all(ch[s:e] == c)
+
+
+def test_expand_closed_form():
+    mem, ch, t, k, cu, ms = _stream(2, 3, 50, 0.3, RNG)
+    e1 = orc.expand_base_events(ch, t, k, cu, 2, 3, 1)
+    assert all(np.array_equal(a, b) for a, b in zip(e1[:4], (ch, t, k, cu)))
+    och, ot, ok, ocu, oms = orc.expand_base_events(ch, t, k, cu, 2, 3, 3)
+    # logical channel c*3+r holds exactly the events of base channel c
+    for c in range(6):
+        for r in range(3):
+            lc = c * 3 + r
+            s, e = ocu[lc], ocu[lc + 1]
+            assert np.all(och[s:e] == lc)
+            assert np.array_equal(ot[s:e], t[cu[c]:cu[c + 1]])
+            assert np.array_equal(ok[s:e], k[cu[c]:cu[c + 1]])
+    assert oms == ms
+
+
+def test_gather_roundtrip():
+    x = RNG.standard_normal((2, 3, 40)).astype(np.float32)
+    mem, ch, t, k, cu, ms = _stream(2, 3, 40, 0.3, RNG)
+    u = orc.gather_fwd(x, ch, t)
+    dx = orc.gather_bwd(u, ch, t, 6, 40)
+    assert np.array_equal(dx[mem.reshape(6, 40) > 0.5], x.reshape(6, 40)[mem.reshape(6, 40) > 0.5])
+    assert np.all(dx[mem.reshape(6, 40) <= 0.5] == 0)
+
+
+# ------------------------------------------------------------------- scan
+def test_scan_one_event_closed_form():
+    dt_i, dt_a, A, WB, WC, Dv = _params(1, 4, RNG)
+    u = np.array([0.7], np.float32)
+    k = np.array([5], np.int32)
+    cu = np.array([0, 1], np.int32)
+    out, x = orc.scan_fwd(u, k, cu, 1, dt_i, dt_a, A, WB, WC, Dv)
+    delta = float(dt_i[0]) * 4 + float(dt_a[0])
+    uu = float(u[0])
+    want = float(Dv[0]) * uu + delta * uu ** 3 * float(np.dot(WB[0].astype(np.float64), WC[0]))
+    assert out[0] == pytest.approx(want, rel=1e-12)
+    assert np.allclose(x[0, 0, 1::2], delta * uu * uu * WB[0].astype(np.float64))
+    assert np.allclose(x[0, 0, 0::2], np.exp(delta * A[0].astype(np.float64)))
+
+
+def test_scan_two_events_closed_form():
+    dt_i, dt_a, A, WB, WC, Dv = _params(1, 3, RNG)
+    u = np.array([0.4, -1.3], np.float32)
+    k = np.array([1, 3], np.int32)
+    cu = np.array([0, 2], np.int32)
+    out, x = orc.scan_fwd(u, k, cu, 2, dt_i, dt_a, A, WB, WC, Dv)
+    f = lambda v: np.asarray(v, np.float64)
+    d1, d2 = f(dt_a[0]), f(dt_i[0]) * 2 + f(dt_a[0])
+    h1 = d1 * f(u[0]) ** 2 * f(WB[0])
+    h2 = np.exp(d2 * f(A[0])) * h1 + d2 * f(u[1]) ** 2 * f(WB[0])
+    assert out[1] == pytest.approx(f(Dv[0]) * f(u[1]) + f(u[1]) * np.dot(h2, f(WC[0])), rel=1e-12)
+    assert np.allclose(x[0, 0, 1::2], h2)
+
+
+@pytest.mark.parametrize("clamp_regime", [False, True])
+def test_scan_fwd_matches_dense_formulation(clamp_regime):
+    B, D, L, N = 2, 6, 90, 5
+    mem, ch, t, k, cu, ms = _stream(B, D, L, 0.25, RNG)
+    dt_i, dt_a, A, WB, WC, Dv = _params(D, N, RNG)
+    if clamp_regime:  # long gaps with large |A| exercise the exp2 clamp
+        A = (A * 800.0).astype(np.float32)
+    u = RNG.standard_normal(len(ch)).astype(np.float32)
+    out, x = orc.scan_fwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv)
+    T = lambda a: torch.from_numpy(np.asarray(a))
+    ref = tp.scan_dense(T(u), T(k).long(), T(ch).long(), T(cu).long(), T(dt_i), T(dt_a), T(A), T(WB), T(WC),
+                        T(Dv), dtype=torch.float64)
+    assert_close(out, ref.numpy(), rtol=1e-12, atol_rel=1e-13, name="scan_fwd vs dense")
+
+
+def test_scan_fwd_all_k1_is_dense_mamba_with_constant_delta():
+    # every step an event: the flat scan is the dense recurrence with Δ = dt_active
+    D, L, N = 3, 25, 4
+    dt_i, dt_a, A, WB, WC, Dv = _params(D, N, RNG)
+    u = RNG.standard_normal((1, D, L)).astype(np.float32)
+    ch = np.repeat(np.arange(D), L).astype(np.int32)
+    k = np.ones(D * L, np.int32)
+    cu = (np.arange(D + 1) * L).astype(np.int32)
+    out, x = orc.scan_fwd(u.reshape(-1), k, cu, L, dt_i, dt_a, A, WB, WC, Dv)
+    for d in range(D):
+        h = np.zeros(N)
+        for s in range(L):
+            ud = float(u[0, d, s])
+            wb, wc = WB[d].astype(np.float64), WC[d].astype(np.float64)
+            h = np.exp(float(dt_a[d]) * A[d].astype(np.float64)) * h + float(dt_a[d]) * ud * ud * wb
+            assert out[d * L + s] == pytest.approx(float(Dv[d]) * ud + ud * float(h @ wc), rel=1e-10)
+
+
+def test_scan_chunk_state_semantics():
+    # a channel of 2500 events: x[:,0] is the state after event 2047, x[:,1] after the last
+    N = 3
+    dt_i, dt_a, A, WB, WC, Dv = _params(1, N, RNG)
+    n = 2500
+    u = RNG.standard_normal(n).astype(np.float32) * 0.3
+    k = RNG.integers(1, 4, n).astype(np.int32)
+    cu = np.array([0, n], np.int32)
+    _, x = orc.scan_fwd(u, k, cu, n, dt_i, dt_a, A * 0.01, WB, WC, Dv)
+    _, x_head = orc.scan_fwd(u[:2048], k[:2048], np.array([0, 2048], np.int32), 2048, dt_i, dt_a, A * 0.01, WB,
+                             WC, Dv)
+    assert x.shape == (1, 2, 2 * N)
+    assert np.allclose(x[0, 0], x_head[0, 0], rtol=1e-12)
+    _, x_all = orc.scan_fwd(u, k, cu, 4096 + 1, dt_i, dt_a, A * 0.01, WB, WC, Dv)
+    assert x_all.shape == (1, 3, 2 * N) and np.all(x_all[0, 2] == 0)
+
+
+def _bwd_case(B, D, L, N, p, with_z, rng):
+    mem, ch, t, k, cu, ms = _stream(B, D, L, p, rng)
+    dt_i, dt_a, A, WB, WC, Dv = _params(D, N, rng)
+    E = len(ch)
+    u = rng.standard_normal(E).astype(np.float32)
+    dout = rng.standard_normal(E).astype(np.float32)
+    z = rng.standard_normal(E).astype(np.float32) if with_z else None
+    return ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, z
+
+
+@pytest.mark.parametrize("with_z", [False, True])
+def test_scan_bwd_matches_float64_autograd(with_z):
+    ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, z = _bwd_case(2, 4, 60, 5, 0.3, with_z, RNG)
+    out, x, *rest = orc.scan_fwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, z)
+    got = orc.scan_bwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, dout, Dv, z, out if with_z else None)
+    T = lambda a: torch.tensor(np.asarray(a), dtype=torch.float64)
+    leaves = [T(v).requires_grad_(True) for v in (u, dt_i, dt_a, A, WB, WC, Dv)]
+    uu, dti, dta, A_, WB_, WC_, D_ = leaves
+    y = tp.scan_dense(uu, torch.from_numpy(k).long(), torch.from_numpy(ch).long(), torch.from_numpy(cu).long(),
+                      dti, dta, A_, WB_, WC_, D_, dtype=torch.float64)
+    if with_z:
+        zt = T(z).requires_grad_(True)
+        y = y * torch.nn.functional.silu(zt)
+        leaves.append(zt)
+    y.backward(T(dout))
+    du, dA, dWB, dWC, ddti, ddta, dD, dz = got
+    for name, mine, ref in [("du", du, uu.grad), ("dA", dA, A_.grad), ("dW_B", dWB, WB_.grad),
+                            ("dW_C", dWC, WC_.grad), ("ddt_idle", ddti, dti.grad), ("ddt_active", ddta, dta.grad),
+                            ("dD", dD, D_.grad)] + ([("dz", dz, leaves[-1].grad)] if with_z else []):
+        assert_close(mine, ref.numpy(), rtol=1e-10, atol_rel=1e-12, name=name)
+
+
+def test_scan_bwd_finite_difference():
+    ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, _ = _bwd_case(1, 2, 30, 3, 0.4, False, RNG)
+    du, dA, *_ = orc.scan_bwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, dout, Dv)
+    f8 = lambda v: np.asarray(v, np.float64)
+    loss = lambda uu, AA: float(np.dot(orc.scan_fwd(uu, k, cu, ms, dt_i, dt_a, AA, WB, WC, Dv)[0], f8(dout)))
+    eps = 1e-6
+    for i in (0, len(u) // 2, len(u) - 1):
+        up, um = f8(u).copy(), f8(u).copy()
+        up[i] += eps
+        um[i] -= eps
+        assert (loss(up, f8(A)) - loss(um, f8(A))) / (2 * eps) == pytest.approx(du[i], rel=1e-6, abs=1e-9)
+    Ap, Am = f8(A).copy(), f8(A).copy()
+    Ap[1, 2] += eps
+    Am[1, 2] -= eps
+    assert (loss(f8(u), Ap) - loss(f8(u), Am)) / (2 * eps) == pytest.approx(dA[1, 2], rel=1e-6, abs=1e-9)
+
+
+def test_scan_bwd_one_event_closed_form():
+    dt_i, dt_a, A, WB, WC, Dv = _params(1, 4, RNG)
+    u = np.array([0.9], np.float32)
+    k = np.array([3], np.int32)
+    cu = np.array([0, 1], np.int32)
+    g = np.array([1.0], np.float32)
+    du, dA, dWB, dWC, ddti, ddta, dD, _ = orc.scan_bwd(u, k, cu, 1, dt_i, dt_a, A, WB, WC, g, Dv)
+    f = lambda v: np.asarray(v, np.float64)
+    delta = f(dt_i[0]) * 2 + f(dt_a[0])
+    s = float(np.dot(f(WB[0]), f(WC[0])))
+    uu = float(u[0])
+    assert du[0] == pytest.approx(f(Dv[0]) + 3 * delta * uu ** 2 * s, rel=1e-12)   # ∂y/∂u
+    assert ddta[0] == pytest.approx(uu ** 3 * s, rel=1e-12)                          # ∂y/∂Δ · ∂Δ/∂dt_active
+    assert ddti[0] == pytest.approx(2 * uu ** 3 * s, rel=1e-12)                      # (k-1) = 2
+    assert np.allclose(dWB[0], delta * uu ** 3 * f(WC[0])) and np.allclose(dWC[0], delta * uu ** 3 * f(WB[0]))
+    assert np.allclose(dA[0], 0.0) and dD[0] == pytest.approx(uu)
+
+
+# ---------------------------------------------------------------- restore
+def test_restore_fwd_brute_force():
+    B, D, L = 2, 3, 45
+    mem, ch, t, k, cu, ms = _stream(B, D, L, 0.2, RNG)
+    y = RNG.standard_normal(len(ch))
+    out = orc.restore_fwd(y, t, cu, D, L)
+    for c in range(B * D):
+        for s in range(L):
+            idx = [e for e in range(cu[c], cu[c + 1]) if t[e] <= s]
+            assert out[c // D, s, c % D] == (y[idx[-1]] if idx else 0.0)
+
+
+def test_restore_bwd_is_adjoint_and_brute_force():
+    B, D, L = 2, 4, 70
+    mem, ch, t, k, cu, ms = _stream(B, D, L, 0.15, RNG)
+    y = RNG.standard_normal(len(ch))
+    g = RNG.standard_normal((B, L, D))
+    dy = orc.restore_bwd(g, t, cu, D, L)
+    assert np.dot(orc.restore_fwd(y, t, cu, D, L).ravel(), g.ravel()) == pytest.approx(np.dot(y, dy), rel=1e-12)
+    for e in range(len(ch)):
+        c = ch[e]
+        nxt = t[e + 1] if e + 1 < cu[c + 1] else L
+        assert dy[e] == pytest.approx(g[c // D, t[e]:nxt, c % D].sum(), rel=1e-12)
+
+
+def test_restore_matches_torch_searchsorted_formulation():
+    B, D, L = 2, 3, 64
+    mem, ch, t, k, cu, ms = _stream(B, D, L, 0.3, RNG)
+    y = RNG.standard_normal(len(ch))
+    ref = tp.restore(torch.from_numpy(y), torch.from_numpy(t).long(), torch.from_numpy(ch).long(),
+                     torch.from_numpy(cu).long(), D, L)
+    assert np.array_equal(orc.restore_fwd(y, t, cu, D, L), ref.numpy())
+
+
+def test_torch_path_extract_matches_oracle():
+    mem = (RNG.random((2, 4, 100)) < 0.2).astype(np.float32)
+    ch, t, k, cu, counts, ms = orc.extract_base_events(mem, 0.5)
+    tch, tt, tk, tcu, _ = tp.extract(torch.from_numpy(mem), 0.5)
+    for a, b in ((ch, tch), (t, tt), (k, tk), (cu, tcu)):
+        assert np.array_equal(a, b.numpy())
