@@ -86,6 +86,8 @@ def restore_dense_fwd(y_flat, time_steps, cu_seqlens, dim, seqlen, out_dtype=Non
         _check(out_dtype == torch.float16, f"{fn}: fp16 input only supports fp16 output")
     if y_flat.dtype == torch.bfloat16:
         _check(out_dtype == torch.bfloat16, f"{fn}: bf16 input only supports bf16 output")
+    if y_flat.numel() == 0:  # no events: every position precedes its channel's first event
+        return torch.zeros((n_ch // dim, seqlen, dim), dtype=out_dtype, device=y_flat.device)
     with torch.cuda.device(y_flat.device):
         bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen)
         return restore_fwd_indexed(y_flat, (bitmask, tile_start, 1), n_ch, dim, seqlen, out_dtype)
@@ -110,6 +112,8 @@ def restore_dense_bwd(dout, time_steps, cu_seqlens, dim, seqlen):
     _check(dout.size(2) == dim, f"{fn}: dout.size(2) must equal dim (D)")
     _check(dout.size(0) * dim == n_ch, f"{fn}: dout.size(0)*dim must equal n_channels")
     dy = torch.empty(int(time_steps.size(0)), dtype=torch.float32, device=dout.device)
+    if dy.numel() == 0:
+        return dy
     with torch.cuda.device(dout.device):
         bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen, zero_f32=dy)
         if n_ch > 0:
