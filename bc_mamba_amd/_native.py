@@ -53,8 +53,9 @@ SIGNATURES = {
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_build_event_index": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_i64, c_p]),
-    "bcm_restore_fwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p]),
-    "bcm_restore_bwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_p]),
+    "bcm_restore_fwd": (c_i32, [c_p, c_i32, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p]),
+    "bcm_restore_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),
+    "bcm_restore_bwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p]),
 }
 
 _lib = None

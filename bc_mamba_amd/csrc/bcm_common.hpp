@@ -109,6 +109,42 @@ __device__ __forceinline__ uint64_t tile_mask(const uint32_t* row, int64_t j) {
   return (uint64_t)w.x | ((uint64_t)w.y << 32);
 }
 
+// ------------------------------------------------------ buffer resources
+// A raw buffer resource over [base, base + bytes). Lanes whose byte offset
+// is out of range read 0 and their stores are dropped by the hardware, which
+// gives branch-free predication (no exec-mask branches, no waits).
+constexpr uint32_t kBufOOB = 0x80000000u;
+constexpr int kBufFlags = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = bytes > 0x7fffffffll ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, kBufFlags);
+}
+
+template <typename T> __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ float buf_load<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+template <> __device__ __forceinline__ float buf_load<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0) << 16);
+}
+template <> __device__ __forceinline__ float buf_load<f16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const unsigned short b = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return __half2float(*reinterpret_cast<const f16*>(&b));
+}
+
+__device__ __forceinline__ void buf_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
+
+// DPP lane permutations inside rows of 16 lanes (VALU, no LDS round trip).
+template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i inside each 8 lanes
+
 // exp2 of a clamped exponent: the decay of the reference scan
 // (selective_scan_common.h:45-52 clamps Δ·A·log2e to [-126, 126]).
 __device__ __forceinline__ float decay(float e) {

@@ -19,6 +19,9 @@
 namespace bcm {
 
 // ------------------------------------------------------------------ count
+// One wave per row. A batch of up to 8 groups (8 x 16 bytes per lane) is
+// loaded before any of it is used, so a row of 2048 fp32 steps is one round
+// trip to memory.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t n_rows, int64_t L, float thr,
                                                uint32_t* __restrict__ bitmask, int64_t W,
@@ -27,6 +30,7 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   constexpr int GS = kWave * PER;      // steps per group
   constexpr int LPW = 32 / PER;        // lanes per 32-bit word
   constexpr int WPG = GS / 32;         // words per group
+  constexpr int BATCH = 8;
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   if (row >= n_rows) return;
@@ -34,25 +38,48 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   uint32_t* br = bitmask + row * W;
   int cnt = 0;
   const int64_t ng = (L + GS - 1) / GS;
-#pragma unroll 4
-  for (int64_t g = 0; g < ng; ++g) {
-    const int64_t t0 = g * GS + (int64_t)lane * PER;
-    uint32_t bits = 0;
-    if (VEC && t0 + PER <= L) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(xr + t0);
-      const T* v = reinterpret_cast<const T*>(&raw);
+  for (int64_t g0 = 0; g0 < ng; g0 += BATCH) {
+    uint32_t bits[BATCH];
+    if (VEC && (g0 + BATCH) * GS <= L) {
+      uint4 raw[BATCH];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) bits |= (uint32_t)(to_f(v[i]) > thr) << i;
-    } else {
+      for (int i = 0; i < BATCH; ++i) raw[i] = *reinterpret_cast<const uint4*>(xr + (g0 + i) * GS + lane * PER);
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        if (t0 + i < L) bits |= (uint32_t)(to_f(xr[t0 + i]) > thr) << i;
+      for (int i = 0; i < BATCH; ++i) {
+        const T* v = reinterpret_cast<const T*>(&raw[i]);
+        bits[i] = 0;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
+      }
+    } else {  // tail batch: full groups still use 16-byte loads
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) {
+        const int64_t t0 = (g0 + i) * GS + (int64_t)lane * PER;
+        bits[i] = 0;
+        if (VEC && t0 + PER <= L) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(xr + t0);
+          const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+          for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
+        } else {
+#pragma unroll
+          for (int e = 0; e < PER; ++e)
+            if (t0 + e < L) bits[i] |= (uint32_t)(to_f(xr[t0 + e]) > thr) << e;
+        }
+      }
     }
-    cnt += __popc(bits);
-    uint32_t w = bits << (PER * (lane % LPW));
 #pragma unroll
-    for (int m = 1; m < LPW; m <<= 1) w |= __shfl_xor(w, m, kWave);
-    if (lane % LPW == 0) br[g * WPG + lane / LPW] = w;
+    for (int i = 0; i < BATCH; ++i) {
+      if (g0 + i < ng) {
+        cnt += __popc(bits[i]);
+        // pack the lanes' PER-bit pieces of one 32-step word (DPP, no LDS)
+        uint32_t w = bits[i] << (PER * (lane % LPW));
+        if constexpr (LPW >= 2) w |= dpp<kDppXor1>(w);
+        if constexpr (LPW >= 4) w |= dpp<kDppXor2>(w);
+        if constexpr (LPW >= 8) w |= dpp<kDppHalfMirror>(w);
+        if (lane % LPW == 0) br[(g0 + i) * WPG + lane / LPW] = w;
+      }
+    }
   }
   cnt = wave_sum(cnt);
   if (lane == 0) counts[row] = cnt;
@@ -156,17 +183,38 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
       st[pos++] = (int)(32 * w + b);
     }
     wave_sync();
+    // write-out in batches of 4 events per lane: the gathers of a batch are
+    // in flight together and the index stores never wait on them
     for (int r = 0; r < expand; ++r) {
       const int64_t lc = c * expand + r;
       const int64_t obase = (int64_t)cu0 * expand + (int64_t)r * n + off;
-      for (int i = lane; i < seg_cnt; i += kWave) {
-        const int t = st[i];
-        const int tp = i > 0 ? st[i - 1] : prev_t;
-        ch_ids[obase + i] = (int32_t)lc;
-        t_steps[obase + i] = t;
-        k_flat[obase + i] = tp < 0 ? t + 1 : t - tp;
-        if (head_flags) head_flags[obase + i] = tp < 0 ? 1 : 0;
-        if (GATHER) x_ev[obase + i] = x[lc * L + t];
+      for (int i0 = 0; i0 < seg_cnt; i0 += 4 * kWave) {
+        int tv[4];
+        T xv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = i0 + q * kWave + lane;
+          tv[q] = i < seg_cnt ? st[i] : 0;
+          if (GATHER) xv[q] = x[lc * L + tv[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = i0 + q * kWave + lane;
+          if (i < seg_cnt) {
+            const int tp = i > 0 ? st[i - 1] : prev_t;
+            ch_ids[obase + i] = (int32_t)lc;
+            t_steps[obase + i] = tv[q];
+            k_flat[obase + i] = tp < 0 ? tv[q] + 1 : tv[q] - tp;
+            if (head_flags) head_flags[obase + i] = tp < 0 ? 1 : 0;
+          }
+        }
+        if (GATHER) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int i = i0 + q * kWave + lane;
+            if (i < seg_cnt) x_ev[obase + i] = xv[q];
+          }
+        }
       }
     }
     wave_sync();

@@ -10,9 +10,11 @@
 // 64-channel row of the (B, L, D) tensor. The tile's event positions come
 // from the 64-bit tile mask of the event bitmask and the first event index
 // from the tile table, so all value loads are independent (no search, no
-// serial pointer chasing) and there are no per-position atomics: the
-// backward writes runs that end inside the tile with plain stores and only
-// the two tile-crossing partial runs per lane with fp32 atomics.
+// serial pointer chasing). Each kernel runs in branch-free phases (all loads,
+// register work, back-to-back stores) so no store waits on another. The
+// backward uses no atomics: runs inside a tile are written by the tile pass,
+// runs that cross a tile edge by a small fix-up pass, each event exactly once
+// (deterministic, no zero-fill of dy).
 #include "bcm_common.hpp"
 
 namespace bcm {
@@ -54,92 +56,135 @@ __global__ __launch_bounds__(64) void k_build_index(const int32_t* __restrict__ 
 }
 
 struct TileWave {
-  int64_t b, j, ch, dd;
-  bool ok;
+  int b, j, g, dd, ch;
+  bool ok;        // lane maps to a channel (dd < dim)
+  int e_base;     // first event index of the wave's 64 channels
 };
 
 // wave id -> (b, tile j, channel group g); g varies fastest so neighbouring
-// waves write neighbouring 256-byte pieces of the same (b, t) rows.
-__device__ __forceinline__ TileWave tile_wave(int64_t n_rows, int64_t dim, int64_t nT, int64_t nG) {
+// waves write neighbouring 256-byte pieces of the same (b, t) rows. Lanes
+// past `dim` are clamped to the group's last channel (addresses stay valid)
+// and flagged !ok.
+__device__ __forceinline__ TileWave tile_wave(int nT, int nG, int dim, const int32_t* tile_start) {
   TileWave w;
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  const int64_t Bn = n_rows / dim;
-  w.ok = wid < Bn * nT * nG;
-  const int64_t g = wid % nG, bj = wid / nG;
+  const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  w.g = wid % nG;
+  const int bj = wid / nG;
   w.j = bj % nT;
   w.b = bj / nT;
-  w.dd = g * kWave + lane_id();
-  w.ok = w.ok && w.dd < dim;
+  const int d = w.g * kWave + lane_id();
+  w.ok = d < dim;
+  w.dd = w.ok ? d : dim - 1;
   w.ch = w.b * dim + w.dd;
+  w.e_base = tile_start[(int64_t)(w.b * dim + w.g * kWave) * (nT + 1)];
   return w;
 }
 
 template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, const uint32_t* __restrict__ bitmask,
-                                                     int64_t W, int64_t mrd, const int32_t* __restrict__ tile_start,
-                                                     int64_t nT, int64_t n_rows, int64_t dim, int64_t L, int64_t nG,
-                                                     TO* __restrict__ out) {
-  const TileWave w = tile_wave(n_rows, dim, nT, nG);
-  if (!w.ok) return;
-  const int32_t* ts = tile_start + w.ch * (nT + 1);
+__global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, int64_t n_events,
+                                                     const uint32_t* __restrict__ bitmask, int64_t W, int64_t mrd,
+                                                     const int32_t* __restrict__ tile_start, int nT, int nG,
+                                                     int waves, int dim, int64_t L, TO* __restrict__ out) {
+  if ((int)(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) >= waves) return;
+  const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
   const int32_t cu0 = ts[0], elo = ts[w.j];
-  const uint64_t m = tile_mask(bitmask + (w.ch / mrd) * W, w.j);
-  float val = elo > cu0 ? to_f(y[elo - 1]) : 0.0f;
-  const int64_t t0 = w.j * kTile;
-  const int steps = (int)((L - t0) < kTile ? (L - t0) : kTile);
+  const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
+  const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y + e_base, (n_events - e_base) * (int64_t)sizeof(TI));
+  // event values of the tile: one load per step, out-of-range offsets for
+  // steps without an event (no branches, all loads independent)
   float v[kTile];
-  int idx = elo - 1;
+  uint32_t idx = (uint32_t)(elo - e_base);
 #pragma unroll
   for (int s = 0; s < kTile; ++s) {
-    if ((m >> s) & 1ull) {
-      ++idx;
-      v[s] = to_f(y[idx]);
-    }
+    const uint32_t bit = (uint32_t)(m >> s) & 1u;
+    v[s] = buf_load<TI>(ry, bit ? idx * (uint32_t)sizeof(TI) : kBufOOB);
+    idx += bit;
   }
-  TO* o = out + (w.b * L + t0) * dim + w.dd;
+  float val = buf_load<TI>(ry, elo > cu0 ? (uint32_t)(elo - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
+  const int64_t t0 = (int64_t)w.j * kTile;
+  TO* op = out + ((int64_t)w.b * L + t0) * dim + w.dd;
+  if (!w.ok) return;
+  if (t0 + kTile <= L) {
 #pragma unroll
-  for (int s = 0; s < kTile; ++s) {
-    if (s < steps) {
-      if ((m >> s) & 1ull) val = v[s];
-      o[(int64_t)s * dim] = from_f<TO>(val);
+    for (int s = 0; s < kTile; ++s) {
+      val = ((m >> s) & 1ull) ? v[s] : val;
+      op[(int64_t)s * dim] = from_f<TO>(val);
+    }
+  } else {
+    const int steps = (int)(L - t0);
+    for (int s = 0; s < steps; ++s) {
+      val = ((m >> s) & 1ull) ? v[s] : val;
+      op[(int64_t)s * dim] = from_f<TO>(val);
     }
   }
 }
 
+// Restore backward, tile pass. Runs that start and end inside the tile are
+// final and stored as they close (buffer stores, out-of-range when there is
+// nothing to store). The partial runs at the tile edges (head: before the
+// first event; tail: from the last event to the tile end) go to per-tile
+// side arrays [nT][n_rows] for the fix-up pass.
 template <typename TI>
-__global__ __launch_bounds__(256) void k_restore_bwd(const TI* __restrict__ dout, const uint32_t* __restrict__ bitmask,
-                                                     int64_t W, int64_t mrd, const int32_t* __restrict__ tile_start,
-                                                     int64_t nT, int64_t n_rows, int64_t dim, int64_t L, int64_t nG,
-                                                     float* __restrict__ dy) {
-  const TileWave w = tile_wave(n_rows, dim, nT, nG);
-  if (!w.ok) return;
-  const int32_t* ts = tile_start + w.ch * (nT + 1);
-  const int32_t cu0 = ts[0], elo = ts[w.j];
-  const uint64_t m = tile_mask(bitmask + (w.ch / mrd) * W, w.j);
-  const int64_t t0 = w.j * kTile;
-  const int steps = (int)((L - t0) < kTile ? (L - t0) : kTile);
-  const TI* g = dout + (w.b * L + t0) * dim + w.dd;
+__global__ __launch_bounds__(256) void k_restore_bwd_tiles(const TI* __restrict__ dout, int64_t n_events,
+                                                           const uint32_t* __restrict__ bitmask, int64_t W,
+                                                           int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                           int nT, int nG, int waves, int dim, int64_t L,
+                                                           int64_t n_rows, float* __restrict__ dy,
+                                                           float* __restrict__ head, float* __restrict__ tail) {
+  if ((int)(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) >= waves) return;
+  const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  const int64_t t0 = (int64_t)w.j * kTile;
+  const TI* g = dout + ((int64_t)w.b * L + t0) * dim + w.dd;
   float gv[kTile];
+  if (t0 + kTile <= L) {
 #pragma unroll
-  for (int s = 0; s < kTile; ++s) gv[s] = s < steps ? to_f(g[(int64_t)s * dim]) : 0.0f;
-  float sum = 0.0f;
-  int idx = elo - 1;
-  bool head = true;  // the open run started before this tile
+    for (int s = 0; s < kTile; ++s) gv[s] = to_f(g[(int64_t)s * dim]);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kTile; ++s) gv[s] = (t0 + s < L) ? to_f(g[(int64_t)s * dim]) : 0.0f;
+  }
+  const int32_t elo = tile_start[(int64_t)w.ch * (nT + 1) + w.j];
+  const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
+  const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
+  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
+  float sum = 0.0f, hsum = 0.0f;
+  uint32_t r = 0;                                // events seen so far in the tile
+  const uint32_t ebase = (uint32_t)(elo - e_base);
 #pragma unroll
   for (int s = 0; s < kTile; ++s) {
-    if ((m >> s) & 1ull) {
-      if (head) {
-        if (idx >= cu0) unsafeAtomicAdd(dy + idx, sum);
-        head = false;
-      } else {
-        dy[idx] = sum;  // run started and ended inside this tile
-      }
-      ++idx;
-      sum = 0.0f;
-    }
-    sum += gv[s];
+    const uint32_t bit = (uint32_t)(m >> s) & 1u;
+    // the run of event (elo + r - 1) closes here when r >= 1
+    buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
+    hsum = (bit && r == 0) ? sum : hsum;
+    r += bit;
+    sum = (bit ? 0.0f : sum) + gv[s];
   }
-  if (idx >= cu0) unsafeAtomicAdd(dy + idx, sum);
+  if (w.ok) {
+    head[(int64_t)w.j * n_rows + w.ch] = r ? hsum : sum;
+    tail[(int64_t)w.j * n_rows + w.ch] = sum;
+  }
+}
+
+// Restore backward, fix-up pass: the run of the last event of tile j is its
+// tail partial plus the head partials of the following tiles up to and
+// including the next tile that holds an event. One lane per (tile, channel).
+__global__ __launch_bounds__(256) void k_restore_bwd_fix(const int32_t* __restrict__ tile_start, int64_t nT,
+                                                         int64_t n_rows, const float* __restrict__ head,
+                                                         const float* __restrict__ tail, float* __restrict__ dy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nT * n_rows) return;
+  const int64_t j = i / n_rows, ch = i - j * n_rows;
+  const int32_t* ts = tile_start + ch * (nT + 1);
+  const int32_t e_end = ts[j + 1];
+  if (e_end == ts[j]) return;  // no event in tile j: its head belongs to an earlier tile's owner
+  float acc = tail[i];
+  for (int64_t jj = j + 1; jj < nT; ++jj) {
+    acc += head[jj * n_rows + ch];
+    if (ts[jj + 1] != ts[jj]) break;
+  }
+  dy[e_end - 1] = acc;
 }
 
 static unsigned nblk(int64_t waves) { return (unsigned)((waves + 3) / 4); }
@@ -178,7 +223,7 @@ int bcm_build_event_index(const int32_t* t_steps, const int32_t* cu_seqlens, int
   return check_launch(fn);
 }
 
-int bcm_restore_fwd(const void* y, int y_dtype, const uint32_t* bitmask, int64_t mask_row_div,
+int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events, const uint32_t* bitmask, int64_t mask_row_div,
                     const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, void* out, int out_dtype,
                     bcm_stream_t stream) {
   const char* fn = "bcm_restore_fwd";
@@ -191,14 +236,16 @@ int bcm_restore_fwd(const void* y, int y_dtype, const uint32_t* bitmask, int64_t
   if (rc) return rc;
   if (n_rows == 0) return BCM_OK;
   if (!out) return set_error(BCM_EINVAL, "%s: null output", fn);
+  if (n_events < 0 || (n_events > 0 && !y)) return set_error(BCM_EINVAL, "%s: invalid y", fn);
   const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
   const int64_t waves = (n_rows / dim) * nT * nG;
+  if (waves > INT32_MAX / 2) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   auto go = [&](auto ti, auto to) {
     using TI = decltype(ti);
     using TO = decltype(to);
     hipLaunchKernelGGL((k_restore_fwd<TI, TO>), dim3(nblk(waves)), dim3(256), 0, hs(stream),
-                       static_cast<const TI*>(y), bitmask, W, mask_row_div, tile_start, nT, n_rows, dim, L, nG,
-                       static_cast<TO*>(out));
+                       static_cast<const TI*>(y), n_events, bitmask, W, mask_row_div, tile_start, (int)nT, (int)nG,
+                       (int)waves, (int)dim, L, static_cast<TO*>(out));
   };
   if (y_dtype == BCM_F32) dispatch_dtype(out_dtype, [&](auto to) { go(float{}, to); });
   else if (y_dtype == BCM_F16) go(f16{}, f16{});
@@ -206,22 +253,37 @@ int bcm_restore_fwd(const void* y, int y_dtype, const uint32_t* bitmask, int64_t
   return check_launch(fn);
 }
 
+int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L) {
+  return (n_rows < 0 || L < 1) ? 0 : 2 * 4 * n_rows * tile_count(L);
+}
+
 int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
-                    const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy,
-                    bcm_stream_t stream) {
+                    const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy, int64_t n_events,
+                    void* workspace, int64_t workspace_bytes, bcm_stream_t stream) {
   const char* fn = "bcm_restore_bwd";
   if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: dout must be fp32/fp16/bf16", fn);
   int rc = check_restore(fn, bitmask, mask_row_div, tile_start, n_rows, dim, L);
   if (rc) return rc;
   if (n_rows == 0) return BCM_OK;
-  if (!dout || !dy) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!dout || (n_events > 0 && !dy) || n_events < 0) return set_error(BCM_EINVAL, "%s: null pointer", fn);
   const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
+  if (!workspace || workspace_bytes < bcm_restore_bwd_workspace_bytes(n_rows, L))
+    return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn,
+                     (long long)bcm_restore_bwd_workspace_bytes(n_rows, L));
+  float* head = static_cast<float*>(workspace);
+  float* tail = head + nT * n_rows;
   const int64_t waves = (n_rows / dim) * nT * nG;
+  if (waves > INT32_MAX / 2) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    hipLaunchKernelGGL(k_restore_bwd<T>, dim3(nblk(waves)), dim3(256), 0, hs(stream), static_cast<const T*>(dout),
-                       bitmask, W, mask_row_div, tile_start, nT, n_rows, dim, L, nG, dy);
+    hipLaunchKernelGGL(k_restore_bwd_tiles<T>, dim3(nblk(waves)), dim3(256), 0, hs(stream),
+                       static_cast<const T*>(dout), n_events, bitmask, W, mask_row_div, tile_start, (int)nT,
+                       (int)nG, (int)waves, (int)dim, L, n_rows, dy, head, tail);
   });
+  rc = check_launch(fn);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, hs(stream),
+                     tile_start, nT, n_rows, head, tail, dy);
   return check_launch(fn);
 }
 

@@ -129,7 +129,6 @@ class _IndexedRestoreFn(torch.autograd.Function):
         dout = dout.contiguous()
         dy = torch.empty(ctx.n_events, dtype=torch.float32, device=dout.device)
         with cuda_stage("restore_backward"):
-            _nat.call("bcm_zero", _nat.ptr(dy), 4 * ctx.n_events, _nat.stream_of(dout))
             restore_dense_cuda_nodecay.restore_bwd_indexed(dout, ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen, dy)
         return dy, None, None, None, None
 

@@ -48,17 +48,22 @@ def restore_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen, out_dtype=None):
     bitmask, tile_start, mrd = event_index
     out_dtype = y_flat.dtype if out_dtype is None else out_dtype
     out = torch.empty((n_ch // dim, seqlen, dim), dtype=out_dtype, device=y_flat.device)
-    _nat.call("bcm_restore_fwd", _nat.ptr(y_flat), _nat.dtype_code(y_flat.dtype), _nat.ptr(bitmask), int(mrd),
+    _nat.call("bcm_restore_fwd", _nat.ptr(y_flat), _nat.dtype_code(y_flat.dtype), int(y_flat.numel()),
+              _nat.ptr(bitmask), int(mrd),
               _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(out), _nat.dtype_code(out_dtype),
               _nat.stream_of(y_flat))
     return out
 
 
 def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy):
-    """Restore backward from an event index into a zeroed float32 dy."""
+    """Restore backward from an event index into the float32 dy (every
+    event's entry is written; no zero-init needed)."""
     bitmask, tile_start, mrd = event_index
+    ws = torch.empty(2 * n_ch * _nat.tile_count(seqlen), dtype=torch.float32, device=dout.device)
     _nat.call("bcm_restore_bwd", _nat.ptr(dout), _nat.dtype_code(dout.dtype), _nat.ptr(bitmask), int(mrd),
-              _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), _nat.stream_of(dout))
+              _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), int(dy.numel()), _nat.ptr(ws),
+              4 * ws.numel(),
+              _nat.stream_of(dout))
     return dy
 
 

@@ -46,8 +46,7 @@ def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
 class Path:
     """The fwd+bwd path driven through the C ABI with reusable buffers."""
 
-    KERNELS = ["count", "offsets", "fill", "scan_fwd", "restore_fwd", "zero_dy", "restore_bwd", "scan_bwd",
-               "gather_bwd"]
+    KERNELS = ["count", "offsets", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd", "gather_bwd"]
 
     def __init__(self, w, dev):
         import torch
@@ -64,6 +63,7 @@ class Path:
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
+        self.ws = torch.empty(2 * self.NC * nat.tile_count(L), dtype=torch.float32, device=dev)
         self.E = -1
         self.events = {}
 
@@ -126,12 +126,12 @@ class Path:
                                       nat.dtype_code(w.dtype), P(self.ch), P(self.ts), P(self.k), P(self.u),
                                       P(self.tile_start), None, s))
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
-        mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), P(self.bitmask), 1,
+        mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense),
                                              nat.dtype_code(w.dtype), s))
-        mark("zero_dy", lambda: nat.call("bcm_zero", P(self.dy32), 4 * E, s))
         mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), nat.dtype_code(w.dtype), P(self.bitmask),
-                                             1, P(self.tile_start), self.NC, D, L, P(self.dy32), s))
+                                             1, P(self.tile_start), self.NC, D, L, P(self.dy32), E, P(self.ws),
+                                             4 * self.ws.numel(), s))
         if self.dy is not self.dy32:
             self.dy.copy_(self.dy32)
         mark("scan_bwd", lambda: nat.call("bcm_scan_bwd", self.args, s))
@@ -222,7 +222,7 @@ def main():
     # algorithmic bytes of one launch of each kernel (its share of the API-contract traffic)
     kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC, "offsets": 8 * path.NC,
                     "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
-                    "restore_fwd": alg["fwd_restore"], "zero_dy": 4 * E, "restore_bwd": alg["bwd_restore"],
+                    "restore_fwd": alg["fwd_restore"], "restore_bwd": alg["bwd_restore"],
                     "scan_bwd": alg["bwd_scan"], "gather_bwd": alg["bwd_gather"]}
     dom_gbs = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
     result = {

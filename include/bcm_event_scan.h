@@ -186,19 +186,27 @@ int bcm_build_event_index(const int32_t* t_steps, const int32_t* cu_seqlens,
 /* restore_dense_fwd (csrc/r_nodecay/restore_dense.cpp:43-130,
  * restore_dense_fwd_kernel.cuh:38-114): out[b, t, d] = y[e] for the last
  * event e of channel b*dim+d with t_e <= t, 0 before the first event.
- * out (n_rows/dim, L, dim) of out_dtype, fully written. */
-int bcm_restore_fwd(const void* y, int y_dtype, const uint32_t* bitmask,
+ * y holds n_events values; out (n_rows/dim, L, dim) of out_dtype is fully
+ * written. */
+int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events,
+                    const uint32_t* bitmask,
                     int64_t mask_row_div, const int32_t* tile_start,
                     int64_t n_rows, int64_t dim, int64_t L, void* out,
                     int out_dtype, bcm_stream_t stream);
 
+/* Workspace of bcm_restore_bwd: 2 * 4 * n_rows * tile_count(L) bytes. */
+int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L);
+
 /* restore_dense_bwd (restore_dense.cpp:138-202,
- * restore_dense_bwd_kernel.cuh:42-112): dy[e] += sum of dout[b, t, d] over
- * t in [t_e, t_next). dy [E] float32 must be zero on entry. */
+ * restore_dense_bwd_kernel.cuh:42-112): dy[e] = sum of dout[b, t, d] over
+ * t in [t_e, t_next) (t_next = next event or L), float32. Every event with
+ * 0 <= t_e < L is written exactly once (no zero-init, no atomics,
+ * deterministic); `workspace` holds per-tile partial sums. */
 int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask,
                     int64_t mask_row_div, const int32_t* tile_start,
                     int64_t n_rows, int64_t dim, int64_t L, float* dy,
-                    bcm_stream_t stream);
+                    int64_t n_events, void* workspace,
+                    int64_t workspace_bytes, bcm_stream_t stream);
 
 #ifdef __cplusplus
 }

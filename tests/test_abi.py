@@ -69,7 +69,7 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert lib.bcm_scan_bwd(a, None) == 1 and "dstate" in lib.bcm_last_error().decode()
     a.dstate, a.n_chunks = 16, 2
     assert lib.bcm_scan_fwd(a, None) == 1 and "n_chunks" in lib.bcm_last_error().decode()
-    assert lib.bcm_restore_fwd(None, 0, None, 1, None, 10, 3, 8, None, 0, None) == 1
+    assert lib.bcm_restore_fwd(None, 0, 0, None, 1, None, 10, 3, 8, None, 0, None) == 1
     assert "divisible" in lib.bcm_last_error().decode()
-    assert lib.bcm_restore_fwd(None, 1, None, 1, None, 8, 4, 8, None, 0, None) == 1
+    assert lib.bcm_restore_fwd(None, 1, 0, None, 1, None, 8, 4, 8, None, 0, None) == 1
     assert "fp16 input only supports fp16 output" in lib.bcm_last_error().decode()
