@@ -55,6 +55,18 @@ template <typename F> inline void dispatch_dtype(int dt, F&& fn) {
 // ---------------------------------------------------------------- wave ops
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// MI355X has 8 XCDs, each with its own L2; workgroup i of a launch runs on
+// XCD i % 8. xcd_block() maps the hardware block id to a logical one so that
+// every XCD works through a contiguous range of logical blocks: data that
+// neighbouring logical blocks share is then fetched into one L2, not eight.
+// A bijection on [0, nblk) for any nblk.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_block(int bid, int nblk) {
+  const int per = nblk / kXcds, rem = nblk % kXcds;
+  const int x = bid % kXcds, i = bid / kXcds;
+  return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 // Orders LDS traffic between the lanes of one wave (no block barrier).
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -135,6 +147,17 @@ template <> __device__ __forceinline__ float buf_load<f16>(__amdgpu_buffer_rsrc_
 
 __device__ __forceinline__ void buf_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+}
+// Store v converted to T (round to nearest even for the 16-bit types).
+template <typename T> __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  if constexpr (sizeof(T) == 4) {
+    buf_store_f32(r, off, v);
+  } else {
+    const T h = from_f<T>(v);
+    unsigned short b;
+    __builtin_memcpy(&b, &h, 2);
+    __builtin_amdgcn_raw_buffer_store_b16(b, r, off, 0, 0);
+  }
 }
 
 // DPP lane permutations inside rows of 16 lanes (VALU, no LDS round trip).

@@ -62,12 +62,14 @@ struct TileWave {
 };
 
 // wave id -> (b, tile j, channel group g); g varies fastest so neighbouring
-// waves write neighbouring 256-byte pieces of the same (b, t) rows. Lanes
+// waves write neighbouring 256-byte pieces of the same (b, t) rows, and the
+// XCD remap keeps consecutive tiles of a channel (which share event-value
+// lines and index rows) in one L2. Lanes
 // past `dim` are clamped to the group's last channel (addresses stay valid)
 // and flagged !ok.
 __device__ __forceinline__ TileWave tile_wave(int nT, int nG, int dim, const int32_t* tile_start) {
   TileWave w;
-  const int wid = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int wid = xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
   w.g = wid % nG;
   const int bj = wid / nG;
   w.j = bj % nT;
@@ -84,8 +86,9 @@ template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, int64_t n_events,
                                                      const uint32_t* __restrict__ bitmask, int64_t W, int64_t mrd,
                                                      const int32_t* __restrict__ tile_start, int nT, int nG,
-                                                     int waves, int dim, int64_t L, TO* __restrict__ out) {
-  if ((int)(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) >= waves) return;
+                                                     int waves, int dim, int64_t L, int64_t out_elems,
+                                                     TO* __restrict__ out) {
+  if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start);
   const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
   const int32_t cu0 = ts[0], elo = ts[w.j];
@@ -103,21 +106,19 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
     idx += bit;
   }
   float val = buf_load<TI>(ry, elo > cu0 ? (uint32_t)(elo - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
+  // One straight-line pass for every tile (v[] stays in registers): lanes
+  // past dim and steps past L get an out-of-range offset, so their stores
+  // are dropped by the buffer unit instead of branched around.
   const int64_t t0 = (int64_t)w.j * kTile;
-  TO* op = out + ((int64_t)w.b * L + t0) * dim + w.dd;
-  if (!w.ok) return;
-  if (t0 + kTile <= L) {
+  const int steps = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const int64_t obase = ((int64_t)w.b * L + t0) * dim + (int64_t)w.g * kWave;
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out + obase, (out_elems - obase) * (int64_t)sizeof(TO));
+  const uint32_t lane_off = w.ok ? (uint32_t)lane_id() * (uint32_t)sizeof(TO) : kBufOOB;
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TO);
 #pragma unroll
-    for (int s = 0; s < kTile; ++s) {
-      val = ((m >> s) & 1ull) ? v[s] : val;
-      op[(int64_t)s * dim] = from_f<TO>(val);
-    }
-  } else {
-    const int steps = (int)(L - t0);
-    for (int s = 0; s < steps; ++s) {
-      val = ((m >> s) & 1ull) ? v[s] : val;
-      op[(int64_t)s * dim] = from_f<TO>(val);
-    }
+  for (int s = 0; s < kTile; ++s) {
+    val = ((m >> s) & 1ull) ? v[s] : val;
+    buf_store<TO>(ro, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB, val);
   }
 }
 
@@ -133,18 +134,18 @@ __global__ __launch_bounds__(256) void k_restore_bwd_tiles(const TI* __restrict_
                                                            int nT, int nG, int waves, int dim, int64_t L,
                                                            int64_t n_rows, float* __restrict__ dy,
                                                            float* __restrict__ head, float* __restrict__ tail) {
-  if ((int)(blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave) >= waves) return;
+  if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  // dout rows of the tile; steps past L and lanes past dim read 0
   const int64_t t0 = (int64_t)w.j * kTile;
-  const TI* g = dout + ((int64_t)w.b * L + t0) * dim + w.dd;
+  const int steps = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const int64_t gbase = ((int64_t)w.b * L + t0) * dim + (int64_t)w.g * kWave;
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + gbase, (n_rows * L - gbase) * (int64_t)sizeof(TI));
+  const uint32_t lane_off = w.ok ? (uint32_t)lane_id() * (uint32_t)sizeof(TI) : kBufOOB;
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TI);
   float gv[kTile];
-  if (t0 + kTile <= L) {
 #pragma unroll
-    for (int s = 0; s < kTile; ++s) gv[s] = to_f(g[(int64_t)s * dim]);
-  } else {
-#pragma unroll
-    for (int s = 0; s < kTile; ++s) gv[s] = (t0 + s < L) ? to_f(g[(int64_t)s * dim]) : 0.0f;
-  }
+  for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
   const int32_t elo = tile_start[(int64_t)w.ch * (nT + 1) + w.j];
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
@@ -239,13 +240,14 @@ int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events, const uint32_t
   if (n_events < 0 || (n_events > 0 && !y)) return set_error(BCM_EINVAL, "%s: invalid y", fn);
   const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
   const int64_t waves = (n_rows / dim) * nT * nG;
-  if (waves > INT32_MAX / 2) return set_error(BCM_EINVAL, "%s: problem too large", fn);
+  // per-lane 32-bit buffer offsets span 64 rows of dim elements
+  if (waves > INT32_MAX / 2 || dim > (1 << 22)) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   auto go = [&](auto ti, auto to) {
     using TI = decltype(ti);
     using TO = decltype(to);
     hipLaunchKernelGGL((k_restore_fwd<TI, TO>), dim3(nblk(waves)), dim3(256), 0, hs(stream),
                        static_cast<const TI*>(y), n_events, bitmask, W, mask_row_div, tile_start, (int)nT, (int)nG,
-                       (int)waves, (int)dim, L, static_cast<TO*>(out));
+                       (int)waves, (int)dim, L, n_rows * L, static_cast<TO*>(out));
   };
   if (y_dtype == BCM_F32) dispatch_dtype(out_dtype, [&](auto to) { go(float{}, to); });
   else if (y_dtype == BCM_F16) go(f16{}, f16{});
@@ -273,7 +275,7 @@ int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_
   float* head = static_cast<float*>(workspace);
   float* tail = head + nT * n_rows;
   const int64_t waves = (n_rows / dim) * nT * nG;
-  if (waves > INT32_MAX / 2) return set_error(BCM_EINVAL, "%s: problem too large", fn);
+  if (waves > INT32_MAX / 2 || dim > (1 << 22)) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     hipLaunchKernelGGL(k_restore_bwd_tiles<T>, dim3(nblk(waves)), dim3(256), 0, hs(stream),
