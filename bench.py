@@ -24,6 +24,14 @@ if ROOT not in sys.path:
 
 METRIC = "fwd+bwd events/s & achieved HBM GB/s, B32 D256 L2048 N16 at 15% density"
 HBM_PEAK_GBS = 8000.0
+PROBE_STEPS = 5
+CAL_BYTES = 256 << 20  # device-to-device copy that calibrates the PMC byte counters
+
+# device kernels behind each stage of Path.KERNELS (symbol substrings)
+STAGE_KERNELS = {"count": ["k_count"], "offsets": ["k_scan_counts"], "fill": ["k_fill"],
+                 "scan_fwd": ["k_scan_fwd"], "restore_fwd": ["k_restore_fwd"],
+                 "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"], "scan_bwd": ["k_scan_bwd"],
+                 "gather_bwd": ["k_gather_bwd_rows"]}
 
 
 def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
@@ -144,6 +152,65 @@ class Path:
         return sum(v) / len(v) if v else float("nan")
 
 
+def calibration_copy(dev):
+    """One plain device copy of CAL_BYTES (hipMemcpyAsync's blit kernel)."""
+    import torch
+    a = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+
+
+def measure_traffic(cfg, stage):
+    """HBM bytes per launch of `stage` from two rocprofv3 --pmc child runs
+    (FETCH_SIZE, then WRITE_SIZE). Each counter is scaled by what it reads
+    for the CAL_BYTES copy in the same child, so the result is in bytes
+    whatever the counter's unit. Returns (bytes or None, detail dict)."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, {"skipped": "rocprofv3 not found"}
+    names = STAGE_KERNELS[stage]
+    detail = {"kernels": names, "calibration_bytes": CAL_BYTES}
+    total = 0.0
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(prefix="bcm_pmc_") as d:
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "--", sys.executable,
+                   os.path.abspath(__file__), "--pmc-child", "--cfg", str(cfg)]
+            try:
+                r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=180)
+            except subprocess.TimeoutExpired:
+                return None, dict(detail, skipped=f"{counter} pass timed out")
+            rows = []
+            for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+                rows += list(csv.DictReader(open(f)))
+            if r.returncode != 0 and not rows:
+                return None, dict(detail, skipped=f"{counter} pass failed: {r.stdout.decode()[-300:]}")
+        per_disp = {}
+        for row in rows:
+            if row.get("Counter_Name") != counter:
+                continue
+            key = (row["Kernel_Name"], row.get("Dispatch_Id", row.get("Correlation_Id", "")))
+            per_disp[key] = per_disp.get(key, 0.0) + float(row["Counter_Value"])
+        cal = max((v for (k, _), v in per_disp.items() if "copyBuffer" in k), default=0.0)
+        if cal <= 0:
+            return None, dict(detail, skipped=f"{counter}: calibration copy not found")
+        per_launch = 0.0
+        for nm in names:
+            vals = [v for (k, _), v in per_disp.items() if nm in k]
+            if not vals:
+                return None, dict(detail, skipped=f"{counter}: no dispatch of {nm}")
+            per_launch += sum(vals) / len(vals)
+        scale = CAL_BYTES / cal
+        detail[counter] = {"raw_per_launch": per_launch, "raw_calibration": cal, "bytes_per_unit": scale}
+        total += per_launch * scale
+    detail["bytes"] = total
+    return total, detail
+
+
 def cpu_baseline(cfg, batches, reps=3):
     """The torch CPU restatement of the path (oracle/torch_path.py) on a
     bounded sample of the workload: `batches` of the config's B batches."""
@@ -186,6 +253,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batches", type=int, default=4)
     ap.add_argument("--api", action="store_true", help="also time the drop-in Python API path (autograd)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc child runs that measure the dominant kernel's HBM bytes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the path shards by batch with no exchange; "
@@ -200,8 +270,18 @@ def main():
     w = make_workload(args.cfg).to(dev)
     path = Path(w, dev)
 
-    # untimed pre-pass: per-kernel durations pick the dominant kernel
+    if args.pmc_child:  # a few steps and the calibration copy, run under rocprofv3 --pmc by the parent
+        for _ in range(3):
+            path.step()
+        calibration_copy(dev)
+        torch.cuda.synchronize()
+        return
+
+    # untimed warmup (first launches load code objects), then probe steps
+    # with events around every kernel pick the dominant kernel
     for _ in range(max(args.warmup, 1)):
+        path.step()
+    for _ in range(PROBE_STEPS):
         path.step(timed=Path.KERNELS)
     per_kernel = {n: path.kernel_ms(n) for n in Path.KERNELS}
     dominant = max(per_kernel, key=per_kernel.get)
@@ -249,6 +329,10 @@ def main():
                      "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None, "launch_ms": dom_ms,
                      "bytes_per_launch": kernel_bytes[dominant]},
     }
+    if not args.no_traffic:
+        traffic, detail = measure_traffic(args.cfg, dominant)
+        result["roofline"]["traffic"] = traffic
+        result["roofline"]["traffic_detail"] = detail
     if args.api:
         result["api_ms_per_step"] = api_path_ms(w, dev, args.steps, args.warmup)
     if not args.no_cpu:
