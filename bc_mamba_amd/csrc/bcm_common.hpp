@@ -145,6 +145,10 @@ template <> __device__ __forceinline__ float buf_load<f16>(__amdgpu_buffer_rsrc_
   return __half2float(*reinterpret_cast<const f16*>(&b));
 }
 
+__device__ __forceinline__ int32_t buf_load_i32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 __device__ __forceinline__ void buf_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
 }
@@ -167,6 +171,17 @@ template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v) {
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i inside each 8 lanes
+
+// Max over the 64 lanes with DPP row steps and four lane reads (no LDS).
+__device__ __forceinline__ int wave_max_dpp(int v) {
+  v = max(v, (int)dpp<kDppXor1>((uint32_t)v));
+  v = max(v, (int)dpp<kDppXor2>((uint32_t)v));
+  v = max(v, (int)dpp<kDppHalfMirror>((uint32_t)v));
+  v = max(v, (int)dpp<0x140>((uint32_t)v));  // row_mirror: every lane holds its row's max
+  const int a = max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16));
+  const int b = max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48));
+  return max(a, b);
+}
 
 // exp2 of a clamped exponent: the decay of the reference scan
 // (selective_scan_common.h:45-52 clamps Δ·A·log2e to [-126, 126]).

@@ -15,48 +15,186 @@
 //     G lanes of a lane group owns R consecutive events (items) in registers.
 //     u, k and dout are staged through LDS with coalesced loads and read back
 //     with an odd lane stride (R+1) so the transposed reads are conflict-free.
-//   * The state loop is outermost: per state s every lane computes its R
-//     decays a = exp2(clamp(Δ·A·log2e)), folds its items into a local
-//     (prod a, h) pair, the G lanes combine the pairs with an inclusive scan
-//     (wave shuffles), and a second register pass produces the exact states.
+//   * The state loop is outermost: per state s every lane folds its R items
+//     into a local (prod a, h) pair, the G lanes combine the pairs with an
+//     inclusive scan, and a second register pass produces the exact states.
 //     y (forward) and du / dΔ (backward) accumulate per item across states in
 //     registers, so no per-event cross-lane reduction is needed.
+//   * Decays come from a per-workgroup LDS table T[s][k] = exp2(clamp(Δ(k)·A
+//     ·log2e)) for gaps k <= 64 (built with the same expression as the
+//     per-event path, so the values are identical); a wave whose chunk holds
+//     a longer gap computes every decay directly for that chunk.
+//   * Scaled recurrences: the forward runs g = h / W_B (g = a·g + Δu²) and the
+//     backward e = dx / W_C (e = a'·e' + dout·u), so the per-item multiplies
+//     by W_B / W_C leave the inner loops; they reappear once per state in the
+//     products W_B·W_C, W_B·W_C·A and in the per-state gradient sums.
+//   * A lane's product of decays is exp2(A·log2e·Σ Δ) (one transcendental per
+//     lane and state instead of a multiply per item) when every exponent is
+//     <= 0 (A <= 0 and Δ >= 0; then the clamp can only shift values below
+//     2^-126); otherwise the workgroup multiplies the decays exactly.
+//   * 16-lane groups scan with DPP row shifts (VALU, no LDS round trip);
+//     wider groups use ds_bpermute shuffles.
 //   * Chunks longer than one workgroup pass (max_seqlen > 2048 uses C = 2048,
-//     the reference's chunk) carry (prod a, h) forward in LDS; the backward
+//     the reference's chunk) carry (prod a, g) forward in LDS; the backward
 //     starts each chunk from the saved state x[ch, c-1] like the reference and
-//     carries a·dx backward in LDS.
+//     carries a·e backward in LDS.
 //   * No MFMA: the work is a first-order recurrence, not a contraction.
 #include "bcm_common.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace bcm {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kScanThreads = 512;  // workgroup size bound (8 waves)
+constexpr int kScanThreads = 512;   // workgroup size bound (8 waves)
+constexpr int kTabK = 64;           // gaps k = 1..kTabK come from the decay table
+constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
+constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
+constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
 
 struct FwdLds {
   int N, nw, G, R, nslots;
+  bool tbl;
   int64_t bytes() const {
-    return 4ll * (3ll * N + (int64_t)nw * kWave * (R + 1) + (int64_t)nslots * 2 * N);
+    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 3ll * N + (int64_t)nw * kWave * (R + 1) +
+                  (int64_t)nslots * 2 * N);
   }
 };
 
 struct BwdLds {
   int N, nw, G, R, nslots;
+  bool tbl;
   int64_t bytes() const {
-    return 4ll * (4ll * N + 2ll * nw * kWave * (R + 1) + (int64_t)nslots * N + (int64_t)nslots * (3 * N + 3));
+    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 6ll * N + 2ll * nw * kWave * (R + 1) +
+                  (int64_t)nslots * (2 * N + 3 * N + 3));
   }
 };
 
-// Position of chunk item idx in a lane-transposed LDS tile (stride R+1).
-template <int R> __device__ __forceinline__ int tpos(int idx) { return (idx / R) * (R + 1) + (idx % R); }
+// ------------------------------------------------------------ lane groups
+// The G lanes of a group hold one channel's chunk. Scan pairs compose as
+// (P1, H1)∘(P2, H2) = (P1·P2, P2·H1 + H2) (selective_scan_common.h:156-161).
+template <int G> struct Grp {  // generic width: ds_bpermute shuffles
+  static __device__ __forceinline__ int j() { return lane_id() % G; }
+  static __device__ __forceinline__ void scan_up(float& P, float& H) {  // inclusive, lanes 0..j
+    const int jj = j();
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) {
+      const float Pp = __shfl_up(P, o, G), Hp = __shfl_up(H, o, G);
+      if (jj >= o) {
+        H = fmaf(P, Hp, H);
+        P *= Pp;
+      }
+    }
+  }
+  static __device__ __forceinline__ void scan_down(float& Q, float& C) {  // inclusive, lanes j..G-1
+    const int jj = j();
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) {
+      const float Qs = __shfl_down(Q, o, G), Cs = __shfl_down(C, o, G);
+      if (jj + o < G) {
+        C = fmaf(Q, Cs, C);
+        Q *= Qs;
+      }
+    }
+  }
+  static __device__ __forceinline__ float prev(float v, float first) {  // lane j-1; `first` in lane 0
+    const float p = __shfl_up(v, 1, G);
+    return j() == 0 ? first : p;
+  }
+  static __device__ __forceinline__ float next(float v, float last) {  // lane j+1; `last` in lane G-1
+    const float p = __shfl_down(v, 1, G);
+    return j() == G - 1 ? last : p;
+  }
+  static __device__ __forceinline__ float sum(float v) { return group_sum<G>(v); }
+};
 
-template <int G, int R, typename T, bool HAS_Z>
+// DPP move inside 16-lane rows; lanes whose source falls outside the row get `old`.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kRowShl = 0x100;     // row_shl:n -> lane i reads lane i+n
+constexpr int kRowShr = 0x110;     // row_shr:n -> lane i reads lane i-n
+constexpr int kRowMirror = 0x140;  // lane i reads lane 15-i
+
+template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are VALU
+  template <int O> static __device__ __forceinline__ void up(float& P, float& H) {
+    const float Pp = dpp_mov<kRowShr + O>(P, 1.0f), Hp = dpp_mov<kRowShr + O>(H, 0.0f);
+    H = fmaf(P, Hp, H);
+    P *= Pp;
+  }
+  template <int O> static __device__ __forceinline__ void down(float& Q, float& C) {
+    const float Qs = dpp_mov<kRowShl + O>(Q, 1.0f), Cs = dpp_mov<kRowShl + O>(C, 0.0f);
+    C = fmaf(Q, Cs, C);
+    Q *= Qs;
+  }
+  static __device__ __forceinline__ void scan_up(float& P, float& H) {
+    up<1>(P, H);
+    up<2>(P, H);
+    up<4>(P, H);
+    up<8>(P, H);
+  }
+  static __device__ __forceinline__ void scan_down(float& Q, float& C) {
+    down<1>(Q, C);
+    down<2>(Q, C);
+    down<4>(Q, C);
+    down<8>(Q, C);
+  }
+  static __device__ __forceinline__ float prev(float v, float first) { return dpp_mov<kRowShr + 1>(v, first); }
+  static __device__ __forceinline__ float next(float v, float last) { return dpp_mov<kRowShl + 1>(v, last); }
+  static __device__ __forceinline__ float sum(float v) {
+    v += __uint_as_float(dpp<kDppXor1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kDppXor2>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(v)));
+    v += __uint_as_float(dpp<kRowMirror>(__float_as_uint(v)));
+    return v;
+  }
+};
+
+// Chunk staging: lane j of a G-lane group owns the R consecutive items
+// j*R .. j*R+R-1 of the chunk. Global memory is read and written row by row
+// (item q*G + j in step q: coalesced) and transposed through the group's LDS
+// tile, where item i sits at i + i/R (lane stride R+1: conflict-free reads).
+template <int R> __device__ __forceinline__ int tile_pos(int idx) { return idx + idx / R; }
+
+// The value itself, hidden from common-subexpression elimination: offsets
+// recomputed after the state loop are not kept live across it.
+template <typename V> __device__ __forceinline__ V opaque(V v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Decay of an item from the table: `tb` is the item's byte offset in a table
+// row, `row` the state's row base in bytes (wave-uniform), so each read costs
+// one address add.
+__device__ __forceinline__ float tab(const float* sT, uint32_t row, uint32_t tb) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + (row + tb));
+}
+
+// Decay table of workgroup d: T[s][0] = 1 (padding), T[s][k] = the decay of
+// gap k (same expression and rounding as the per-event path).
+__device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
+  const int N = a.dstate;
+  for (int i = threadIdx.x; i < N * kTabStride; i += blockDim.x) {
+    const int s = i / kTabStride, q = i - s * kTabStride;
+    sT[i] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * (a.A[(int64_t)d * N + s] * kLog2e));
+  }
+}
+
+// 1 if some decay exponent of workgroup d can be positive (A > 0 or Δ < 0):
+// lane products are then multiplied out exactly. Block-wide vote.
+__device__ __forceinline__ bool exact_products(const bcm_scan_args& a, int d, float dti, float dta) {
+  int f = (dti < 0.0f || dta < 0.0f) ? 1 : 0;
+  for (int s = threadIdx.x; s < a.dstate; s += blockDim.x) f |= a.A[(int64_t)d * a.dstate + s] > 0.0f ? 1 : 0;
+  return __syncthreads_or(f) != 0;
+}
+
+template <int G, int R, typename T, bool HAS_Z, bool TBL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a) {
+  using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
-  constexpr int RS = R + 1;
   constexpr int C = G * R;
+  constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
   const int d = blockIdx.x;
   const int nw = blockDim.x / kWave;
@@ -66,120 +204,146 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   const int slot = wave * CPW + grp;
 
   extern __shared__ float smem[];
-  float* sAl = smem;
+  float* sT = smem;
+  float* sAl = sT + (TBL ? N * kTabStride : 0);
   float* sWB = sAl + N;
-  float* sWC = sWB + N;
-  float* gst = sWC + N + wave * (kWave * RS) + grp * (G * RS);
-  float* carry = smem + 3 * N + nw * kWave * RS + slot * 2 * N;  // [P_run(N), h_run(N)]
+  float* sWBC = sWB + N;
+  float* tile = sWBC + N + wave * (kWave * (R + 1)) + grp * (G * (R + 1));  // the group's staging tile
+  float* mine = tile + j * (R + 1);                                         // this lane's R items
+  float* carry = sWBC + N + nw * kWave * (R + 1) + slot * 2 * N;            // [P_run(N), g_run(N)]
 
-  for (int s = threadIdx.x; s < N; s += blockDim.x) {
-    sAl[s] = a.A[(int64_t)d * N + s] * kLog2e;
-    sWB[s] = a.W_B[(int64_t)d * N + s];
-    sWC[s] = a.W_C[(int64_t)d * N + s];
-  }
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  __syncthreads();
+  for (int s = threadIdx.x; s < N; s += blockDim.x) {
+    const float wb = a.W_B[(int64_t)d * N + s];
+    sAl[s] = a.A[(int64_t)d * N + s] * kLog2e;
+    sWB[s] = wb;
+    sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
+  }
+  if (TBL) build_decay_table(sT, a, d, dti, dta);
+  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
+  (void)nslots;
 
-  const T* __restrict__ u = static_cast<const T*>(a.u);
-  const T* __restrict__ z = static_cast<const T*>(a.z);
-  T* __restrict__ out = static_cast<T*>(a.out);
-  T* __restrict__ out_z = static_cast<T*>(a.out_z);
+  // per-event arrays as buffer resources: items past a channel's events use
+  // an out-of-range offset (loads read 0, stores are dropped)
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.out, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), roz = buf_rsrc(a.out_z, HAS_Z ? E * SZ : 0);
   const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
 
-  for (int b0 = 0; b0 < n_per_d; b0 += nslots) {
+  for (int b0 = 0; b0 < n_per_d; b0 += nw * CPW) {
     const int b = b0 + slot;
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
     const int e0 = act ? a.cu_seqlens[ch] : 0;
     const int n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
     const int nch = n > 0 ? (n + C - 1) / C : 0;
-    const int wmax = wave_max(nch);
+    const int wmax = wave_max_dpp(nch);
     for (int c = 0; c < wmax; ++c) {
       const int cnt = min(max(n - c * C, 0), C);
-      const int64_t eb = (int64_t)e0 + (int64_t)c * C;
-      // ---- stage u and k through LDS (coalesced global reads)
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        gst[tpos<R>(idx)] = idx < cnt ? to_f(u[eb + idx]) : 0.0f;
-      }
-      wave_sync();
+      const int nv = cnt - j * R;                 // events among this lane's R items
+      const uint32_t eb = (uint32_t)(e0 + c * C);  // event index of the chunk's first item
+      // ---- stage u, then k (positions recomputed per chunk: opaque() keeps
+      // them from being hoisted and held in registers across chunks)
       float uu[R];
+      {
+        const int jo = opaque(j);
 #pragma unroll
-      for (int r = 0; r < R; ++r) uu[r] = gst[j * RS + r];
-      wave_sync();
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
+        }
+        wave_sync();
 #pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        gst[tpos<R>(idx)] = __int_as_float(idx < cnt ? a.k[eb + idx] : 1);
+        for (int r = 0; r < R; ++r) uu[r] = mine[r];
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          tile[tile_pos<R>(idx)] = __int_as_float(buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB));
+        }
+        wave_sync();
       }
-      wave_sync();
       float dl[R], du2[R], acc[R];
+      uint32_t tb[R];  // byte offset of the item's gap in a table row (0: padding)
+      int big = 0;
+      float S = 0.0f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int kk = __float_as_int(gst[j * RS + r]);
-        // padding items are identities of the scan: Δ = 0 -> a = 1, b = 0
-        dl[r] = (j * R + r < cnt) ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+        const bool valid = r < nv;
+        const int kk = __float_as_int(mine[r]);
+        // padding items are identities of the scan: Δ = 0 -> a = 1, Δu² = 0
+        const int km1 = valid ? kk - 1 : -1;
+        dl[r] = valid ? fmaf(dti, (float)km1, dta) : 0.0f;
         du2[r] = dl[r] * uu[r] * uu[r];
+        tb[r] = (uint32_t)(km1 + 1) * 4u;
+        big |= km1 >= kTabK ? 1 : 0;
+        S += dl[r];
         acc[r] = 0.0f;
       }
-      wave_sync();
-      // ---- state loop
-      for (int s = 0; s < N; ++s) {
-        const float Al = sAl[s], wb = sWB[s], wc = sWC[s];
-        float av[R];
-        float P = 1.0f, H = 0.0f;
+      // ---- state loop; EXACT: decays computed per item, products multiplied out
+      auto states = [&](auto exact_tag) {
+        constexpr bool EXACT = decltype(exact_tag)::value;
+#pragma unroll 1
+        for (int s = 0; s < N; ++s) {
+          const float Al = sAl[s], wbc = sWBC[s];
+          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(s * kTabStride * 4);
+          float av[R];
+          float P = 1.0f, H = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          av[r] = decay(dl[r] * Al);
-          H = fmaf(av[r], H, du2[r] * wb);
-          P *= av[r];
-        }
+          for (int r = 0; r < R; ++r) {
+            av[r] = EXACT ? decay(dl[r] * Al) : tab(sT, row, tb[r]);
+            H = fmaf(av[r], H, du2[r]);
+            if (EXACT) P *= av[r];
+          }
+          if (!EXACT) P = decay(S * Al);
+          Ops::scan_up(P, H);
+          const float g0 = c > 0 ? carry[N + s] : 0.0f;
+          const float P0 = c > 0 ? carry[s] : 1.0f;
+          const float gend = fmaf(P, g0, H);
+          float g = Ops::prev(gend, g0);
 #pragma unroll
-        for (int o = 1; o < G; o <<= 1) {
-          const float Pp = __shfl_up(P, o, G);
-          const float Hp = __shfl_up(H, o, G);
-          if (j >= o) {
-            H = fmaf(P, Hp, H);
-            P *= Pp;
+          for (int r = 0; r < R; ++r) {
+            g = fmaf(av[r], g, du2[r]);
+            acc[r] = fmaf(g, wbc, acc[r]);
+          }
+          if (j == G - 1 && c < nch) {
+            const float Pn = P0 * P;
+            carry[s] = Pn;
+            carry[N + s] = gend;
+            if (c < nck)
+              reinterpret_cast<float2*>(a.x + (ch * nck + c) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
           }
         }
-        const float h0 = c > 0 ? carry[N + s] : 0.0f;
-        const float P0 = c > 0 ? carry[s] : 1.0f;
-        const float hend = fmaf(P, h0, H);
-        float h = __shfl_up(hend, 1, G);
-        if (j == 0) h = h0;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          h = fmaf(av[r], h, du2[r] * wb);
-          acc[r] = fmaf(h, wc, acc[r]);
-        }
-        if (j == G - 1 && c < nch) {
-          const float Pn = P0 * P;
-          carry[s] = Pn;
-          carry[N + s] = hend;
-          if (c < nck) reinterpret_cast<float2*>(a.x + (ch * nck + c) * 2 * N)[s] = make_float2(Pn, hend);
-        }
+      };
+      if constexpr (TBL) {
+        if (exact_blk || __any(big)) states(std::true_type{});
+        else states(std::false_type{});
+      } else {
+        states(std::true_type{});
       }
-      // ---- outputs: y = D·u + u·Σ_s h·W_C, staged for a coalesced store
-#pragma unroll
-      for (int r = 0; r < R; ++r) gst[j * RS + r] = fmaf(Dv, uu[r], uu[r] * acc[r]);
+      // ---- outputs: y = D·u + u·Σ_s g·W_B·W_C (and y·silu(z)), stored row by row
       wave_sync();
 #pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        if (idx < cnt) {
-          const float yv = gst[tpos<R>(idx)];
-          out[eb + idx] = from_f<T>(yv);
+      for (int r = 0; r < R; ++r) mine[r] = fmaf(Dv, uu[r], uu[r] * acc[r]);
+      wave_sync();
+      {
+        const int jo = opaque(j);
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
+          const float yv = tile[tile_pos<R>(idx)];
+          buf_store<T>(ro, off, yv);
           if (HAS_Z) {
-            const float zv = to_f(z[eb + idx]);
-            out_z[eb + idx] = from_f<T>(yv * (zv / (1.0f + __expf(-zv))));
+            const float zv = buf_load<T>(rz, off);
+            buf_store<T>(roz, off, yv * (zv / (1.0f + __expf(-zv))));
           }
         }
       }
-      wave_sync();
+      wave_sync();  // the tile and the carry (written by lane G-1) are reused in the next chunk
     }
     // chunks past the channel's end keep the reference's zero state
     if (act) {
@@ -189,11 +353,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   }
 }
 
-template <int G, int R, typename T, bool HAS_Z>
+template <int G, int R, typename T, bool HAS_Z, bool TBL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a) {
+  using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int RS = R + 1;
   constexpr int C = G * R;
+  constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
   const int d = blockIdx.x;
   const int nw = blockDim.x / kWave;
@@ -204,36 +370,47 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   const int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
 
   extern __shared__ float smem[];
-  float* sA = smem;
-  float* sAl = sA + N;
+  float* sT = smem;
+  float* sAl = sT + (TBL ? N * kTabStride : 0);
   float* sWB = sAl + N;
   float* sWC = sWB + N;
-  float* wbase = sWC + N + wave * (2 * kWave * RS);
-  float* gdt = wbase + grp * (G * RS);            // gated dout, kept for the chunk
-  float* gkm = wbase + kWave * RS + grp * (G * RS);  // staging, then k-1 kept for the chunk
-  float* sdx = smem + 4 * N + nw * 2 * kWave * RS;   // [nslots][N] a·dx carried to the previous chunk
-  float* sacc = sdx + nslots * N;                    // [nslots][NA]
+  float* sWBC = sWC + N;
+  float* sWBCA = sWBC + N;
+  float* sA = sWBCA + N;
+  // per lane, stride R+1 (conflict-free): the states g of the current state
+  // s (the group's staging tile outside the state loop), and the items' gap
+  // k-1 (0 for padding)
+  float* tile = sA + N + wave * (kWave * RS) + grp * (G * RS);
+  float* gg = tile + j * RS;
+  float* gkm = sA + N + nw * kWave * RS + threadIdx.x * RS;
+  float* sdx = sA + N + 2 * nw * kWave * RS;  // [nslots][N] a·e carried to the previous chunk
+  float* sg0 = sdx + nslots * N;              // [nslots][N] g at the chunk start
+  float* sacc = sg0 + nslots * N;             // [nslots][NA]
   float* cdx = sdx + slot * N;
+  float* cg0 = sg0 + slot * N;
   float* cacc = sacc + slot * NA;
 
-  for (int s = threadIdx.x; s < N; s += blockDim.x) {
-    const float Av = a.A[(int64_t)d * N + s];
-    sA[s] = Av;
-    sAl[s] = Av * kLog2e;
-    sWB[s] = a.W_B[(int64_t)d * N + s];
-    sWC[s] = a.W_C[(int64_t)d * N + s];
-  }
-  for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  __syncthreads();
+  for (int s = threadIdx.x; s < N; s += blockDim.x) {
+    const float Av = a.A[(int64_t)d * N + s];
+    const float wb = a.W_B[(int64_t)d * N + s], wc = a.W_C[(int64_t)d * N + s];
+    sA[s] = Av;
+    sAl[s] = Av * kLog2e;
+    sWB[s] = wb;
+    sWC[s] = wc;
+    sWBC[s] = wb * wc;
+    sWBCA[s] = wb * wc * Av;
+  }
+  for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
+  if (TBL) build_decay_table(sT, a, d, dti, dta);
+  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
 
-  const T* __restrict__ u = static_cast<const T*>(a.u);
-  const T* __restrict__ dout = static_cast<const T*>(a.dout);
-  const T* __restrict__ z = static_cast<const T*>(a.z);
-  const T* __restrict__ outs = static_cast<const T*>(a.out_saved);
-  T* __restrict__ du_o = static_cast<T*>(a.du);
-  T* __restrict__ dz_o = static_cast<T*>(a.dz);
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
+  const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
   const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
 
@@ -244,158 +421,217 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
     const int e0 = act ? a.cu_seqlens[ch] : 0;
     const int n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
     const int nch = n > 0 ? (n + C - 1) / C : 0;
-    const int wmax = wave_max(nch);
+    const int wmax = wave_max_dpp(nch);
     float ddti_l = 0.0f, ddta_l = 0.0f, dD_l = 0.0f;
     for (int c = wmax - 1; c >= 0; --c) {
       const bool cact = c < nch;
       const int cnt = min(max(n - c * C, 0), C);
-      const int64_t eb = (int64_t)e0 + (int64_t)c * C;
-      // ---- stage u
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        gkm[tpos<R>(idx)] = idx < cnt ? to_f(u[eb + idx]) : 0.0f;
-      }
-      wave_sync();
-      float uu[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) uu[r] = gkm[j * RS + r];
-      wave_sync();
-      // ---- stage k-1 (kept) and the gated dout (kept); dz on the way
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        const int p = tpos<R>(idx);
-        float km1 = 0.0f, dv = 0.0f;
-        if (idx < cnt) {
-          km1 = (float)(a.k[eb + idx] - 1);
-          dv = to_f(dout[eb + idx]);
-          if (HAS_Z) {
-            const float zv = to_f(z[eb + idx]);
-            const float ov = to_f(outs[eb + idx]);
-            const float sg = 1.0f / (1.0f + __expf(-zv));
-            dz_o[eb + idx] = from_f<T>(dv * ov * sg * (1.0f + zv * (1.0f - sg)));
-            dv *= zv * sg;
-          }
+      const int nv = cnt - j * R;
+      const uint32_t eb = (uint32_t)(e0 + c * C);
+      // chunk-start state in g = h / W_B form (saved h of the previous chunk)
+      if (c > 0) {
+        for (int s = j; s < N; s += G) {
+          const float h0 = (c - 1 < nck) ? a.x_saved[(ch * nck + (c - 1)) * 2 * N + 2 * s + 1] : 0.0f;
+          const float wb = sWB[s];
+          cg0[s] = wb != 0.0f ? h0 / wb : 0.0f;
         }
-        gkm[p] = km1;
-        gdt[p] = dv;
       }
-      wave_sync();
-      float dl[R], du2[R], doutu[R], acc1[R], acc2[R], acc3[R];
+      float du2[R], doutu[R], acc1[R], acc2[R];
+      uint32_t tb[R];  // byte offset of the item's gap k in a table row (4k; 0: padding)
+      int big = 0;
+      float S = 0.0f, dl0 = 0.0f;
+      {
+        // ---- stage k, u and the gated dout through the tile (dz on the way);
+        // positions recomputed per chunk (opaque: not hoisted across chunks)
+        const int jo = opaque(j);
+        float dlv[R], uvv[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const bool valid = j * R + r < cnt;
-        dl[r] = valid ? fmaf(dti, gkm[j * RS + r], dta) : 0.0f;
-        du2[r] = dl[r] * uu[r] * uu[r];
-        doutu[r] = gdt[j * RS + r] * uu[r];
-        acc1[r] = 0.0f;
-        acc2[r] = 0.0f;
-        acc3[r] = 0.0f;
-      }
-      // ---- state loop
-      for (int s = 0; s < N; ++s) {
-        const float Ar = sA[s], Al = sAl[s], wb = sWB[s], wc = sWC[s];
-        const float h0 = (c > 0 && c - 1 < nck) ? a.x_saved[(ch * nck + (c - 1)) * 2 * N + 2 * s + 1] : 0.0f;
-        const float dxc = (c < nch - 1) ? cdx[s] : 0.0f;
-        float av[R], hh[R];
-        // forward: local fold, group scan, exact states
-        float P = 1.0f, H = 0.0f;
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          tile[tile_pos<R>(idx)] = __int_as_float(buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB));
+        }
+        wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          av[r] = decay(dl[r] * Al);
-          H = fmaf(av[r], H, du2[r] * wb);
-          P *= av[r];
+          const bool valid = r < nv;
+          const int kk = __float_as_int(gg[r]);
+          tb[r] = valid ? (uint32_t)kk * 4u : 0u;
+          dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+          gkm[r] = valid ? (float)(kk - 1) : 0.0f;
+          big |= (valid && kk > kTabK) ? 1 : 0;
+          S += dlv[r];
         }
+        dl0 = dlv[0];
+        wave_sync();
 #pragma unroll
-        for (int o = 1; o < G; o <<= 1) {
-          const float Pp = __shfl_up(P, o, G);
-          const float Hp = __shfl_up(H, o, G);
-          if (j >= o) {
-            H = fmaf(P, Hp, H);
-            P *= Pp;
-          }
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
         }
-        const float hend = fmaf(P, h0, H);
-        float hin = __shfl_up(hend, 1, G);
-        if (j == 0) hin = h0;
-        {
-          float h = hin;
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r) uvv[r] = gg[r];
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
+          float dv = buf_load<T>(rdo, off);
+          if (HAS_Z) {
+            const float zv = buf_load<T>(rz, off);
+            const float ov = buf_load<T>(ros, off);
+            const float sg = 1.0f / (1.0f + __expf(-zv));
+            buf_store<T>(rdz, off, dv * ov * sg * (1.0f + zv * (1.0f - sg)));
+            dv *= zv * sg;
+          }
+          tile[tile_pos<R>(idx)] = dv;
+        }
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          du2[r] = dlv[r] * uvv[r] * uvv[r];
+          doutu[r] = gg[r] * uvv[r];
+          acc1[r] = 0.0f;
+          acc2[r] = 0.0f;
+        }
+        wave_sync();  // the tile becomes the states g of the state loop
+      }
+      // Σ Δ over the items that follow each of the lane's items (the next
+      // lane's first; nothing past the chunk: its carry already holds a·e)
+      const float S1 = S - dl0 + Ops::next(dl0, 0.0f);
+      // the state loop reads gkm through an index the compiler cannot see
+      // through, so it re-reads LDS instead of keeping the stored values live
+      const float* km = gkm + opaque(0);
+      wave_sync();  // cg0 written by the group's lanes
+      // ---- state loop; EXACT: decays computed per item, products multiplied out
+      auto states = [&](auto exact_tag) {
+        constexpr bool EXACT = decltype(exact_tag)::value;
+#pragma unroll 1
+        for (int s = 0; s < N; ++s) {
+          const float Al = sAl[s], wbc = sWBC[s], wbca = sWBCA[s];
+          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(s * kTabStride * 4);
+          const float g0 = c > 0 ? cg0[s] : 0.0f;
+          const float ec = (c < nch - 1) ? cdx[s] : 0.0f;
+          float av[R];
+          // forward: local fold, group scan, exact states (kept in LDS)
+          float P = 1.0f, H = 0.0f;
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            h = fmaf(av[r], h, du2[r] * wb);
-            hh[r] = h;
+            av[r] = EXACT ? decay((tb[r] ? fmaf(dti, km[r], dta) : 0.0f) * Al) : tab(sT, row, tb[r]);
+            H = fmaf(av[r], H, du2[r]);
+            if (EXACT) P *= av[r];
+          }
+          if (!EXACT) P = decay(S * Al);
+          Ops::scan_up(P, H);
+          const float gin = Ops::prev(fmaf(P, g0, H), g0);
+          {
+            float g = gin;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              g = fmaf(av[r], g, du2[r]);
+              gg[r] = g;
+            }
+          }
+          // reverse: e_i = dout_i·u_i + a_{i+1}·e_{i+1}   (dx = W_C·e)
+          const float anext = Ops::next(av[0], 1.0f);  // the chunk carry already holds a_next·e_next
+          float Q = 1.0f, Ce = 0.0f;
+#pragma unroll
+          for (int r = R - 1; r >= 0; --r) {
+            const float al = (r == R - 1) ? anext : av[r + 1];
+            Ce = fmaf(al, Ce, doutu[r]);
+            if (EXACT) Q *= al;
+          }
+          if (!EXACT) Q = decay(S1 * Al);
+          Ops::scan_down(Q, Ce);
+          float e = Ops::next(fmaf(Q, ec, Ce), ec);
+          // tg = dx·a·h_prev / (W_B·W_C); with Δ = dt_idle·(k-1) + dt_active the
+          // Δ-weighted sums need only T0 = Σ tg and T1 = Σ tg·(k-1)
+          float T0 = 0.0f, T1 = 0.0f, dWB_l = 0.0f, dWC_l = 0.0f;
+#pragma unroll
+          for (int r = R - 1; r >= 0; --r) {
+            if (r % kSchedBlock == kSchedBlock - 1) __builtin_amdgcn_sched_barrier(0);
+            const float al = (r == R - 1) ? anext : av[r + 1];
+            const float gr = gg[r];
+            const float gp = r > 0 ? gg[r - 1] : gin;
+            e = fmaf(al, e, doutu[r]);
+            acc1[r] = fmaf(e, wbc, acc1[r]);       // Σ_s dx·W_B
+            acc2[r] = fmaf(gr, wbc, acc2[r]);      // Σ_s h·W_C
+            const float tg = e * (av[r] * gp);
+            T0 += tg;
+            T1 = fmaf(tg, km[r], T1);
+            dWB_l = fmaf(e, du2[r], dWB_l);
+            dWC_l = fmaf(doutu[r], gr, dWC_l);
+          }
+          if (j == 0 && cact) cdx[s] = av[0] * e;
+          // dΔ_i gets Σ_s dx·a·h_prev·A: its ddt sums take T0, T1 lane by lane
+          ddta_l = fmaf(wbca, T0, ddta_l);
+          ddti_l = fmaf(wbca, T1, ddti_l);
+          float dA_l = Ops::sum(fmaf(dti, T1, dta * T0));
+          dWB_l = Ops::sum(dWB_l);
+          dWC_l = Ops::sum(dWC_l);
+          if (j == 0 && cact) {
+            cacc[s] += dA_l * wbc;
+            cacc[N + s] += dWB_l * sWC[s];
+            cacc[2 * N + s] += dWC_l * sWB[s];
           }
         }
-        // reverse: dx_i = dout_i·u_i·W_C + a_{i+1}·dx_{i+1}
-        float anext = __shfl_down(av[0], 1, G);
-        if (j == G - 1) anext = 1.0f;  // the chunk carry already holds a_next·dx_next
-        float Q = 1.0f, Cc = 0.0f;
+      };
+      if constexpr (TBL) {
+        if (exact_blk || __any(big)) states(std::true_type{});
+        else states(std::false_type{});
+      } else {
+        states(std::true_type{});
+      }
+      // ---- per item: du, dΔ -> ddt, dD (u and the gated dout staged again)
+      wave_sync();
+      {
+        const int jo = opaque(j);
+        float uvv[R];
 #pragma unroll
-        for (int r = R - 1; r >= 0; --r) {
-          const float al = (r == R - 1) ? anext : av[r + 1];
-          Cc = fmaf(al, Cc, doutu[r] * wc);
-          Q *= al;
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
         }
+        wave_sync();
 #pragma unroll
-        for (int o = 1; o < G; o <<= 1) {
-          const float Qs = __shfl_down(Q, o, G);
-          const float Cs = __shfl_down(Cc, o, G);
-          if (j + o < G) {
-            Cc = fmaf(Q, Cs, Cc);
-            Q *= Qs;
+        for (int r = 0; r < R; ++r) uvv[r] = gg[r];
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
+          float dv = buf_load<T>(rdo, off);
+          if (HAS_Z) {
+            const float zv = buf_load<T>(rz, off);
+            dv *= zv / (1.0f + __expf(-zv));
           }
+          tile[tile_pos<R>(idx)] = dv;
         }
-        const float tfirst = fmaf(Q, dxc, Cc);
-        float dx = __shfl_down(tfirst, 1, G);
-        if (j == G - 1) dx = dxc;
-        float dA_l = 0.0f, dWB_l = 0.0f, dWC_l = 0.0f;
+        wave_sync();
 #pragma unroll
-        for (int r = R - 1; r >= 0; --r) {
-          const float al = (r == R - 1) ? anext : av[r + 1];
-          dx = fmaf(al, dx, doutu[r] * wc);
-          acc1[r] = fmaf(dx, wb, acc1[r]);
-          acc2[r] = fmaf(hh[r], wc, acc2[r]);
-          const float hp = r > 0 ? hh[r - 1] : hin;
-          const float t2 = dx * (av[r] * hp);
-          acc3[r] = fmaf(t2, Ar, acc3[r]);
-          dA_l = fmaf(t2, dl[r], dA_l);
-          dWB_l = fmaf(dx, du2[r], dWB_l);
-          dWC_l = fmaf(doutu[r], hh[r], dWC_l);
+        for (int r = 0; r < R; ++r) {
+          const float uv = uvv[r];
+          const float km1 = gkm[r];
+          const float dlr = tb[r] ? fmaf(dti, km1, dta) : 0.0f;
+          const float duv = fmaf(gg[r], Dv + acc2[r], 2.0f * dlr * uv * acc1[r]);
+          const float dd = uv * uv * acc1[r];  // the A-term of dΔ went into ddt in the state loop
+          ddti_l = fmaf(dd, km1, ddti_l);
+          ddta_l += dd;
+          dD_l += doutu[r];
+          gg[r] = duv;
         }
-        if (j == 0 && cact) cdx[s] = av[0] * dx;
-        dA_l = group_sum<G>(dA_l);
-        dWB_l = group_sum<G>(dWB_l);
-        dWC_l = group_sum<G>(dWC_l);
-        if (j == 0 && cact) {
-          cacc[s] += dA_l;
-          cacc[N + s] += dWB_l;
-          cacc[2 * N + s] += dWC_l;
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, tile[tile_pos<R>(idx)]);
         }
       }
-      // ---- per item: du, dΔ -> ddt, dD
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float dt = gdt[j * RS + r];
-        const float km1 = gkm[j * RS + r];
-        const float duv = fmaf(dt, Dv + acc2[r], 2.0f * dl[r] * uu[r] * acc1[r]);
-        const float dd = fmaf(uu[r] * uu[r], acc1[r], acc3[r]);
-        ddti_l = fmaf(dd, km1, ddti_l);
-        ddta_l += dd;
-        dD_l += doutu[r];
-        gdt[j * RS + r] = duv;
-      }
-      wave_sync();
-#pragma unroll
-      for (int q = 0; q < R; ++q) {
-        const int idx = q * G + j;
-        if (idx < cnt) du_o[eb + idx] = from_f<T>(gdt[tpos<R>(idx)]);
-      }
-      wave_sync();
+      wave_sync();  // cdx (LDS) written by lane 0, read by the group in the previous chunk
     }
-    ddti_l = group_sum<G>(ddti_l);
-    ddta_l = group_sum<G>(ddta_l);
-    dD_l = group_sum<G>(dD_l);
+    ddti_l = Ops::sum(ddti_l);
+    ddta_l = Ops::sum(ddta_l);
+    dD_l = Ops::sum(dD_l);
     if (j == 0 && act) {
       cacc[3 * N] += ddti_l;
       cacc[3 * N + 1] += ddta_l;
@@ -423,7 +659,7 @@ static int max_lds_bytes() {
   return v;
 }
 
-template <int G, int R, typename T, bool Z, bool BWD>
+template <int G, int R, typename T, bool Z, bool BWD, bool TBL>
 static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
   constexpr int CPW = kWave / G;
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
@@ -432,34 +668,41 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
   const int64_t cap = max_lds_bytes();
   int64_t lds = 0;
   for (;;) {
-    lds = BWD ? BwdLds{a.dstate, nw, G, R, nw * CPW}.bytes() : FwdLds{a.dstate, nw, G, R, nw * CPW}.bytes();
+    lds = BWD ? BwdLds{a.dstate, nw, G, R, nw * CPW, TBL}.bytes() : FwdLds{a.dstate, nw, G, R, nw * CPW, TBL}.bytes();
     if (lds <= cap || nw == 1) break;
     --nw;
   }
   if (lds > cap) return set_error(BCM_EINVAL, "%s: dstate %d needs %lld bytes of LDS (> %lld)", fn, a.dstate,
                                   (long long)lds, (long long)cap);
   if (BWD)
-    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
+    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
   else
-    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
+    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
   return check_launch(fn);
+}
+
+// Lane-group shape (G lanes x R items per channel chunk) by dstate and the
+// longest channel; channels longer than one pass loop over 2048-event chunks.
+template <typename T, bool Z, bool BWD, bool TBL>
+static int dispatch_len(const bcm_scan_args& a, hipStream_t s, const char* fn) {
+  const int m = a.max_seqlen;
+  if (TBL) {
+    if (m <= 64) return launch<16, 4, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 128) return launch<16, 8, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 256) return launch<16, 16, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 384) return launch<16, 24, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 512) return launch<32, 16, T, Z, BWD, TBL>(a, s, fn);
+  } else {
+    if (m <= 256) return launch<64, 4, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 512) return launch<64, 8, T, Z, BWD, TBL>(a, s, fn);
+  }
+  if (m <= 1024) return launch<64, 16, T, Z, BWD, TBL>(a, s, fn);
+  return launch<64, 32, T, Z, BWD, TBL>(a, s, fn);
 }
 
 template <typename T, bool Z, bool BWD>
 static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn) {
-  const int m = a.max_seqlen;
-  if (a.dstate <= 64) {
-    if (m <= 64) return launch<16, 4, T, Z, BWD>(a, s, fn);
-    if (m <= 128) return launch<16, 8, T, Z, BWD>(a, s, fn);
-    if (m <= 256) return launch<16, 16, T, Z, BWD>(a, s, fn);
-    if (m <= 384) return launch<16, 24, T, Z, BWD>(a, s, fn);
-    if (m <= 512) return launch<32, 16, T, Z, BWD>(a, s, fn);
-  } else {
-    if (m <= 256) return launch<64, 4, T, Z, BWD>(a, s, fn);
-    if (m <= 512) return launch<64, 8, T, Z, BWD>(a, s, fn);
-  }
-  if (m <= 1024) return launch<64, 16, T, Z, BWD>(a, s, fn);
-  return launch<64, 32, T, Z, BWD>(a, s, fn);
+  return a.dstate <= kTabMaxN ? dispatch_len<T, Z, BWD, true>(a, s, fn) : dispatch_len<T, Z, BWD, false>(a, s, fn);
 }
 
 template <bool BWD>

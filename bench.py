@@ -173,6 +173,10 @@ def measure_traffic(cfg, stage):
     prof = shutil.which("rocprofv3")
     if prof is None:
         return None, {"skipped": "rocprofv3 not found"}
+    if any(k.startswith("ROCPROF") for k in os.environ) or "rocprof" in os.environ.get("LD_PRELOAD", ""):
+        # already running under a profiler: its preloaded library has the GPU
+        # open, and a nested profiler would re-exec from this process
+        return None, {"skipped": "running under a profiler"}
     names = STAGE_KERNELS[stage]
     detail = {"kernels": names, "calibration_bytes": CAL_BYTES}
     total = 0.0
