@@ -283,39 +283,54 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
         S += dl[r];
         acc[r] = 0.0f;
       }
-      // ---- state loop; EXACT: decays computed per item, products multiplied out
+      // ---- state loop. EXACT: decays computed per item, products multiplied
+      // out. Otherwise decays come from the table, and the next state's reads
+      // are issued before this state's second pass (two register buffers).
+      auto state = [&](int s, float (&av)[R], float (&avn)[R], auto exact_tag) {
+        constexpr bool EXACT = decltype(exact_tag)::value;
+        const float Al = sAl[s], wbc = sWBC[s];
+        float P = 1.0f, H = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (EXACT) av[r] = decay(dl[r] * Al);
+          H = fmaf(av[r], H, du2[r]);
+          if (EXACT) P *= av[r];
+        }
+        if (!EXACT) P = decay(S * Al);
+        Ops::scan_up(P, H);
+        const float g0 = c > 0 ? carry[N + s] : 0.0f;
+        const float P0 = c > 0 ? carry[s] : 1.0f;
+        const float gend = fmaf(P, g0, H);
+        float g = Ops::prev(gend, g0);
+        if (!EXACT) {
+          const int sn = s + 1 < N ? s + 1 : s;
+          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(sn * kTabStride * 4);
+#pragma unroll
+          for (int r = 0; r < R; ++r) avn[r] = tab(sT, row, tb[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          g = fmaf(av[r], g, du2[r]);
+          acc[r] = fmaf(g, wbc, acc[r]);
+        }
+        if (j == G - 1 && c < nch) {
+          const float Pn = P0 * P;
+          carry[s] = Pn;
+          carry[N + s] = gend;
+          if (c < nck) reinterpret_cast<float2*>(a.x + (ch * nck + c) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
+        }
+      };
       auto states = [&](auto exact_tag) {
         constexpr bool EXACT = decltype(exact_tag)::value;
+        float av0[R], av1[R];
+        if (!EXACT) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) av0[r] = tab(sT, 0u, tb[r]);
+        }
 #pragma unroll 1
-        for (int s = 0; s < N; ++s) {
-          const float Al = sAl[s], wbc = sWBC[s];
-          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(s * kTabStride * 4);
-          float av[R];
-          float P = 1.0f, H = 0.0f;
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            av[r] = EXACT ? decay(dl[r] * Al) : tab(sT, row, tb[r]);
-            H = fmaf(av[r], H, du2[r]);
-            if (EXACT) P *= av[r];
-          }
-          if (!EXACT) P = decay(S * Al);
-          Ops::scan_up(P, H);
-          const float g0 = c > 0 ? carry[N + s] : 0.0f;
-          const float P0 = c > 0 ? carry[s] : 1.0f;
-          const float gend = fmaf(P, g0, H);
-          float g = Ops::prev(gend, g0);
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            g = fmaf(av[r], g, du2[r]);
-            acc[r] = fmaf(g, wbc, acc[r]);
-          }
-          if (j == G - 1 && c < nch) {
-            const float Pn = P0 * P;
-            carry[s] = Pn;
-            carry[N + s] = gend;
-            if (c < nck)
-              reinterpret_cast<float2*>(a.x + (ch * nck + c) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
-          }
+        for (int s = 0; s < N; s += 2) {
+          state(s, av0, av1, exact_tag);
+          if (s + 1 < N) state(s + 1, av1, av0, exact_tag);
         }
       };
       if constexpr (TBL) {
