@@ -732,6 +732,8 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
   const int want = a.max_seqlen > 0 ? (a.max_seqlen + 2047) / 2048 : 1;
   if (a.n_chunks != want) return set_error(BCM_EINVAL, "%s: n_chunks must equal max(1, ceil(max_seqlen/2048))", fn);
   if (a.n_events < 0 || a.n_events > INT32_MAX) return set_error(BCM_EINVAL, "%s: n_events out of range", fn);
+  // per-event arrays are addressed with 32-bit buffer offsets
+  if (a.n_events * 4 > INT32_MAX) return set_error(BCM_EINVAL, "%s: per-event arrays must be below 2 GiB", fn);
   if (!a.cu_seqlens || !a.dt_idle || !a.dt_active || !a.A || !a.W_B || !a.W_C)
     return set_error(BCM_EINVAL, "%s: null input pointer", fn);
   if (a.n_events > 0 && (!a.u || !a.k)) return set_error(BCM_EINVAL, "%s: null u/k pointer", fn);
