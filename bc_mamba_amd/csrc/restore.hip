@@ -69,7 +69,10 @@ struct TileWave {
 // and flagged !ok.
 __device__ __forceinline__ TileWave tile_wave(int nT, int nG, int dim, const int32_t* tile_start) {
   TileWave w;
-  const int wid = xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  // wave-uniform by construction; readfirstlane lets the compiler keep it (and
+  // the buffer descriptors built from it) in SGPRs
+  const int wid = __builtin_amdgcn_readfirstlane(xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
+                                                 (int)(threadIdx.x / kWave));
   w.g = wid % nG;
   const int bj = wid / nG;
   w.j = bj % nT;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
 // first event; tail: from the last event to the tile end) go to per-tile
 // side arrays [nT][n_rows] for the fix-up pass.
 template <typename TI>
-__global__ __launch_bounds__(256) void k_restore_bwd_tiles(const TI* __restrict__ dout, int64_t n_events,
+__global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restrict__ dout, int64_t n_events,
                                                            const uint32_t* __restrict__ bitmask, int64_t W,
                                                            int64_t mrd, const int32_t* __restrict__ tile_start,
                                                            int nT, int nG, int waves, int dim, int64_t L,
@@ -150,20 +153,23 @@ __global__ __launch_bounds__(256) void k_restore_bwd_tiles(const TI* __restrict_
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
   const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
+  // sum: the open run; hsum: the steps before the tile's first event (the
+  // whole tile when it has none), kept as a running value
   float sum = 0.0f, hsum = 0.0f;
   uint32_t r = 0;                                // events seen so far in the tile
   const uint32_t ebase = (uint32_t)(elo - e_base);
+  const int first = m ? __builtin_ctzll(m) : kTile;  // step of the tile's first event
 #pragma unroll
   for (int s = 0; s < kTile; ++s) {
     const uint32_t bit = (uint32_t)(m >> s) & 1u;
     // the run of event (elo + r - 1) closes here when r >= 1
     buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
-    hsum = (bit && r == 0) ? sum : hsum;
     r += bit;
     sum = (bit ? 0.0f : sum) + gv[s];
+    hsum += s < first ? gv[s] : 0.0f;
   }
   if (w.ok) {
-    head[(int64_t)w.j * n_rows + w.ch] = r ? hsum : sum;
+    head[(int64_t)w.j * n_rows + w.ch] = hsum;
     tail[(int64_t)w.j * n_rows + w.ch] = sum;
   }
 }
