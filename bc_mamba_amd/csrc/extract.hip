@@ -87,44 +87,67 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
 
 // ------------------------------------------------------------------- scan
 // One block: exclusive offsets of the per-row counts, total and maximum.
+// Inclusive prefix sum over the 64 lanes: DPP row scans, then the row
+// totals (lanes 15, 31, 47) read as scalars. No LDS round trips.
+__device__ __forceinline__ int wave_incl_sum_dpp(int v) {
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1, zero fill
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31);
+  const int t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+}
+
+// cu[0] = 0, cu[i+1] = counts[0] + ... + counts[i]; meta = (total, max).
+// One workgroup: 8 counts per thread (two 16-byte loads), DPP wave scans,
+// one barrier per 8192 counts.
+template <bool VEC>
 __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict__ counts, int64_t n,
                                                       int32_t* __restrict__ cu, int32_t* __restrict__ meta) {
   constexpr int ITEMS = 8;
-  __shared__ int s_wsum[16];
+  __shared__ int s_wsum[2][16];
   __shared__ int s_wmax[16];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
   const int nw = blockDim.x / kWave;
-  int carry = 0, mx = 0;
-  for (int64_t base = 0; base < n; base += (int64_t)blockDim.x * ITEMS) {
+  int carry = 0, mx = 0, par = 0;
+  for (int64_t base = 0; base < n; base += (int64_t)blockDim.x * ITEMS, par ^= 1) {
+    const int64_t i0 = base + (int64_t)tid * ITEMS;
     int v[ITEMS];
-    int s = 0;
+    if (VEC && i0 + ITEMS <= n) {
+      const int4 a = *reinterpret_cast<const int4*>(counts + i0);
+      const int4 b = *reinterpret_cast<const int4*>(counts + i0 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) v[i] = i0 + i < n ? counts[i0 + i] : 0;
+    }
+    int sum = 0;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int64_t idx = base + (int64_t)tid * ITEMS + i;
-      v[i] = idx < n ? counts[idx] : 0;
-      s += v[i];
+      sum += v[i];
       mx = max(mx, v[i]);
     }
-    const int incl = wave_incl_sum(s);
-    if (lane == kWave - 1) s_wsum[wave] = incl;
+    const int incl = wave_incl_sum_dpp(sum);
+    if (lane == kWave - 1) s_wsum[par][wave] = incl;  // double-buffered: one barrier per pass
     __syncthreads();
     int woff = 0, total = 0;
     for (int w = 0; w < nw; ++w) {
-      const int x = s_wsum[w];
-      if (w < wave) woff += x;
+      const int x = s_wsum[par][w];
+      woff += w < wave ? x : 0;
       total += x;
     }
-    __syncthreads();
-    int run = carry + woff + incl - s;
+    int run = carry + woff + incl - sum;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       run += v[i];
-      const int64_t idx = base + (int64_t)tid * ITEMS + i;
-      if (idx < n) cu[idx + 1] = run;
+      if (i0 + i < n) cu[i0 + i + 1] = run;
     }
     carry += total;
   }
-  mx = wave_max(mx);
+  mx = wave_max_dpp(mx);
   if (lane == 0) s_wmax[wave] = mx;
   __syncthreads();
   if (tid == 0) {
@@ -374,7 +397,10 @@ int bcm_extract_scan(const int32_t* counts, int64_t n_rows, int32_t* cu_seqlens,
   const char* fn = "bcm_extract_scan";
   if (n_rows < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
   if (!cu_seqlens || !meta || (n_rows > 0 && !counts)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
-  hipLaunchKernelGGL(k_scan_counts, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
+  if (aligned(counts, 16))
+    hipLaunchKernelGGL(k_scan_counts<true>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
+  else
+    hipLaunchKernelGGL(k_scan_counts<false>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
   return check_launch(fn);
 }
 

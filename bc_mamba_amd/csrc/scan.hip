@@ -57,7 +57,7 @@ struct FwdLds {
   int N, nw, G, R, nslots;
   bool tbl;
   int64_t bytes() const {
-    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 3ll * N + (int64_t)nw * kWave * (R + 1) +
+    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 3ll * N + 2ll * nw * kWave * (R + 1) +
                   (int64_t)nslots * 2 * N);
   }
 };
@@ -194,6 +194,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int C = G * R;
+  constexpr int HR = R / 2;  // items per half chain
+  static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
   const int d = blockIdx.x;
@@ -208,21 +210,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   float* sAl = sT + (TBL ? N * kTabStride : 0);
   float* sWB = sAl + N;
   float* sWBC = sWB + N;
-  float* tile = sWBC + N + wave * (kWave * (R + 1)) + grp * (G * (R + 1));  // the group's staging tile
-  float* mine = tile + j * (R + 1);                                         // this lane's R items
-  float* carry = sWBC + N + nw * kWave * (R + 1) + slot * 2 * N;            // [P_run(N), g_run(N)]
-
-  const float dti = a.dt_idle[d], dta = a.dt_active[d];
-  const float Dv = a.D ? a.D[d] : 0.0f;
-  for (int s = threadIdx.x; s < N; s += blockDim.x) {
-    const float wb = a.W_B[(int64_t)d * N + s];
-    sAl[s] = a.A[(int64_t)d * N + s] * kLog2e;
-    sWB[s] = wb;
-    sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
-  }
-  if (TBL) build_decay_table(sT, a, d, dti, dta);
-  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
-  (void)nslots;
+  // the group's staging tiles for u and k (the u tile also stages y)
+  float* tile = sWBC + N + wave * (kWave * (R + 1)) + grp * (G * (R + 1));
+  float* tilek = tile + nw * kWave * (R + 1);
+  float* mine = tile + j * (R + 1);  // this lane's R items
+  float* minek = tilek + j * (R + 1);
+  float* carry = sWBC + N + 2 * nw * kWave * (R + 1) + slot * 2 * N;  // [P_run(N), g_run(N)]
 
   // per-event arrays as buffer resources: items past a channel's events use
   // an out-of-range offset (loads read 0, stores are dropped)
@@ -233,54 +226,90 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
 
+  // Chunk loads, row by row (item q*G + j in step q, coalesced), written
+  // into the tiles at their transposed positions (positions recomputed per
+  // call: opaque() keeps them from being hoisted and held in registers). The
+  // first chunk's loads are issued before the parameter set-up so their
+  // latency overlaps it.
+  float rawu[R];
+  int rawk[R];
+  auto issue = [&](int e0, int n, int c) {
+    const int cnt = min(max(n - c * C, 0), C);
+    const uint32_t eb = (uint32_t)(e0 + c * C);
+    const int jo = opaque(j);
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int idx = q * G + jo;
+      rawu[q] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
+      rawk[q] = buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB);
+    }
+  };
+  auto to_tiles = [&]() {
+    const int jo = opaque(j);
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      tile[tile_pos<R>(q * G + jo)] = rawu[q];
+      tilek[tile_pos<R>(q * G + jo)] = __int_as_float(rawk[q]);
+    }
+  };
+  auto channel = [&](int b, int& e0, int& n) {
+    const bool act = b < n_per_d;
+    const int64_t ch = (int64_t)d + (int64_t)b * dim;
+    e0 = act ? a.cu_seqlens[ch] : 0;
+    n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
+  };
+  int e0, n;
+  channel(slot, e0, n);
+  if (n_per_d > 0) issue(e0, n, 0);
+
+  const float dti = a.dt_idle[d], dta = a.dt_active[d];
+  const float Dv = a.D ? a.D[d] : 0.0f;
+  for (int s = threadIdx.x; s < N; s += blockDim.x) {
+    const float wb = a.W_B[(int64_t)d * N + s];
+    sAl[s] = a.A[(int64_t)d * N + s] * kLog2e;
+    sWB[s] = wb;
+    sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
+  }
+  if (TBL) build_decay_table(sT, a, d, dti, dta);
+  if (n_per_d > 0) to_tiles();
+  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
+  (void)nslots;
+
   for (int b0 = 0; b0 < n_per_d; b0 += nw * CPW) {
     const int b = b0 + slot;
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    const int e0 = act ? a.cu_seqlens[ch] : 0;
-    const int n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
+    if (b0 > 0) channel(b, e0, n);
     const int nch = n > 0 ? (n + C - 1) / C : 0;
     const int wmax = wave_max_dpp(nch);
     for (int c = 0; c < wmax; ++c) {
       const int cnt = min(max(n - c * C, 0), C);
       const int nv = cnt - j * R;                 // events among this lane's R items
       const uint32_t eb = (uint32_t)(e0 + c * C);  // event index of the chunk's first item
-      // ---- stage u, then k (positions recomputed per chunk: opaque() keeps
-      // them from being hoisted and held in registers across chunks)
-      float uu[R];
-      {
-        const int jo = opaque(j);
-#pragma unroll
-        for (int q = 0; q < R; ++q) {
-          const int idx = q * G + jo;
-          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
-        }
-        wave_sync();
-#pragma unroll
-        for (int r = 0; r < R; ++r) uu[r] = mine[r];
-        wave_sync();
-#pragma unroll
-        for (int q = 0; q < R; ++q) {
-          const int idx = q * G + jo;
-          tile[tile_pos<R>(idx)] = __int_as_float(buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB));
-        }
-        wave_sync();
+      if (b0 > 0 || c > 0) {
+        issue(e0, n, c);
+        to_tiles();
       }
+      wave_sync();
+      float uu[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) uu[r] = mine[r];
       float dl[R], du2[R], acc[R];
       uint32_t tb[R];  // byte offset of the item's gap in a table row (0: padding)
       int big = 0;
-      float S = 0.0f;
+      float Sa = 0.0f, Sb = 0.0f;  // Σ Δ of each half chain
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const bool valid = r < nv;
-        const int kk = __float_as_int(mine[r]);
+        const int kk = __float_as_int(minek[r]);
         // padding items are identities of the scan: Δ = 0 -> a = 1, Δu² = 0
         const int km1 = valid ? kk - 1 : -1;
         dl[r] = valid ? fmaf(dti, (float)km1, dta) : 0.0f;
         du2[r] = dl[r] * uu[r] * uu[r];
         tb[r] = (uint32_t)(km1 + 1) * 4u;
         big |= km1 >= kTabK ? 1 : 0;
-        S += dl[r];
+        if (r < HR) Sa += dl[r];
+        else Sb += dl[r];
         acc[r] = 0.0f;
       }
       // ---- state loop. EXACT: decays computed per item, products multiplied
@@ -289,29 +318,45 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
       auto state = [&](int s, float (&av)[R], float (&avn)[R], auto exact_tag) {
         constexpr bool EXACT = decltype(exact_tag)::value;
         const float Al = sAl[s], wbc = sWBC[s];
-        float P = 1.0f, H = 0.0f;
+        // two independent half chains (items 0..HR-1 and HR..R-1), interleaved
+        // for instruction-level parallelism and joined with the scan operator
+        float Pa = 1.0f, Ha = 0.0f, Pb = 1.0f, Hb = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (EXACT) av[r] = decay(dl[r] * Al);
-          H = fmaf(av[r], H, du2[r]);
-          if (EXACT) P *= av[r];
+        for (int i = 0; i < HR; ++i) {
+          if (EXACT) {
+            av[i] = decay(dl[i] * Al);
+            av[i + HR] = decay(dl[i + HR] * Al);
+          }
+          Ha = fmaf(av[i], Ha, du2[i]);
+          Hb = fmaf(av[i + HR], Hb, du2[i + HR]);
+          if (EXACT) {
+            Pa *= av[i];
+            Pb *= av[i + HR];
+          }
         }
-        if (!EXACT) P = decay(S * Al);
+        if (!EXACT) {
+          Pa = decay(Sa * Al);
+          Pb = decay(Sb * Al);
+        }
+        float P = Pa * Pb, H = fmaf(Pb, Ha, Hb);
         Ops::scan_up(P, H);
         const float g0 = c > 0 ? carry[N + s] : 0.0f;
         const float P0 = c > 0 ? carry[s] : 1.0f;
         const float gend = fmaf(P, g0, H);
-        float g = Ops::prev(gend, g0);
+        const float gin = Ops::prev(gend, g0);
         if (!EXACT) {
           const int sn = s + 1 < N ? s + 1 : s;
           const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(sn * kTabStride * 4);
 #pragma unroll
           for (int r = 0; r < R; ++r) avn[r] = tab(sT, row, tb[r]);
         }
+        float ga = gin, gb = fmaf(Pa, gin, Ha);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          g = fmaf(av[r], g, du2[r]);
-          acc[r] = fmaf(g, wbc, acc[r]);
+        for (int i = 0; i < HR; ++i) {
+          ga = fmaf(av[i], ga, du2[i]);
+          gb = fmaf(av[i + HR], gb, du2[i + HR]);
+          acc[i] = fmaf(ga, wbc, acc[i]);
+          acc[i + HR] = fmaf(gb, wbc, acc[i + HR]);
         }
         if (j == G - 1 && c < nch) {
           const float Pn = P0 * P;
@@ -374,6 +419,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   constexpr int CPW = kWave / G;
   constexpr int RS = R + 1;
   constexpr int C = G * R;
+  constexpr int HR = R / 2;  // items per half chain
+  static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
   const int d = blockIdx.x;
@@ -397,13 +444,61 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   // k-1 (0 for padding)
   float* tile = sA + N + wave * (kWave * RS) + grp * (G * RS);
   float* gg = tile + j * RS;
-  float* gkm = sA + N + nw * kWave * RS + threadIdx.x * RS;
+  float* tilek = tile + nw * kWave * RS;  // the k tile; then k-1 per lane
+  float* gkm = tilek + j * RS;
   float* sdx = sA + N + 2 * nw * kWave * RS;  // [nslots][N] a·e carried to the previous chunk
   float* sg0 = sdx + nslots * N;              // [nslots][N] g at the chunk start
   float* sacc = sg0 + nslots * N;             // [nslots][NA]
   float* cdx = sdx + slot * N;
   float* cg0 = sg0 + slot * N;
   float* cacc = sacc + slot * NA;
+
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
+  const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
+  const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
+  const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
+
+  // Chunk loads, row by row (item q*G + j in step q, coalesced): k and u go
+  // to their tiles at the transposed positions (opaque(): positions are not
+  // hoisted and held in registers); they are issued one chunk ahead (the
+  // first before the parameter set-up, the next after a chunk's last use of
+  // the tiles), so their latency overlaps other work. dout is loaded at the
+  // top of its chunk and goes through the u tile once u has been read.
+  float rawu[R];
+  int rawk[R];
+  auto issue = [&](int e0, int n, int c) {
+    const int cnt = min(max(n - c * C, 0), C);
+    const uint32_t eb = (uint32_t)(e0 + c * C);
+    const int jo = opaque(j);
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      const int idx = q * G + jo;
+      rawk[q] = buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB);
+      rawu[q] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
+    }
+  };
+  auto to_tiles = [&]() {
+    const int jo = opaque(j);
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+      tilek[tile_pos<R>(q * G + jo)] = __int_as_float(rawk[q]);
+      tile[tile_pos<R>(q * G + jo)] = rawu[q];
+    }
+  };
+  auto channel = [&](int b, int& e0, int& n) {
+    const bool act = b < n_per_d;
+    const int64_t ch = (int64_t)d + (int64_t)b * dim;
+    e0 = act ? a.cu_seqlens[ch] : 0;
+    n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
+  };
+  int e0, n;
+  channel(slot, e0, n);
+  int nch = n > 0 ? (n + C - 1) / C : 0;
+  int wmax = wave_max_dpp(nch);
+  if (n_per_d > 0 && wmax > 0) issue(e0, n, wmax - 1);
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
@@ -419,24 +514,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   }
   for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   if (TBL) build_decay_table(sT, a, d, dti, dta);
+  if (n_per_d > 0 && wmax > 0) to_tiles();
   const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
-
-  const int64_t E = a.n_events;
-  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
-  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
-  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
-  const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
-  const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
-  const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
 
   for (int b0 = 0; b0 < n_per_d; b0 += nslots) {
     const int b = b0 + slot;
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    const int e0 = act ? a.cu_seqlens[ch] : 0;
-    const int n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
-    const int nch = n > 0 ? (n + C - 1) / C : 0;
-    const int wmax = wave_max_dpp(nch);
+    // e0, n, nch, wmax describe this channel, and the loads of its last
+    // chunk are in the tiles and rawd: issued before the loop or at the end
+    // of the previous channel, so raw registers never span a state loop
     float ddti_l = 0.0f, ddta_l = 0.0f, dD_l = 0.0f;
     for (int c = wmax - 1; c >= 0; --c) {
       const bool cact = c < nch;
@@ -454,44 +541,38 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       float du2[R], doutu[R], acc1[R], acc2[R];
       uint32_t tb[R];  // byte offset of the item's gap k in a table row (4k; 0: padding)
       int big = 0;
-      float S = 0.0f, dl0 = 0.0f;
+      float Sa = 0.0f, Sb = 0.0f, dl0 = 0.0f, dlh = 0.0f;
       {
-        // ---- stage k, u and the gated dout through the tile (dz on the way);
-        // positions recomputed per chunk (opaque: not hoisted across chunks)
+        // ---- k (-> k-1 in place) and u from their tiles, then the gated
+        // dout through the u tile (dz on the way)
         const int jo = opaque(j);
-        float dlv[R], uvv[R];
+        float dlv[R], uvv[R], rawd[R];
 #pragma unroll
         for (int q = 0; q < R; ++q) {
           const int idx = q * G + jo;
-          tile[tile_pos<R>(idx)] = __int_as_float(buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB));
+          rawd[q] = buf_load<T>(rdo, idx < cnt ? (eb + idx) * SZ : kBufOOB);
         }
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const bool valid = r < nv;
-          const int kk = __float_as_int(gg[r]);
+          const int kk = __float_as_int(gkm[r]);
           tb[r] = valid ? (uint32_t)kk * 4u : 0u;
           dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
           gkm[r] = valid ? (float)(kk - 1) : 0.0f;
           big |= (valid && kk > kTabK) ? 1 : 0;
-          S += dlv[r];
+          if (r < HR) Sa += dlv[r];
+          else Sb += dlv[r];
+          uvv[r] = gg[r];
         }
         dl0 = dlv[0];
-        wave_sync();
-#pragma unroll
-        for (int q = 0; q < R; ++q) {
-          const int idx = q * G + jo;
-          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
-        }
-        wave_sync();
-#pragma unroll
-        for (int r = 0; r < R; ++r) uvv[r] = gg[r];
+        dlh = dlv[HR];
         wave_sync();
 #pragma unroll
         for (int q = 0; q < R; ++q) {
           const int idx = q * G + jo;
           const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
-          float dv = buf_load<T>(rdo, off);
+          float dv = rawd[q];
           if (HAS_Z) {
             const float zv = buf_load<T>(rz, off);
             const float ov = buf_load<T>(ros, off);
@@ -511,9 +592,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
         }
         wave_sync();  // the tile becomes the states g of the state loop
       }
-      // Σ Δ over the items that follow each of the lane's items (the next
-      // lane's first; nothing past the chunk: its carry already holds a·e)
-      const float S1 = S - dl0 + Ops::next(dl0, 0.0f);
+      // Σ Δ over each half chain's items, and over the items that follow
+      // them (the next lane's first; nothing past the chunk: its carry
+      // already holds a·e)
+      const float S1a = Sa - dl0 + dlh;
+      const float S1b = Sb - dlh + Ops::next(dl0, 0.0f);
       // the state loop reads gkm through an index the compiler cannot see
       // through, so it re-reads LDS instead of keeping the stored values live
       const float* km = gkm + opaque(0);
@@ -528,55 +611,100 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           const float g0 = c > 0 ? cg0[s] : 0.0f;
           const float ec = (c < nch - 1) ? cdx[s] : 0.0f;
           float av[R];
-          // forward: local fold, group scan, exact states (kept in LDS)
-          float P = 1.0f, H = 0.0f;
+          // Each lane's R items run as two independent half chains (items
+          // 0..HR-1 and HR..R-1), interleaved for instruction-level
+          // parallelism and joined with the scan operator.
+          // forward: local folds, group scan, exact states (kept in LDS)
+          float Pa = 1.0f, Ha = 0.0f, Pb = 1.0f, Hb = 0.0f;
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            av[r] = EXACT ? decay((tb[r] ? fmaf(dti, km[r], dta) : 0.0f) * Al) : tab(sT, row, tb[r]);
-            H = fmaf(av[r], H, du2[r]);
-            if (EXACT) P *= av[r];
+          for (int i = 0; i < HR; ++i) {
+            const int ra = i, rb = i + HR;
+            if (EXACT) {
+              av[ra] = decay((tb[ra] ? fmaf(dti, km[ra], dta) : 0.0f) * Al);
+              av[rb] = decay((tb[rb] ? fmaf(dti, km[rb], dta) : 0.0f) * Al);
+            } else {
+              av[ra] = tab(sT, row, tb[ra]);
+              av[rb] = tab(sT, row, tb[rb]);
+            }
+            Ha = fmaf(av[ra], Ha, du2[ra]);
+            Hb = fmaf(av[rb], Hb, du2[rb]);
+            if (EXACT) {
+              Pa *= av[ra];
+              Pb *= av[rb];
+            }
           }
-          if (!EXACT) P = decay(S * Al);
+          if (!EXACT) {
+            Pa = decay(Sa * Al);
+            Pb = decay(Sb * Al);
+          }
+          float P = Pa * Pb, H = fmaf(Pb, Ha, Hb);
           Ops::scan_up(P, H);
           const float gin = Ops::prev(fmaf(P, g0, H), g0);
           {
-            float g = gin;
+            float ga = gin, gb = fmaf(Pa, gin, Ha);
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-              g = fmaf(av[r], g, du2[r]);
-              gg[r] = g;
+            for (int i = 0; i < HR; ++i) {
+              ga = fmaf(av[i], ga, du2[i]);
+              gb = fmaf(av[i + HR], gb, du2[i + HR]);
+              gg[i] = ga;
+              gg[i + HR] = gb;
             }
           }
           // reverse: e_i = dout_i·u_i + a_{i+1}·e_{i+1}   (dx = W_C·e)
           const float anext = Ops::next(av[0], 1.0f);  // the chunk carry already holds a_next·e_next
-          float Q = 1.0f, Ce = 0.0f;
+          float Qa = 1.0f, Cea = 0.0f, Qb = 1.0f, Ceb = 0.0f;
 #pragma unroll
-          for (int r = R - 1; r >= 0; --r) {
-            const float al = (r == R - 1) ? anext : av[r + 1];
-            Ce = fmaf(al, Ce, doutu[r]);
-            if (EXACT) Q *= al;
+          for (int i = 0; i < HR; ++i) {
+            const int ra = HR - 1 - i, rb = R - 1 - i;
+            const float ala = av[ra + 1];
+            const float alb = (rb == R - 1) ? anext : av[rb + 1];
+            Cea = fmaf(ala, Cea, doutu[ra]);
+            Ceb = fmaf(alb, Ceb, doutu[rb]);
+            if (EXACT) {
+              Qa *= ala;
+              Qb *= alb;
+            }
           }
-          if (!EXACT) Q = decay(S1 * Al);
+          if (!EXACT) {
+            Qa = decay(S1a * Al);
+            Qb = decay(S1b * Al);
+          }
+          float Q = Qa * Qb, Ce = fmaf(Qa, Ceb, Cea);
           Ops::scan_down(Q, Ce);
-          float e = Ops::next(fmaf(Q, ec, Ce), ec);
+          const float ein = Ops::next(fmaf(Q, ec, Ce), ec);
+          float eb = ein, ea = fmaf(Qb, ein, Ceb);  // ea starts from e at item HR
           // tg = dx·a·h_prev / (W_B·W_C); with Δ = dt_idle·(k-1) + dt_active the
           // Δ-weighted sums need only T0 = Σ tg and T1 = Σ tg·(k-1)
-          float T0 = 0.0f, T1 = 0.0f, dWB_l = 0.0f, dWC_l = 0.0f;
+          float T0a = 0.0f, T1a = 0.0f, dWBa = 0.0f, dWCa = 0.0f;
+          float T0b = 0.0f, T1b = 0.0f, dWBb = 0.0f, dWCb = 0.0f;
 #pragma unroll
-          for (int r = R - 1; r >= 0; --r) {
-            if (r % kSchedBlock == kSchedBlock - 1) __builtin_amdgcn_sched_barrier(0);
-            const float al = (r == R - 1) ? anext : av[r + 1];
-            const float gr = gg[r];
-            const float gp = r > 0 ? gg[r - 1] : gin;
-            e = fmaf(al, e, doutu[r]);
-            acc1[r] = fmaf(e, wbc, acc1[r]);       // Σ_s dx·W_B
-            acc2[r] = fmaf(gr, wbc, acc2[r]);      // Σ_s h·W_C
-            const float tg = e * (av[r] * gp);
-            T0 += tg;
-            T1 = fmaf(tg, km[r], T1);
-            dWB_l = fmaf(e, du2[r], dWB_l);
-            dWC_l = fmaf(doutu[r], gr, dWC_l);
+          for (int i = 0; i < HR; ++i) {
+            const int ra = HR - 1 - i, rb = R - 1 - i;
+            const float ala = av[ra + 1];
+            const float alb = (rb == R - 1) ? anext : av[rb + 1];
+            const float gra = gg[ra], grb = gg[rb];
+            const float gpa = ra > 0 ? gg[ra - 1] : gin;
+            const float gpb = gg[rb - 1];
+            ea = fmaf(ala, ea, doutu[ra]);
+            eb = fmaf(alb, eb, doutu[rb]);
+            acc1[ra] = fmaf(ea, wbc, acc1[ra]);       // Σ_s dx·W_B
+            acc1[rb] = fmaf(eb, wbc, acc1[rb]);
+            acc2[ra] = fmaf(gra, wbc, acc2[ra]);      // Σ_s h·W_C
+            acc2[rb] = fmaf(grb, wbc, acc2[rb]);
+            const float tga = ea * (av[ra] * gpa);
+            const float tgb = eb * (av[rb] * gpb);
+            T0a += tga;
+            T0b += tgb;
+            T1a = fmaf(tga, km[ra], T1a);
+            T1b = fmaf(tgb, km[rb], T1b);
+            dWBa = fmaf(ea, du2[ra], dWBa);
+            dWBb = fmaf(eb, du2[rb], dWBb);
+            dWCa = fmaf(doutu[ra], gra, dWCa);
+            dWCb = fmaf(doutu[rb], grb, dWCb);
           }
+          const float e = ea;  // e of item 0
+          const float T0 = T0a + T0b, T1 = T1a + T1b;
+          float dWB_l = dWBa + dWBb, dWC_l = dWCa + dWCb;
           if (j == 0 && cact) cdx[s] = av[0] * e;
           // dΔ_i gets Σ_s dx·a·h_prev·A: its ddt sums take T0, T1 lane by lane
           ddta_l = fmaf(wbca, T0, ddta_l);
@@ -601,27 +729,26 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       wave_sync();
       {
         const int jo = opaque(j);
-        float uvv[R];
+        float uvv[R], fu[R], fd[R];
 #pragma unroll
-        for (int q = 0; q < R; ++q) {
+        for (int q = 0; q < R; ++q) {  // both loads in flight together
           const int idx = q * G + jo;
-          tile[tile_pos<R>(idx)] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
+          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
+          fu[q] = buf_load<T>(ru, off);
+          fd[q] = buf_load<T>(rdo, off);
+          if (HAS_Z) {
+            const float zv = buf_load<T>(rz, off);
+            fd[q] *= zv / (1.0f + __expf(-zv));
+          }
         }
+#pragma unroll
+        for (int q = 0; q < R; ++q) tile[tile_pos<R>(q * G + jo)] = fu[q];
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) uvv[r] = gg[r];
         wave_sync();
 #pragma unroll
-        for (int q = 0; q < R; ++q) {
-          const int idx = q * G + jo;
-          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
-          float dv = buf_load<T>(rdo, off);
-          if (HAS_Z) {
-            const float zv = buf_load<T>(rz, off);
-            dv *= zv / (1.0f + __expf(-zv));
-          }
-          tile[tile_pos<R>(idx)] = dv;
-        }
+        for (int q = 0; q < R; ++q) tile[tile_pos<R>(q * G + jo)] = fd[q];
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -642,6 +769,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, tile[tile_pos<R>(idx)]);
         }
       }
+      if (c > 0) {  // the previous chunk's loads, now that the tiles are free
+        wave_sync();
+        issue(e0, n, c - 1);
+        to_tiles();
+      }
       wave_sync();  // cdx (LDS) written by lane 0, read by the group in the previous chunk
     }
     ddti_l = Ops::sum(ddti_l);
@@ -651,6 +783,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       cacc[3 * N] += ddti_l;
       cacc[3 * N + 1] += ddta_l;
       cacc[3 * N + 2] += dD_l;
+    }
+    if (b0 + nslots < n_per_d) {  // the next channel of this lane group
+      channel(b + nslots, e0, n);
+      nch = n > 0 ? (n + C - 1) / C : 0;
+      wmax = wave_max_dpp(nch);
+      if (wmax > 0) {
+        wave_sync();
+        issue(e0, n, wmax - 1);
+        to_tiles();
+      }
     }
   }
   __syncthreads();

@@ -2,9 +2,10 @@
 
 One step = one fwd+bwd pass of the whole path over the config's synthetic
 batch, inputs resident in HBM:
-  forward : extract (count -> offsets -> host read of E -> fill, with x_conv
-            gathered at the events and the event index built in the same
-            pass) -> flat selective scan -> zero-order-hold restore
+  forward : extract (count -> offsets -> fill, with x_conv gathered at the
+            events and the event index built in the same pass; the host
+            reads E while fill runs) -> flat selective scan ->
+            zero-order-hold restore
   backward: restore backward -> selective scan backward -> gather backward
 All stages run in libbcm_event_scan.so on torch's current stream. Prints one
 JSON line (metric / value / roofline / cpu_baseline ...).
@@ -52,7 +53,12 @@ def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
 
 
 class Path:
-    """The fwd+bwd path driven through the C ABI with reusable buffers."""
+    """The fwd+bwd path driven through the C ABI with reusable buffers.
+
+    Event buffers are sized for the largest possible event count (every
+    step of every channel), so the fill kernel can be enqueued before the
+    host has read E: the host waits on an event recorded after the offsets
+    kernel while fill runs, and the GPU never idles on the round trip."""
 
     KERNELS = ["count", "offsets", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd", "gather_bwd"]
 
@@ -68,32 +74,29 @@ class Path:
         self.cu = torch.empty(self.NC + 1, **i32)
         self.meta = torch.empty(2, **i32)
         self.meta_h = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        self.meta_ev = torch.cuda.Event()
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
         self.ws = torch.empty(2 * self.NC * nat.tile_count(L), dtype=torch.float32, device=dev)
-        self.E = -1
+        cap = self.NC * L  # upper bound of E
+        self.ch, self.ts, self.k = (torch.empty(cap, **i32) for _ in range(3))
+        self.u = torch.empty(cap, dtype=w.dtype, device=dev)
+        self.y = torch.empty(cap, dtype=w.dtype, device=dev)
+        self.dy32 = torch.empty(cap, dtype=torch.float32, device=dev)
+        self.dy = self.dy32 if w.dtype == torch.float32 else torch.empty(cap, dtype=w.dtype, device=dev)
+        self.du = torch.empty(cap, dtype=w.dtype, device=dev)
+        self.x = torch.empty((self.NC, max(1, -(-L // 2048)), 2 * w.N), dtype=torch.float32, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.grads = [torch.empty((w.D, w.N), **f32) for _ in range(3)] + [torch.empty(w.D, **f32) for _ in range(3)]
+        self.args = self._scan_args()
+        self.E = self.ms = -1
         self.events = {}
-
-    def _alloc(self, E, ms):
-        t, dev, w = self.t, self.dev, self.w
-        i32 = dict(dtype=t.int32, device=dev)
-        self.E, self.ms = E, ms
-        self.ch, self.ts, self.k = (t.empty(E, **i32) for _ in range(3))
-        self.u = t.empty(E, dtype=w.dtype, device=dev)
-        self.y = t.empty(E, dtype=w.dtype, device=dev)
-        self.dy32 = t.empty(E, dtype=t.float32, device=dev)
-        self.du = t.empty(E, dtype=w.dtype, device=dev)
-        self.n_chunks = max(1, -(-ms // 2048))
-        self.x = t.empty((self.NC, self.n_chunks, 2 * w.N), dtype=t.float32, device=dev)
-        f32 = dict(dtype=t.float32, device=dev)
-        self.grads = [t.empty((w.D, w.N), **f32) for _ in range(3)] + [t.empty(w.D, **f32) for _ in range(3)]
 
     def _scan_args(self):
         nat, w = self.nat, self.w
         a = nat.ScanArgs()
-        a.n_events, a.n_channels, a.dim, a.dstate = self.E, self.NC, w.D, w.N
-        a.max_seqlen, a.n_chunks, a.dtype = self.ms, self.n_chunks, nat.dtype_code(w.dtype)
+        a.n_channels, a.dim, a.dstate, a.dtype = self.NC, w.D, w.N, nat.dtype_code(w.dtype)
         a.u, a.k, a.cu_seqlens = self.u.data_ptr(), self.k.data_ptr(), self.cu.data_ptr()
         a.dt_idle, a.dt_active = w.dt_idle.data_ptr(), w.dt_active.data_ptr()
         a.A, a.W_B, a.W_C, a.D = w.A.data_ptr(), w.W_B.data_ptr(), w.W_C.data_ptr(), w.D_skip.data_ptr()
@@ -124,15 +127,16 @@ class Path:
                                        self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), s))
         mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta), s))
         self.meta_h.copy_(self.meta, non_blocking=True)
-        t.cuda.current_stream().synchronize()
-        E, ms = int(self.meta_h[0]), int(self.meta_h[1])
-        if E != self.E or ms != getattr(self, "ms", -1):
-            self._alloc(E, ms)
-            self.dy = self.dy32 if w.dtype == t.float32 else t.empty(E, dtype=w.dtype, device=self.dev)
-            self.args = self._scan_args()
+        self.meta_ev.record()
         mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
                                       nat.dtype_code(w.dtype), P(self.ch), P(self.ts), P(self.k), P(self.u),
                                       P(self.tile_start), None, s))
+        self.meta_ev.synchronize()  # E and max_seqlen; fill keeps the GPU busy meanwhile
+        E, ms = int(self.meta_h[0]), int(self.meta_h[1])
+        if E != self.E or ms != self.ms:
+            self.E, self.ms = E, ms
+            a = self.args
+            a.n_events, a.max_seqlen, a.n_chunks = E, ms, max(1, -(-ms // 2048))
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense),
@@ -141,7 +145,7 @@ class Path:
                                              1, P(self.tile_start), self.NC, D, L, P(self.dy32), E, P(self.ws),
                                              4 * self.ws.numel(), s))
         if self.dy is not self.dy32:
-            self.dy.copy_(self.dy32)
+            self.dy[:E].copy_(self.dy32[:E])
         mark("scan_bwd", lambda: nat.call("bcm_scan_bwd", self.args, s))
         mark("gather_bwd", lambda: nat.call("bcm_gather_bwd_rows", P(self.du), nat.dtype_code(w.dtype),
                                             P(self.bitmask), 1, P(self.tile_start), self.NC, L, P(self.dx), s))
