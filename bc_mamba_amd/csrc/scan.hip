@@ -181,12 +181,15 @@ __device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args
   }
 }
 
-// 1 if some decay exponent of workgroup d can be positive (A > 0 or Δ < 0):
-// lane products are then multiplied out exactly. Block-wide vote.
-__device__ __forceinline__ bool exact_products(const bcm_scan_args& a, int d, float dti, float dta) {
-  int f = (dti < 0.0f || dta < 0.0f) ? 1 : 0;
-  for (int s = threadIdx.x; s < a.dstate; s += blockDim.x) f |= a.A[(int64_t)d * a.dstate + s] > 0.0f ? 1 : 0;
-  return __syncthreads_or(f) != 0;
+// Barrier after the LDS set-up, then: true if some decay exponent of
+// workgroup d can be positive (A > 0 or Δ < 0); lane products are then
+// multiplied out exactly. Every thread reads the N values of A·log2e from
+// LDS (same sign as A), so the kernel needs no static LDS for a vote.
+__device__ __forceinline__ bool exact_products(const float* sAl, int N, float dti, float dta) {
+  __syncthreads();
+  bool f = dti < 0.0f || dta < 0.0f;
+  for (int s = 0; s < N; ++s) f |= sAl[s] > 0.0f;
+  return f;
 }
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   }
   if (TBL) build_decay_table(sT, a, d, dti, dta);
   if (n_per_d > 0) to_tiles();
-  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
+  const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
   (void)nslots;
 
   for (int b0 = 0; b0 < n_per_d; b0 += nw * CPW) {
@@ -515,7 +518,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   if (TBL) build_decay_table(sT, a, d, dti, dta);
   if (n_per_d > 0 && wmax > 0) to_tiles();
-  const bool exact_blk = exact_products(a, d, dti, dta);  // also the barrier after the LDS set-up
+  const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
   for (int b0 = 0; b0 < n_per_d; b0 += nslots) {
     const int b = b0 + slot;
@@ -822,7 +825,12 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
   int nw = (per_d + CPW - 1) / CPW;
   nw = nw < 1 ? 1 : (nw > kScanThreads / kWave ? kScanThreads / kWave : nw);
-  const int64_t cap = max_lds_bytes();
+  // the per-workgroup limit covers static and dynamic LDS together
+  hipFuncAttributes fa{};
+  const void* kfn = BWD ? reinterpret_cast<const void*>(&k_scan_bwd<G, R, T, Z, TBL>)
+                        : reinterpret_cast<const void*>(&k_scan_fwd<G, R, T, Z, TBL>);
+  if (hipFuncGetAttributes(&fa, kfn) != hipSuccess) return set_error(BCM_EHIP, "%s: hipFuncGetAttributes failed", fn);
+  const int64_t cap = max_lds_bytes() - (int64_t)fa.sharedSizeBytes;
   int64_t lds = 0;
   for (;;) {
     lds = BWD ? BwdLds{a.dstate, nw, G, R, nw * CPW, TBL}.bytes() : FwdLds{a.dstate, nw, G, R, nw * CPW, TBL}.bytes();

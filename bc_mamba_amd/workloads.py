@@ -63,7 +63,7 @@ def _markov_events(g, NC, L):
     u = torch.rand(NC, L, generator=g)
     ev = torch.empty(NC, L, dtype=torch.bool)
     for t in range(L):
-        stay = torch.where(state, u[:, t] < 0.9, u[:, t] >= 0.98)
+        stay = torch.where(state, u[:, t] < 0.9, u[:, t] < 0.98)
         state = torch.where(stay, state, ~state)
         ev[:, t] = state
     sparse = torch.randperm(NC, generator=g)[: NC // 2]

@@ -84,6 +84,10 @@ SHAPES = [  # B, D, L, density, N  (max_seqlen lands in each kernel-shape bucket
     (2, 4, 700, 0.4, 64),
     (1, 4, 700, 0.4, 65),
     (1, 2, 300, 0.5, 256),
+    # dstate 64 with 8 channels per d and channels of 1024..2048 events: the
+    # widest lane groups, whose LDS use sits at the per-workgroup limit
+    (8, 2, 2600, 0.6, 64),
+    (8, 2, 5000, 0.7, 64),    # and two 2048-event chunks (config-3 scale)
 ]
 
 
