@@ -183,6 +183,19 @@ __device__ __forceinline__ int wave_max_dpp(int v) {
   return max(a, b);
 }
 
+// Inclusive prefix sum over the 64 lanes: DPP row scans, then the row
+// totals (lanes 15, 31, 47) read as scalars. No LDS round trips.
+__device__ __forceinline__ int wave_incl_sum_dpp(int v) {
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1, zero fill
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31);
+  const int t2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
+}
+
 // exp2 of a clamped exponent: the decay of the reference scan
 // (selective_scan_common.h:45-52 clamps Δ·A·log2e to [-126, 126]).
 __device__ __forceinline__ float decay(float e) {

@@ -87,19 +87,6 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
 
 // ------------------------------------------------------------------- scan
 // One block: exclusive offsets of the per-row counts, total and maximum.
-// Inclusive prefix sum over the 64 lanes: DPP row scans, then the row
-// totals (lanes 15, 31, 47) read as scalars. No LDS round trips.
-__device__ __forceinline__ int wave_incl_sum_dpp(int v) {
-  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1, zero fill
-  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
-  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
-  v += (int)__builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
-  const int t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31);
-  const int t2 = __builtin_amdgcn_readlane(v, 47);
-  const int row = lane_id() >> 4;
-  return v + (row >= 1 ? t0 : 0) + (row >= 2 ? t1 : 0) + (row >= 3 ? t2 : 0);
-}
-
 // cu[0] = 0, cu[i+1] = counts[0] + ... + counts[i]; meta = (total, max).
 // One workgroup: 8 counts per thread (two 16-byte loads), DPP wave scans,
 // one barrier per 8192 counts.

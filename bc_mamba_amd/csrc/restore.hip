@@ -126,25 +126,35 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
 }
 
 // Restore backward, tile pass. Runs that start and end inside the tile are
-// final and stored as they close (buffer stores, out-of-range when there is
-// nothing to store). The partial runs at the tile edges (head: before the
-// first event; tail: from the last event to the tile end) go to per-tile
-// side arrays [nT][n_rows] for the fix-up pass.
+// final; the partial runs at the tile edges (head: before the first event;
+// tail: from the last event to the tile end) go to per-tile side arrays
+// [nT][n_rows] for the fix-up pass. The final runs of the wave's 64
+// channels are staged in LDS (value and destination, at a slot from a wave
+// prefix sum of the per-channel run counts) and written out with
+// consecutive lanes on consecutive slots: a channel's runs are consecutive
+// dy entries, so each store instruction covers a few contiguous pieces
+// instead of up to 64 scattered words. Waves with more runs than the
+// staging area store them directly.
+constexpr int kBwdStage = 1024;  // staged runs per wave (about 620 at 15% density)
+
 template <typename TI>
 __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restrict__ dout, int64_t n_events,
-                                                           const uint32_t* __restrict__ bitmask, int64_t W,
-                                                           int64_t mrd, const int32_t* __restrict__ tile_start,
-                                                           int nT, int nG, int waves, int dim, int64_t L,
-                                                           int64_t n_rows, float* __restrict__ dy,
-                                                           float* __restrict__ head, float* __restrict__ tail) {
+                                                              const uint32_t* __restrict__ bitmask, int64_t W,
+                                                              int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                              int nT, int nG, int waves, int dim, int64_t L,
+                                                              int64_t n_rows, float* __restrict__ dy,
+                                                              float* __restrict__ head, float* __restrict__ tail) {
+  __shared__ float s_val[4][kBwdStage + kWave];    // + one discard slot per lane
+  __shared__ uint32_t s_dst[4][kBwdStage + kWave];
   if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  const int wave = threadIdx.x / kWave, lane = lane_id();
   // dout rows of the tile; steps past L and lanes past dim read 0
   const int64_t t0 = (int64_t)w.j * kTile;
   const int steps = (int)(L - t0 < kTile ? L - t0 : kTile);
   const int64_t gbase = ((int64_t)w.b * L + t0) * dim + (int64_t)w.g * kWave;
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + gbase, (n_rows * L - gbase) * (int64_t)sizeof(TI));
-  const uint32_t lane_off = w.ok ? (uint32_t)lane_id() * (uint32_t)sizeof(TI) : kBufOOB;
+  const uint32_t lane_off = w.ok ? (uint32_t)lane * (uint32_t)sizeof(TI) : kBufOOB;
   const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TI);
   float gv[kTile];
 #pragma unroll
@@ -153,6 +163,15 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
   const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
+  // runs closing inside the tile: events - 1 per channel with events
+  const int nrun = m ? __popcll(m) - 1 : 0;
+  const int incl = wave_incl_sum_dpp(nrun);
+  const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+  const bool staged = total <= kBwdStage;  // wave-uniform
+  const uint32_t slot0 = (uint32_t)(incl - nrun);
+  const uint32_t discard = kBwdStage + lane;
+  float* sv = s_val[wave];
+  uint32_t* sd = s_dst[wave];
   // sum: the open run; hsum: the steps before the tile's first event (the
   // whole tile when it has none), kept as a running value
   float sum = 0.0f, hsum = 0.0f;
@@ -163,7 +182,14 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   for (int s = 0; s < kTile; ++s) {
     const uint32_t bit = (uint32_t)(m >> s) & 1u;
     // the run of event (elo + r - 1) closes here when r >= 1
-    buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
+    const bool close = bit && r;
+    if (staged) {
+      const uint32_t slot = close ? slot0 + r - 1 : discard;
+      sv[slot] = sum;
+      sd[slot] = ebase + r - 1;
+    } else {
+      buf_store_f32(rdy, close ? (ebase + r - 1) * 4u : kBufOOB, sum);
+    }
     r += bit;
     sum = (bit ? 0.0f : sum) + gv[s];
     hsum += s < first ? gv[s] : 0.0f;
@@ -171,6 +197,16 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   if (w.ok) {
     head[(int64_t)w.j * n_rows + w.ch] = hsum;
     tail[(int64_t)w.j * n_rows + w.ch] = sum;
+  }
+  if (staged) {
+    wave_sync();
+    for (int k = 0; k < total; k += kWave) {
+      const int i = k + lane;
+      const bool ok = i < total;
+      const float v = sv[ok ? i : discard];
+      const uint32_t dst = sd[ok ? i : discard];
+      buf_store_f32(rdy, ok ? dst * 4u : kBufOOB, v);
+    }
   }
 }
 

@@ -117,14 +117,24 @@ constexpr int kRowShl = 0x100;     // row_shl:n -> lane i reads lane i+n
 constexpr int kRowShr = 0x110;     // row_shr:n -> lane i reads lane i-n
 constexpr int kRowMirror = 0x140;  // lane i reads lane 15-i
 
+// DPP move inside 16-lane rows with zero fill for lanes whose source falls
+// outside the row (lets the compiler fold the move into the consuming op).
+template <int CTRL> __device__ __forceinline__ float dpp_zero(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
 template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are VALU
+  // A lane with no partner gets H += P·0 and P *= 1 (the identities), so
+  // each step can compile to one v_fmac_f32_dpp and one v_mul_f32_dpp.
   template <int O> static __device__ __forceinline__ void up(float& P, float& H) {
-    const float Pp = dpp_mov<kRowShr + O>(P, 1.0f), Hp = dpp_mov<kRowShr + O>(H, 0.0f);
+    const float Hp = dpp_zero<kRowShr + O>(H);
+    const float Pp = dpp_mov<kRowShr + O>(P, 1.0f);
     H = fmaf(P, Hp, H);
     P *= Pp;
   }
   template <int O> static __device__ __forceinline__ void down(float& Q, float& C) {
-    const float Qs = dpp_mov<kRowShl + O>(Q, 1.0f), Cs = dpp_mov<kRowShl + O>(C, 0.0f);
+    const float Cs = dpp_zero<kRowShl + O>(C);
+    const float Qs = dpp_mov<kRowShl + O>(Q, 1.0f);
     C = fmaf(Q, Cs, C);
     Q *= Qs;
   }
