@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
+#include <type_traits>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 #include <stdarg.h>
@@ -133,35 +134,60 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, kBufFlags);
 }
 
-template <typename T> __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
-template <> __device__ __forceinline__ float buf_load<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-template <> __device__ __forceinline__ float buf_load<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0) << 16);
-}
-template <> __device__ __forceinline__ float buf_load<f16>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const unsigned short b = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-  return __half2float(*reinterpret_cast<const f16*>(&b));
+// Cache policy of a buffer access. kStream marks data read or written once
+// (the dense [B, L, D] / [B, D, L] streams): non-temporal, so written lines are
+// not kept dirty in the last-level cache, where their later write-back would
+// compete with the next kernel's traffic, and read lines do not displace the
+// event arrays that one kernel hands to the next.
+constexpr int kKeep = 0;
+constexpr int kStream = 2;  // nt
+
+template <typename T, int POL = kKeep>
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL));
+  } else if constexpr (std::is_same<T, bf16>::value) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL) << 16);
+  } else {
+    const unsigned short b = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL);
+    return __half2float(*reinterpret_cast<const f16*>(&b));
+  }
 }
 
 __device__ __forceinline__ int32_t buf_load_i32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
-__device__ __forceinline__ void buf_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+template <int POL = kKeep> __device__ __forceinline__ void buf_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, POL);
 }
 // Store v converted to T (round to nearest even for the 16-bit types).
-template <typename T> __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+template <typename T, int POL = kKeep>
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
   if constexpr (sizeof(T) == 4) {
-    buf_store_f32(r, off, v);
+    buf_store_f32<POL>(r, off, v);
   } else {
     const T h = from_f<T>(v);
     unsigned short b;
     __builtin_memcpy(&b, &h, 2);
-    __builtin_amdgcn_raw_buffer_store_b16(b, r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(b, r, off, 0, POL);
   }
+}
+
+// Non-temporal (streaming) plain loads and stores of raw bits.
+template <typename V> __device__ __forceinline__ V ld_stream(const V* p) { return __builtin_nontemporal_load(p); }
+template <typename V> __device__ __forceinline__ void st_stream(V v, V* p) { __builtin_nontemporal_store(v, p); }
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// One element of T read with streaming policy (its raw bits).
+template <typename T> __device__ __forceinline__ T ld_stream_elem(const T* p) {
+  using U = typename std::conditional<sizeof(T) == 4, uint32_t,
+                                      typename std::conditional<sizeof(T) == 2, unsigned short, uint8_t>::type>::type;
+  const U b = ld_stream(reinterpret_cast<const U*>(p));
+  T h;
+  __builtin_memcpy(&h, &b, sizeof(T));
+  return h;
 }
 
 // DPP lane permutations inside rows of 16 lanes (VALU, no LDS round trip).

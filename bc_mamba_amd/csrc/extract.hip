@@ -43,7 +43,10 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
     if (VEC && (g0 + BATCH) * GS <= L) {
       uint4 raw[BATCH];
 #pragma unroll
-      for (int i = 0; i < BATCH; ++i) raw[i] = *reinterpret_cast<const uint4*>(xr + (g0 + i) * GS + lane * PER);
+      for (int i = 0; i < BATCH; ++i) {
+        const u32x4 t = ld_stream(reinterpret_cast<const u32x4*>(xr + (g0 + i) * GS + lane * PER));
+        __builtin_memcpy(&raw[i], &t, 16);
+      }
 #pragma unroll
       for (int i = 0; i < BATCH; ++i) {
         const T* v = reinterpret_cast<const T*>(&raw[i]);
@@ -57,7 +60,7 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
         const int64_t t0 = (g0 + i) * GS + (int64_t)lane * PER;
         bits[i] = 0;
         if (VEC && t0 + PER <= L) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(xr + t0);
+          const u32x4 raw = ld_stream(reinterpret_cast<const u32x4*>(xr + t0));
           const T* v = reinterpret_cast<const T*>(&raw);
 #pragma unroll
           for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
         for (int q = 0; q < 4; ++q) {
           const int i = i0 + q * kWave + lane;
           tv[q] = i < seg_cnt ? st[i] : 0;
-          if (GATHER) xv[q] = x[lc * L + tv[q]];
+          if (GATHER) xv[q] = ld_stream_elem(x + lc * L + tv[q]);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -337,8 +340,8 @@ __global__ __launch_bounds__(256) void k_gather_bwd_rows(const T* __restrict__ g
     T o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = from_f<T>(v[i]);
-    if (sizeof(T) == 4) *reinterpret_cast<uint4*>(dr + t0) = *reinterpret_cast<uint4*>(o);
-    else *reinterpret_cast<uint2*>(dr + t0) = *reinterpret_cast<uint2*>(o);
+    if constexpr (sizeof(T) == 4) st_stream(*reinterpret_cast<u32x4*>(o), reinterpret_cast<u32x4*>(dr + t0));
+    else st_stream(*reinterpret_cast<u32x2*>(o), reinterpret_cast<u32x2*>(dr + t0));
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
 #pragma unroll
   for (int s = 0; s < kTile; ++s) {
     val = ((m >> s) & 1ull) ? v[s] : val;
-    buf_store<TO>(ro, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB, val);
+    buf_store<TO, kStream>(ro, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB, val);
   }
 }
 
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TI);
   float gv[kTile];
 #pragma unroll
-  for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
+  for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI, kStream>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
   const int32_t elo = tile_start[(int64_t)w.ch * (nT + 1) + w.j];
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);

@@ -29,14 +29,16 @@ def _empty_i32(n, dev):
     return torch.empty(n, dtype=_I32, device=dev)
 
 
-def _count_scan(x2d, dtype_code, threshold):
-    """Passes 1-2: bitmask, counts, cu_seqlens, meta=(E, max) on the device."""
+def _count_scan(x2d, dtype_code, threshold, host_meta=False):
+    """Passes 1-2: bitmask, counts, cu_seqlens, meta=(E, max), on the device
+    or (host_meta) in pinned host memory that the offsets kernel writes
+    directly, read after an event sync with no copy kernel."""
     NC, L = x2d.shape
     dev = x2d.device
     bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
     counts = _empty_i32(NC, dev)
     cu = _empty_i32(NC + 1, dev)
-    meta = _empty_i32(2, dev)
+    meta = torch.empty(2, dtype=_I32, pin_memory=True) if host_meta else _empty_i32(2, dev)
     s = _nat.stream_of(x2d)
     _nat.call("bcm_extract_count", _nat.ptr(x2d), dtype_code, NC, L, float(threshold),
               _nat.ptr(bitmask), _nat.ptr(counts), s)
@@ -175,7 +177,11 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None):
     dev = base_input.device
     with torch.cuda.device(dev):
         x2d = base_input.view(B * Dm, L)
-        bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold)
+        bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold,
+                                                     host_meta=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        ev.synchronize()
         E_base, max_seqlen = (int(v) for v in meta.tolist())
         NCi = B * Dm * expand
         cu = base_cu if expand == 1 else _empty_i32(NCi + 1, dev)

@@ -72,7 +72,6 @@ class Path:
         self.bitmask = torch.empty((self.NC, nat.bitmask_words(L)), **i32)
         self.counts = torch.empty(self.NC, **i32)
         self.cu = torch.empty(self.NC + 1, **i32)
-        self.meta = torch.empty(2, **i32)
         self.meta_h = torch.empty(2, dtype=torch.int32, pin_memory=True)
         self.meta_ev = torch.cuda.Event()
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
@@ -125,8 +124,8 @@ class Path:
         B, D, L = w.B, w.D, w.L
         mark("count", lambda: nat.call("bcm_extract_count", P(w.membrane), nat.dtype_code(w.membrane.dtype),
                                        self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), s))
-        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta), s))
-        self.meta_h.copy_(self.meta, non_blocking=True)
+        # (E, max_seqlen) go straight to pinned host memory: no copy kernel
+        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta_h), s))
         self.meta_ev.record()
         mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
                                       nat.dtype_code(w.dtype), P(self.ch), P(self.ts), P(self.k), P(self.u),

@@ -68,7 +68,9 @@ int bcm_extract_count(const void* membrane, int dtype, int64_t n_rows,
 
 /* Pass 2 (extract_events_cuda.cu:361-372, DeviceScan + cu[0]=0 + counts.max):
  * cu_seqlens[0] = 0, cu_seqlens[i+1] = sum(counts[0..i]);
- * meta[0] = total events E, meta[1] = max(counts) (0 when n_rows == 0). */
+ * meta[0] = total events E, meta[1] = max(counts) (0 when n_rows == 0).
+ * meta may be device memory or pinned (hipHostMalloc'd, device-mapped) host
+ * memory: the host then reads E after an event on `stream`, with no copy. */
 int bcm_extract_scan(const int32_t* counts, int64_t n_rows,
                      int32_t* cu_seqlens, int32_t* meta, bcm_stream_t stream);
 
