@@ -309,43 +309,80 @@ __global__ __launch_bounds__(256) void k_scatter(const T* __restrict__ g, const 
   if (c >= 0 && c < n_rows && s >= 0 && s < L) dx[(int64_t)c * L + s] = g[e];
 }
 
-// Row-wise gather backward: one wave per (row, 256-step segment); lane l
-// owns steps 4l..4l+3 of the segment and reads its events' gradients at
-// tile_start + rank (rank from the tile's bitmask).
+// Row-wise gather backward for time-sorted events: dx[row, t] = g[e] at the
+// row's events, 0 elsewhere. One wave per row, in windows of kGatherWin
+// steps: the window's event values (contiguous in g) are staged in LDS with
+// coalesced loads, then each lane writes 4 consecutive steps per 256-step
+// segment (one 16-byte store per lane, whole 1 KB rows per instruction),
+// taking its events' positions from the tile masks and the tile table.
+constexpr int kGatherWin = 2048;  // steps per window (32 tiles)
+
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void k_gather_bwd_rows(const T* __restrict__ g, const uint32_t* __restrict__ bitmask,
                                                          int64_t W, int64_t mrd,
                                                          const int32_t* __restrict__ tile_start, int64_t nT,
-                                                         int64_t n_rows, int64_t L, int64_t n_seg,
-                                                         T* __restrict__ dx) {
-  const int lane = lane_id();
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (wid >= n_rows * n_seg) return;
-  const int64_t row = wid / n_seg, seg = wid - row * n_seg;
-  const int64_t t0 = seg * 256 + 4 * lane;
-  if (t0 >= L) return;
-  const int64_t j = t0 / kTile;
-  const uint64_t m = tile_mask(bitmask + (row / mrd) * W, j);
-  const int off = (int)(t0 - j * kTile);
-  int e = tile_start[row * (nT + 1) + j] + __popcll(m & ((1ull << off) - 1ull));
-  const uint32_t nib = (uint32_t)(m >> off) & 0xFu;
-  float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[i] = 0.0f;
-    if ((nib >> i) & 1u) v[i] = to_f(g[e++]);
-  }
+                                                         int64_t n_rows, int64_t L, T* __restrict__ dx) {
+  __shared__ float s_g[4][kGatherWin];
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= n_rows) return;
+  const int32_t* ts = tile_start + row * (nT + 1);
+  const uint32_t* br = bitmask + (row / mrd) * W;
+  float* sg = s_g[wave];
   T* dr = dx + row * L;
-  if (VEC && t0 + 4 <= L) {
-    T o[4];
+  constexpr int SEGS = kGatherWin / 256;
+  for (int64_t w0 = 0; w0 < L; w0 += kGatherWin) {
+    const int64_t j0 = w0 / kTile;
+    const int64_t j1 = j0 + kGatherWin / kTile < nT ? j0 + kGatherWin / kTile : nT;
+    const int32_t e0 = ts[j0];
+    const int n = ts[j1] - e0;  // events in the window, <= kGatherWin
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(g + e0, (int64_t)n * (int64_t)sizeof(T));
+    // tile table entries and masks of the lane's segments, and the window's
+    // values, all in flight together
+    int32_t te[SEGS];
+    uint64_t tm[SEGS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = from_f<T>(v[i]);
-    if constexpr (sizeof(T) == 4) st_stream(*reinterpret_cast<u32x4*>(o), reinterpret_cast<u32x4*>(dr + t0));
-    else st_stream(*reinterpret_cast<u32x2*>(o), reinterpret_cast<u32x2*>(dr + t0));
-  } else {
+    for (int k = 0; k < SEGS; ++k) {
+      const int64_t t = w0 + 256 * k + 4 * lane;
+      const int64_t j = (t < L ? t : L - 1) / kTile;
+      te[k] = ts[j];
+      tm[k] = tile_mask(br, j);
+    }
+    for (int q = 0; q * kWave < n; ++q) {
+      const int i = q * kWave + lane;
+      const float v = buf_load<T>(rg, (uint32_t)i * (uint32_t)sizeof(T));
+      if (i < n && i < kGatherWin) sg[i] = v;
+    }
+    wave_sync();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (t0 + i < L) dr[t0 + i] = from_f<T>(v[i]);
+    for (int k = 0; k < SEGS; ++k) {
+      const int64_t t0 = w0 + 256 * k + 4 * lane;
+      if (t0 >= L) break;
+      const int off = (int)(t0 % kTile);
+      const uint64_t m = tm[k];
+      int e = te[k] - e0 + __popcll(m & ((1ull << off) - 1ull));
+      const uint32_t nib = (uint32_t)(m >> off) & 0xFu;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool bit = (nib >> i) & 1u;
+        const float x = sg[bit ? e : 0];
+        v[i] = bit ? x : 0.0f;
+        e += bit ? 1 : 0;
+      }
+      if (VEC && t0 + 4 <= L) {
+        T o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = from_f<T>(v[i]);
+        if constexpr (sizeof(T) == 4) st_stream(*reinterpret_cast<u32x4*>(o), reinterpret_cast<u32x4*>(dr + t0));
+        else st_stream(*reinterpret_cast<u32x2*>(o), reinterpret_cast<u32x2*>(dr + t0));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (t0 + i < L) dr[t0 + i] = from_f<T>(v[i]);
+      }
+    }
+    wave_sync();  // the staging area is refilled by the next window
   }
 }
 
@@ -499,18 +536,17 @@ int bcm_gather_bwd_rows(const void* g, int dtype, const uint32_t* bitmask, int64
   if (!bitmask || !tile_start || !dx) return set_error(BCM_EINVAL, "%s: null pointer", fn);
   if (!aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
   const int64_t W = bitmask_words(L), nT = tile_count(L);
-  const int64_t n_seg = (L + 255) / 256;
   const size_t es = dtype_size(dtype);
   const bool vec = aligned(dx, 4 * es) && ((L * (int64_t)es) % (4 * es) == 0);
-  const dim3 grid(blocks_for(n_rows * n_seg, 4)), block(256);
+  const dim3 grid(blocks_for(n_rows, 4)), block(256);
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     if (vec)
       hipLaunchKernelGGL((k_gather_bwd_rows<T, true>), grid, block, 0, hs(stream), static_cast<const T*>(g), bitmask,
-                         W, mask_row_div, tile_start, nT, n_rows, L, n_seg, static_cast<T*>(dx));
+                         W, mask_row_div, tile_start, nT, n_rows, L, static_cast<T*>(dx));
     else
       hipLaunchKernelGGL((k_gather_bwd_rows<T, false>), grid, block, 0, hs(stream), static_cast<const T*>(g),
-                         bitmask, W, mask_row_div, tile_start, nT, n_rows, L, n_seg, static_cast<T*>(dx));
+                         bitmask, W, mask_row_div, tile_start, nT, n_rows, L, static_cast<T*>(dx));
   });
   return check_launch(fn);
 }
