@@ -215,8 +215,8 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
           const int i = i0 + q * kWave + lane;
           if (i < seg_cnt) {
             const int tp = i > 0 ? st[i - 1] : prev_t;
-            ch_ids[obase + i] = (int32_t)lc;
-            t_steps[obase + i] = tv[q];
+            if (ch_ids) ch_ids[obase + i] = (int32_t)lc;
+            if (t_steps) t_steps[obase + i] = tv[q];
             k_flat[obase + i] = tp < 0 ? tv[q] + 1 : tv[q] - tp;
             if (head_flags) head_flags[obase + i] = tp < 0 ? 1 : 0;
           }
@@ -456,7 +456,7 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_
   };
   using Y = std::true_type;
   using N = std::false_type;
-  if (!ch_ids || !t_steps || !k_flat) return set_error(BCM_EINVAL, "%s: null output pointer", fn);
+  if (!k_flat) return set_error(BCM_EINVAL, "%s: null output pointer", fn);
   if (x) {
     dispatch_dtype(x_dtype, [&](auto tag) {
       if (tile_start) launch(tag, Y{}, Y{});

@@ -270,7 +270,8 @@ class Mamba(nn.Module):
             base_input = rearrange(hidden_states.detach(), "b l d -> b d l").contiguous()
             with cuda_stage("routing_index_extraction"):
                 _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_ev, event_index = \
-                    _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach())
+                    _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach(),
+                                                    positions=False)
             with cuda_stage("active_gather_forward"):
                 x_conv_flat = _IndexedGatherFn.apply(x, (x_ev,), event_index)
         else:

@@ -163,13 +163,15 @@ def gather_events_bwd(grad_x, channel_ids, time_steps, NC, L):
     return [dx]
 
 
-def extract_events_indexed(base_input, threshold, expand=1, x=None):
+def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True):
     """Fused extraction for the block forward (no reference counterpart; the
     reference composes extract_base_events + expand_base_events +
     gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
     max_seqlen as a Python int, x_events or None, event_index) where
     event_index = (bitmask, tile_start, expand) feeds the restore and the
-    row-wise gather backward. One host sync (E and max_seqlen together)."""
+    row-wise gather backward. With positions=False channel_ids and
+    time_steps are None and never written (the indexed restore and gather
+    do not use them). One host sync (E and max_seqlen together)."""
     _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
            "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
     B, Dm, L = base_input.shape
@@ -190,7 +192,8 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None):
             _nat.call("bcm_expand_events", None, None, None, _nat.ptr(base_cu), B * Dm, 0, expand,
                       None, None, None, _nat.ptr(cu), s)
         E = E_base * expand
-        ch, t, k = _empty_i32(E, dev), _empty_i32(E, dev), _empty_i32(E, dev)
+        k = _empty_i32(E, dev)
+        ch, t = (_empty_i32(E, dev), _empty_i32(E, dev)) if positions else (None, None)
         tile_start = torch.empty((NCi, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
         xe = None
         if x is not None:

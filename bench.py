@@ -43,7 +43,7 @@ def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
     n_ch = max(1, -(-max_seqlen // 2048))
     st = NC * n_ch * N * 8
     return {
-        "fwd_extract_gather": M // expand * s_m + M * s_u + 3 * E * 4 + E * s_u + 4 * (NC + 1),
+        "fwd_extract_gather": M // expand * s_m + M * s_u + E * 4 + E * s_u + 4 * (NC + 1),
         "fwd_scan": E * s_u + E * 4 + E * s_u + st,
         "fwd_restore": E * s_u + E * 4 + M * s_o,
         "bwd_restore": M * s_o + E * 4 + E * 4,
@@ -79,7 +79,7 @@ class Path:
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
         self.ws = torch.empty(2 * self.NC * nat.tile_count(L), dtype=torch.float32, device=dev)
         cap = self.NC * L  # upper bound of E
-        self.ch, self.ts, self.k = (torch.empty(cap, **i32) for _ in range(3))
+        self.k = torch.empty(cap, **i32)
         self.u = torch.empty(cap, dtype=w.dtype, device=dev)
         self.y = torch.empty(cap, dtype=w.dtype, device=dev)
         self.dy32 = torch.empty(cap, dtype=torch.float32, device=dev)
@@ -128,7 +128,7 @@ class Path:
         mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta_h), s))
         self.meta_ev.record()
         mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
-                                      nat.dtype_code(w.dtype), P(self.ch), P(self.ts), P(self.k), P(self.u),
+                                      nat.dtype_code(w.dtype), None, None, P(self.k), P(self.u),
                                       P(self.tile_start), None, s))
         self.meta_ev.synchronize()  # E and max_seqlen; fill keeps the GPU busy meanwhile
         E, ms = int(self.meta_h[0]), int(self.meta_h[1])

@@ -78,8 +78,10 @@ int bcm_extract_scan(const int32_t* counts, int64_t n_rows,
  * expand_events_direct_kernel :482-509 and gather_events_fwd2_kernel
  * :629-642). Emits the events of every base row c into the `expand` logical
  * channels c*expand + r at positions base_cu[c]*expand + r*count_c + i:
- * ch_ids, t_steps, k_flat (k = t+1 for a channel's first event, else the gap
- * to the previous event). Optional (NULL to skip): x [n_rows*expand, L] of
+ * k_flat (k = t+1 for a channel's first event, else the gap to the previous
+ * event) and, unless NULL, ch_ids and t_steps (a consumer that works from
+ * the bitmask and tile table needs neither). Optional (NULL to skip): x
+ * [n_rows*expand, L] of
  * x_dtype gathered at the events into x_events [E*expand]; tile_start
  * [n_rows*expand, tile_count+1]; head_flags [E*expand] (1 at a channel's
  * first event, else 0: the legacy extract_events output, :102-114). */

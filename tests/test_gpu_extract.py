@@ -136,6 +136,13 @@ def test_fused_extract_matches_composition(cuda_device, expand, dtype, L):
     assert ms == int(rms) and ex == expand
     assert torch.equal(xe, ee.gather_events_fwd(x, rch, rt)[0])
     assert np.array_equal(_np(tile_start), _tile_starts(_np(rt), _np(rcu), L))
+    # without positions: same k, offsets, gathered values and tile table
+    ch2, t2, k2, cu2, ms2, xe2, (bitmask2, tile_start2, _) = ee.extract_events_indexed(mem, 0.5, expand, x,
+                                                                                      positions=False)
+    assert ch2 is None and t2 is None and ms2 == ms
+    assert torch.equal(k2, k) and torch.equal(cu2, cu) and torch.equal(xe2, xe)
+    nw = 2 * ((L + 63) // 64)  # the words the tile masks read (the rest is row padding)
+    assert torch.equal(bitmask2[:, :nw], bitmask[:, :nw]) and torch.equal(tile_start2, tile_start)
 
 
 def test_gather_bwd_rows_matches_scatter(cuda_device):
