@@ -109,3 +109,36 @@ def bitmask_words(L):
 
 def tile_count(L):
     return (L + 63) // 64
+
+
+class HostMeta:
+    """(E, max_seqlen) handed from the offsets kernel to the host through
+    pinned memory. The kernel writes both values with one 64-bit store that
+    goes through to memory, so the host polls the pinned words instead of
+    recording an event: an event record makes the GPU write back its caches
+    (several microseconds of idle device between two kernels)."""
+
+    def __init__(self):
+        self.t = torch.empty(2, dtype=torch.int32, pin_memory=True)
+        self._v = self.t.numpy()
+
+    def arm(self):
+        """Call before enqueuing the offsets kernel that writes it."""
+        self._v[0] = -1
+
+    def ptr(self):
+        return c_p(self.t.data_ptr())
+
+    def wait(self, stream, timeout_s=10.0):
+        """(E, max_seqlen) once written. Falls back to a stream sync (which
+        also makes any pending write visible) if polling times out."""
+        import time
+        t0 = time.perf_counter()
+        v = self._v
+        while v[0] < 0:
+            if time.perf_counter() - t0 > timeout_s:
+                stream.synchronize()
+                if v[0] < 0:
+                    raise RuntimeError("bc_mamba_amd: offsets kernel did not deliver the event count")
+                break
+        return int(v[0]), int(v[1])

@@ -144,8 +144,11 @@ __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict_
     int m = 0;
     for (int w = 0; w < nw; ++w) m = max(m, s_wmax[w]);
     cu[0] = 0;
-    meta[0] = carry;
-    meta[1] = m;
+    // (total, max) in one 64-bit system-scope store: written through to
+    // memory, so a host polling pinned memory sees both values at once,
+    // before the kernel ends and without an event
+    const uint64_t packed = (uint64_t)(uint32_t)carry | ((uint64_t)(uint32_t)m << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(meta), packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -424,6 +427,7 @@ int bcm_extract_scan(const int32_t* counts, int64_t n_rows, int32_t* cu_seqlens,
   const char* fn = "bcm_extract_scan";
   if (n_rows < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
   if (!cu_seqlens || !meta || (n_rows > 0 && !counts)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!aligned(meta, 8)) return set_error(BCM_EINVAL, "%s: meta must be 8-byte aligned", fn);
   if (aligned(counts, 16))
     hipLaunchKernelGGL(k_scan_counts<true>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
   else

@@ -38,11 +38,13 @@ def _count_scan(x2d, dtype_code, threshold, host_meta=False):
     bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
     counts = _empty_i32(NC, dev)
     cu = _empty_i32(NC + 1, dev)
-    meta = torch.empty(2, dtype=_I32, pin_memory=True) if host_meta else _empty_i32(2, dev)
+    meta = _nat.HostMeta() if host_meta else _empty_i32(2, dev)
+    if host_meta:
+        meta.arm()
     s = _nat.stream_of(x2d)
     _nat.call("bcm_extract_count", _nat.ptr(x2d), dtype_code, NC, L, float(threshold),
               _nat.ptr(bitmask), _nat.ptr(counts), s)
-    _nat.call("bcm_extract_scan", _nat.ptr(counts), NC, _nat.ptr(cu), _nat.ptr(meta), s)
+    _nat.call("bcm_extract_scan", _nat.ptr(counts), NC, _nat.ptr(cu), meta.ptr() if host_meta else _nat.ptr(meta), s)
     return bitmask, counts, cu, meta
 
 
@@ -181,10 +183,7 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
         x2d = base_input.view(B * Dm, L)
         bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold,
                                                      host_meta=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        ev.synchronize()
-        E_base, max_seqlen = (int(v) for v in meta.tolist())
+        E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
         NCi = B * Dm * expand
         cu = base_cu if expand == 1 else _empty_i32(NCi + 1, dev)
         s = _nat.stream_of(x2d)

@@ -72,8 +72,7 @@ class Path:
         self.bitmask = torch.empty((self.NC, nat.bitmask_words(L)), **i32)
         self.counts = torch.empty(self.NC, **i32)
         self.cu = torch.empty(self.NC + 1, **i32)
-        self.meta_h = torch.empty(2, dtype=torch.int32, pin_memory=True)
-        self.meta_ev = torch.cuda.Event()
+        self.meta_h = nat.HostMeta()
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
@@ -124,14 +123,15 @@ class Path:
         B, D, L = w.B, w.D, w.L
         mark("count", lambda: nat.call("bcm_extract_count", P(w.membrane), nat.dtype_code(w.membrane.dtype),
                                        self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), s))
-        # (E, max_seqlen) go straight to pinned host memory: no copy kernel
-        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), P(self.meta_h), s))
-        self.meta_ev.record()
+        # (E, max_seqlen) go straight to pinned host memory: no copy kernel,
+        # no event (the host polls while fill runs)
+        self.meta_h.arm()
+        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), self.meta_h.ptr(),
+                                         s))
         mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
                                       nat.dtype_code(w.dtype), None, None, P(self.k), P(self.u),
                                       P(self.tile_start), None, s))
-        self.meta_ev.synchronize()  # E and max_seqlen; fill keeps the GPU busy meanwhile
-        E, ms = int(self.meta_h[0]), int(self.meta_h[1])
+        E, ms = self.meta_h.wait(t.cuda.current_stream())  # fill keeps the GPU busy meanwhile
         if E != self.E or ms != self.ms:
             self.E, self.ms = E, ms
             a = self.args
@@ -294,12 +294,19 @@ def main():
     dominant = max(per_kernel, key=per_kernel.get)
     path.events.clear()
 
+    # timed region: no events inside (an event record makes the GPU write
+    # back its caches, several microseconds of idle device per record)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        path.step(timed=(dominant,))
+        path.step()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the dominant kernel's launch duration: HIP events around it, on its
+    # stream, over as many steps again right after the timed region
+    for _ in range(args.steps):
+        path.step(timed=(dominant,))
+    torch.cuda.synchronize()
     dom_ms = path.kernel_ms(dominant)
 
     E, ms = path.E, path.ms

@@ -69,8 +69,10 @@ int bcm_extract_count(const void* membrane, int dtype, int64_t n_rows,
 /* Pass 2 (extract_events_cuda.cu:361-372, DeviceScan + cu[0]=0 + counts.max):
  * cu_seqlens[0] = 0, cu_seqlens[i+1] = sum(counts[0..i]);
  * meta[0] = total events E, meta[1] = max(counts) (0 when n_rows == 0).
- * meta may be device memory or pinned (hipHostMalloc'd, device-mapped) host
- * memory: the host then reads E after an event on `stream`, with no copy. */
+ * meta (8-byte aligned) may be device memory or pinned (hipHostMalloc'd,
+ * device-mapped) host memory. Both values land in one 64-bit store written
+ * through to memory, so a host that set meta[0] = -1 beforehand may poll it
+ * (no event, no copy): once meta[0] >= 0, meta[1] is valid too. */
 int bcm_extract_scan(const int32_t* counts, int64_t n_rows,
                      int32_t* cu_seqlens, int32_t* meta, bcm_stream_t stream);
 
