@@ -124,19 +124,23 @@ template <int CTRL> __device__ __forceinline__ float dpp_zero(float v) {
 }
 
 template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are VALU
-  // A lane with no partner gets H += P·0 and P *= 1 (the identities), so
-  // each step can compile to one v_fmac_f32_dpp and one v_mul_f32_dpp.
+  // One scan step is two DPP instructions: H += P·H[lane∓o] with a zero
+  // source for a lane without a partner (bound_ctrl), then P *= P[lane∓o]
+  // with no write for a lane without a partner (P unchanged: P·1). The
+  // compiler does not fold a float DPP move into a v_fmac / v_mul itself
+  // (1.0 is not an identity it recognises), which costs three extra moves
+  // per step. Each block starts with s_nop 1: a DPP read needs two wait
+  // states after the VALU write of its source, whichever instruction the
+  // compiler placed just before.
   template <int O> static __device__ __forceinline__ void up(float& P, float& H) {
-    const float Hp = dpp_zero<kRowShr + O>(H);
-    const float Pp = dpp_mov<kRowShr + O>(P, 1.0f);
-    H = fmaf(P, Hp, H);
-    P *= Pp;
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shr:%2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(H) : "v"(P), "n"(O));
+    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shr:%1 row_mask:0xf bank_mask:0xf" : "+v"(P) : "n"(O));
   }
   template <int O> static __device__ __forceinline__ void down(float& Q, float& C) {
-    const float Cs = dpp_zero<kRowShl + O>(C);
-    const float Qs = dpp_mov<kRowShl + O>(Q, 1.0f);
-    C = fmaf(Q, Cs, C);
-    Q *= Qs;
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_shl:%2 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "+v"(C) : "v"(Q), "n"(O));
+    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_shl:%1 row_mask:0xf bank_mask:0xf" : "+v"(Q) : "n"(O));
   }
   static __device__ __forceinline__ void scan_up(float& P, float& H) {
     up<1>(P, H);
