@@ -190,6 +190,14 @@ template <typename T> __device__ __forceinline__ T ld_stream_elem(const T* p) {
   return h;
 }
 
+// The value itself, hidden from common-subexpression elimination and
+// loop-invariant code motion: offsets derived from it are recomputed where
+// they are used instead of being kept live in registers.
+template <typename V> __device__ __forceinline__ V opaque(V v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // DPP lane permutations inside rows of 16 lanes (VALU, no LDS round trip).
 template <int CTRL> __device__ __forceinline__ uint32_t dpp(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);

@@ -171,13 +171,6 @@ template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are
 // tile, where item i sits at i + i/R (lane stride R+1: conflict-free reads).
 template <int R> __device__ __forceinline__ int tile_pos(int idx) { return idx + idx / R; }
 
-// The value itself, hidden from common-subexpression elimination: offsets
-// recomputed after the state loop are not kept live across it.
-template <typename V> __device__ __forceinline__ V opaque(V v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
 // Decay of an item from the table: `tb` is the item's byte offset in a table
 // row, `row` the state's row base in bytes (wave-uniform), so each read costs
 // one address add.
