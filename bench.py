@@ -37,13 +37,16 @@ STAGE_KERNELS = {"count": ["k_count"], "offsets": ["k_scan_counts"], "fill": ["k
 
 def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
     """Compulsory traffic of the path's API contract, each tensor once
-    (x_conv read and dx written dense)."""
+    (x_conv read and dx written dense), as the reference's interface moves
+    it: extract emits ch, t and k (the indexed path here writes k only and
+    reads a 3 MB event index instead of t in restore and gather, so its own
+    traffic is below these figures)."""
     M = B * D * L
     NC = B * D
     n_ch = max(1, -(-max_seqlen // 2048))
     st = NC * n_ch * N * 8
     return {
-        "fwd_extract_gather": M // expand * s_m + M * s_u + E * 4 + E * s_u + 4 * (NC + 1),
+        "fwd_extract_gather": M // expand * s_m + M * s_u + 3 * E * 4 + E * s_u + 4 * (NC + 1),
         "fwd_scan": E * s_u + E * 4 + E * s_u + st,
         "fwd_restore": E * s_u + E * 4 + M * s_o,
         "bwd_restore": M * s_o + E * 4 + E * 4,
