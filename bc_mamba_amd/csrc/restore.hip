@@ -67,7 +67,8 @@ struct TileWave {
 // lines and index rows) in one L2. Lanes
 // past `dim` are clamped to the group's last channel (addresses stay valid)
 // and flagged !ok.
-__device__ __forceinline__ TileWave tile_wave(int nT, int nG, int dim, const int32_t* tile_start) {
+// nPos: positions along time per (b, g); nT: tiles per row of the tile table.
+__device__ __forceinline__ TileWave tile_wave(int nPos, int nG, int dim, const int32_t* tile_start, int nT) {
   TileWave w;
   // wave-uniform by construction; readfirstlane lets the compiler keep it (and
   // the buffer descriptors built from it) in SGPRs
@@ -75,8 +76,8 @@ __device__ __forceinline__ TileWave tile_wave(int nT, int nG, int dim, const int
                                                  (int)(threadIdx.x / kWave));
   w.g = wid % nG;
   const int bj = wid / nG;
-  w.j = bj % nT;
-  w.b = bj / nT;
+  w.j = bj % nPos;
+  w.b = bj / nPos;
   const int d = w.g * kWave + lane_id();
   w.ok = d < dim;
   w.dd = w.ok ? d : dim - 1;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
                                                      int waves, int dim, int64_t L, int64_t out_elems,
                                                      TO* __restrict__ out) {
   if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
-  const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT);
   const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
   const int32_t cu0 = ts[0], elo = ts[w.j];
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
@@ -128,14 +129,17 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
 // Restore backward, tile pass. Runs that start and end inside the tile are
 // final; the partial runs at the tile edges (head: before the first event;
 // tail: from the last event to the tile end) go to per-tile side arrays
-// [nT][n_rows] for the fix-up pass. The final runs of the wave's 64
-// channels are staged in LDS (value and destination, at a slot from a wave
-// prefix sum of the per-channel run counts) and written out with
-// consecutive lanes on consecutive slots: a channel's runs are consecutive
-// dy entries, so each store instruction covers a few contiguous pieces
-// instead of up to 64 scattered words. Waves with more runs than the
-// staging area store them directly.
-constexpr int kBwdStage = 1024;  // staged runs per wave (about 620 at 15% density)
+// [nT][n_rows] for the fix-up pass. At each event a lane stages the run that
+// the event closes in LDS (value and destination, one 8-byte write at the
+// lane's next slot; slots from a wave prefix sum of the per-lane event
+// counts). A lane's first slot holds its head, which is read back and whose
+// destination is then marked out of range. The staged runs are written out
+// with consecutive lanes on consecutive slots: a channel's runs are
+// consecutive dy entries, so each store instruction covers a few contiguous
+// pieces instead of up to 64 scattered words. Waves with more events than
+// the staging area store the runs directly.
+constexpr int kBwdStage = 1024;    // staged runs per wave (about 680 at 15% density)
+constexpr uint32_t kNoDst = kBufOOB / 4;  // destination whose byte offset is out of range
 
 template <typename TI>
 __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restrict__ dout, int64_t n_events,
@@ -144,10 +148,9 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
                                                               int nT, int nG, int waves, int dim, int64_t L,
                                                               int64_t n_rows, float* __restrict__ dy,
                                                               float* __restrict__ head, float* __restrict__ tail) {
-  __shared__ float s_val[4][kBwdStage + kWave];    // + one discard slot per lane
-  __shared__ uint32_t s_dst[4][kBwdStage + kWave];
+  __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
   if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
-  const TileWave w = tile_wave(nT, nG, dim, tile_start);
+  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT);
   const int wave = threadIdx.x / kWave, lane = lane_id();
   // dout rows of the tile; steps past L and lanes past dim read 0
   const int64_t t0 = (int64_t)w.j * kTile;
@@ -163,50 +166,56 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
   const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
-  // runs closing inside the tile: events - 1 per channel with events
-  const int nrun = m ? __popcll(m) - 1 : 0;
-  const int incl = wave_incl_sum_dpp(nrun);
+  const int nev = __popcll(m);
+  const int incl = wave_incl_sum_dpp(nev);
   const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
-  const bool staged = total <= kBwdStage;  // wave-uniform
-  const uint32_t slot0 = (uint32_t)(incl - nrun);
-  const uint32_t discard = kBwdStage + lane;
-  float* sv = s_val[wave];
-  uint32_t* sd = s_dst[wave];
   // sum: the open run; hsum: the steps before the tile's first event (the
-  // whole tile when it has none), kept as a running value
-  float sum = 0.0f, hsum = 0.0f;
-  uint32_t r = 0;                                // events seen so far in the tile
-  const uint32_t ebase = (uint32_t)(elo - e_base);
-  const int first = m ? __builtin_ctzll(m) : kTile;  // step of the tile's first event
+  // whole tile when it has none)
+  float sum = 0.0f, hsum;
+  if (total <= kBwdStage) {  // wave-uniform
+    uint2* sr = s_run[wave];
+    const int pre = incl - nev;
+    uint32_t slot = (uint32_t)pre;
+    uint32_t dst = (uint32_t)(elo - e_base) - 1u;  // event whose run the next event closes
 #pragma unroll
-  for (int s = 0; s < kTile; ++s) {
-    const uint32_t bit = (uint32_t)(m >> s) & 1u;
-    // the run of event (elo + r - 1) closes here when r >= 1
-    const bool close = bit && r;
-    if (staged) {
-      const uint32_t slot = close ? slot0 + r - 1 : discard;
-      sv[slot] = sum;
-      sd[slot] = ebase + r - 1;
-    } else {
-      buf_store_f32(rdy, close ? (ebase + r - 1) * 4u : kBufOOB, sum);
+    for (int s = 0; s < kTile; ++s) {
+      const bool bit = (m >> s) & 1ull;
+      if (bit) {
+        sr[slot] = make_uint2(__float_as_uint(sum), dst);
+        ++slot;
+        ++dst;
+      }
+      sum = (bit ? 0.0f : sum) + gv[s];
     }
-    r += bit;
-    sum = (bit ? 0.0f : sum) + gv[s];
-    hsum += s < first ? gv[s] : 0.0f;
+    hsum = sum;
+    if (nev) {  // the first slot is the head: read it back, drop its store
+      hsum = __uint_as_float(sr[pre].x);
+      sr[pre].y = kNoDst;
+    }
+    wave_sync();
+    for (int k = 0; k < total; k += kWave) {
+      const int i = k + lane;
+      const uint2 v = sr[i < total ? i : 0];
+      buf_store_f32(rdy, i < total ? v.y * 4u : kBufOOB, __uint_as_float(v.x));
+    }
+  } else {
+    uint32_t r = 0;  // events seen so far in the tile
+    const uint32_t ebase = (uint32_t)(elo - e_base);
+    const int first = m ? __builtin_ctzll(m) : kTile;  // step of the tile's first event
+    hsum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kTile; ++s) {
+      const uint32_t bit = (uint32_t)(m >> s) & 1u;
+      // the run of event (elo + r - 1) closes here when r >= 1
+      buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
+      r += bit;
+      sum = (bit ? 0.0f : sum) + gv[s];
+      hsum += s < first ? gv[s] : 0.0f;
+    }
   }
   if (w.ok) {
     head[(int64_t)w.j * n_rows + w.ch] = hsum;
     tail[(int64_t)w.j * n_rows + w.ch] = sum;
-  }
-  if (staged) {
-    wave_sync();
-    for (int k = 0; k < total; k += kWave) {
-      const int i = k + lane;
-      const bool ok = i < total;
-      const float v = sv[ok ? i : discard];
-      const uint32_t dst = sd[ok ? i : discard];
-      buf_store_f32(rdy, ok ? dst * 4u : kBufOOB, v);
-    }
   }
 }
 
@@ -310,6 +319,7 @@ int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_
   if (rc) return rc;
   if (n_rows == 0) return BCM_OK;
   if (!dout || (n_events > 0 && !dy) || n_events < 0) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_events * 4 > INT32_MAX) return set_error(BCM_EINVAL, "%s: dy must be below 2 GiB", fn);
   const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
   if (!workspace || workspace_bytes < bcm_restore_bwd_workspace_bytes(n_rows, L))
     return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn,

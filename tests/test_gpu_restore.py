@@ -27,6 +27,7 @@ CASES = [  # B, D, L, density
     (1, 3, 1, 0.9),
     (1, 2, 6000, 0.9),     # > 4095 events per channel (beyond the reference's exact range)
     (2, 64, 300, 0.02),
+    (1, 64, 256, 0.6),     # > 1024 events per 64-channel tile: the backward's direct-store path
 ]
 
 
