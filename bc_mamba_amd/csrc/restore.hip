@@ -129,7 +129,8 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
 // Restore backward, tile pass. Runs that start and end inside the tile are
 // final; the partial runs at the tile edges (head: before the first event;
 // tail: from the last event to the tile end) go to per-tile side arrays
-// [nT][n_rows] for the fix-up pass. At each event a lane stages the run that
+// [nT][n_rows] for the fix-up pass, with the tile's end event index (-1 for
+// a tile without events). At each event a lane stages the run that
 // the event closes in LDS (value and destination, one 8-byte write at the
 // lane's next slot; slots from a wave prefix sum of the per-lane event
 // counts). A lane's first slot holds its head, which is read back and whose
@@ -147,7 +148,8 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
                                                               int64_t mrd, const int32_t* __restrict__ tile_start,
                                                               int nT, int nG, int waves, int dim, int64_t L,
                                                               int64_t n_rows, float* __restrict__ dy,
-                                                              float* __restrict__ head, float* __restrict__ tail) {
+                                                              float* __restrict__ head, float* __restrict__ tail,
+                                                              int32_t* __restrict__ tend) {
   __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
   if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start, nT);
@@ -214,27 +216,29 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
     }
   }
   if (w.ok) {
-    head[(int64_t)w.j * n_rows + w.ch] = hsum;
-    tail[(int64_t)w.j * n_rows + w.ch] = sum;
+    const int64_t o = (int64_t)w.j * n_rows + w.ch;
+    head[o] = hsum;
+    tail[o] = sum;
+    tend[o] = nev ? elo + nev : -1;
   }
 }
 
 // Restore backward, fix-up pass: the run of the last event of tile j is its
 // tail partial plus the head partials of the following tiles up to and
-// including the next tile that holds an event. One lane per (tile, channel).
-__global__ __launch_bounds__(256) void k_restore_bwd_fix(const int32_t* __restrict__ tile_start, int64_t nT,
-                                                         int64_t n_rows, const float* __restrict__ head,
-                                                         const float* __restrict__ tail, float* __restrict__ dy) {
+// including the next tile that holds an event. One lane per (tile, channel);
+// every read is coalesced ([nT][n_rows] side arrays), only the dy store is
+// scattered.
+__global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_rows, const float* __restrict__ head,
+                                                         const float* __restrict__ tail,
+                                                         const int32_t* __restrict__ tend, float* __restrict__ dy) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nT * n_rows) return;
-  const int64_t j = i / n_rows, ch = i - j * n_rows;
-  const int32_t* ts = tile_start + ch * (nT + 1);
-  const int32_t e_end = ts[j + 1];
-  if (e_end == ts[j]) return;  // no event in tile j: its head belongs to an earlier tile's owner
+  const int32_t e_end = tend[i];
+  if (e_end < 0) return;  // no event in the tile: its head belongs to an earlier tile's owner
   float acc = tail[i];
-  for (int64_t jj = j + 1; jj < nT; ++jj) {
-    acc += head[jj * n_rows + ch];
-    if (ts[jj + 1] != ts[jj]) break;
+  for (int64_t q = i + n_rows; q < nT * n_rows; q += n_rows) {
+    acc += head[q];
+    if (tend[q] >= 0) break;
   }
   dy[e_end - 1] = acc;
 }
@@ -307,7 +311,7 @@ int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events, const uint32_t
 }
 
 int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L) {
-  return (n_rows < 0 || L < 1) ? 0 : 2 * 4 * n_rows * tile_count(L);
+  return (n_rows < 0 || L < 1) ? 0 : 3 * 4 * n_rows * tile_count(L);
 }
 
 int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
@@ -326,18 +330,19 @@ int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_
                      (long long)bcm_restore_bwd_workspace_bytes(n_rows, L));
   float* head = static_cast<float*>(workspace);
   float* tail = head + nT * n_rows;
+  int32_t* tend = reinterpret_cast<int32_t*>(tail + nT * n_rows);
   const int64_t waves = (n_rows / dim) * nT * nG;
   if (waves > INT32_MAX / 2 || dim > (1 << 22)) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
     hipLaunchKernelGGL(k_restore_bwd_tiles<T>, dim3(nblk(waves)), dim3(256), 0, hs(stream),
                        static_cast<const T*>(dout), n_events, bitmask, W, mask_row_div, tile_start, (int)nT,
-                       (int)nG, (int)waves, (int)dim, L, n_rows, dy, head, tail);
+                       (int)nG, (int)waves, (int)dim, L, n_rows, dy, head, tail, tend);
   });
   rc = check_launch(fn);
   if (rc) return rc;
   hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, hs(stream),
-                     tile_start, nT, n_rows, head, tail, dy);
+                     nT, n_rows, head, tail, tend, dy);
   return check_launch(fn);
 }
 

@@ -59,7 +59,8 @@ def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy):
     """Restore backward from an event index into the float32 dy (every
     event's entry is written; no zero-init needed)."""
     bitmask, tile_start, mrd = event_index
-    ws = torch.empty(2 * n_ch * _nat.tile_count(seqlen), dtype=torch.float32, device=dout.device)
+    ws = torch.empty(_nat.lib().bcm_restore_bwd_workspace_bytes(n_ch, seqlen) // 4, dtype=torch.float32,
+                     device=dout.device)
     _nat.call("bcm_restore_bwd", _nat.ptr(dout), _nat.dtype_code(dout.dtype), _nat.ptr(bitmask), int(mrd),
               _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), int(dy.numel()), _nat.ptr(ws),
               4 * ws.numel(),

@@ -79,7 +79,8 @@ class Path:
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
-        self.ws = torch.empty(2 * self.NC * nat.tile_count(L), dtype=torch.float32, device=dev)
+        self.ws = torch.empty(nat.lib().bcm_restore_bwd_workspace_bytes(self.NC, L) // 4, dtype=torch.float32,
+                              device=dev)
         cap = self.NC * L  # upper bound of E
         self.k = torch.empty(cap, **i32)
         self.u = torch.empty(cap, dtype=w.dtype, device=dev)

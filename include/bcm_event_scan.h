@@ -200,14 +200,14 @@ int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events,
                     int64_t n_rows, int64_t dim, int64_t L, void* out,
                     int out_dtype, bcm_stream_t stream);
 
-/* Workspace of bcm_restore_bwd: 2 * 4 * n_rows * tile_count(L) bytes. */
+/* Workspace of bcm_restore_bwd: 3 * 4 * n_rows * tile_count(L) bytes. */
 int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L);
 
 /* restore_dense_bwd (restore_dense.cpp:138-202,
  * restore_dense_bwd_kernel.cuh:42-112): dy[e] = sum of dout[b, t, d] over
  * t in [t_e, t_next) (t_next = next event or L), float32. Every event with
  * 0 <= t_e < L is written exactly once (no zero-init, no atomics,
- * deterministic); `workspace` holds per-tile partial sums. */
+ * deterministic); `workspace` holds per-tile partial sums and end indices. */
 int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask,
                     int64_t mask_row_div, const int32_t* tile_start,
                     int64_t n_rows, int64_t dim, int64_t L, float* dy,
