@@ -171,6 +171,23 @@ template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are
 // tile, where item i sits at i + i/R (lane stride R+1: conflict-free reads).
 template <int R> __device__ __forceinline__ int tile_pos(int idx) { return idx + idx / R; }
 
+// Byte offsets in a group's tile of the items q*G + j (q = 0..R-1) of lane j.
+// They repeat with period P = R / gcd(G, R) in q, shifted by P*G + P*G/R
+// slots, so P registers and immediate offsets cover all R of them.
+template <int G, int R> struct TilePos {
+  static constexpr int gcd(int a, int b) { return b ? gcd(b, a % b) : a; }
+  static constexpr int P = R / gcd(G, R);
+  static constexpr uint32_t STEP = 4u * (P * G + (P * G) / R);
+  uint32_t base[P];
+  __device__ __forceinline__ explicit TilePos(int j) {
+#pragma unroll
+    for (int t = 0; t < P; ++t) base[t] = 4u * (uint32_t)tile_pos<R>(t * G + j);
+  }
+  __device__ __forceinline__ float& at(float* tile, int q) const {
+    return *reinterpret_cast<float*>(reinterpret_cast<char*>(tile) + base[q % P] + (uint32_t)(q / P) * STEP);
+  }
+};
+
 // Decay of an item from the table: `tb` is the item's byte offset in a table
 // row, `row` the state's row base in bytes (wave-uniform), so each read costs
 // one address add.
@@ -241,25 +258,26 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   // call: opaque() keeps them from being hoisted and held in registers). The
   // first chunk's loads are issued before the parameter set-up so their
   // latency overlaps it.
+  // Items past the channel's events load the next channel's values (or 0
+  // past E): they are padding, whose Δ the item set-up forces to 0, and
+  // their outputs are never stored.
   float rawu[R];
   int rawk[R];
+  const TilePos<G, R> tp(j);
   auto issue = [&](int e0, int n, int c) {
-    const int cnt = min(max(n - c * C, 0), C);
-    const uint32_t eb = (uint32_t)(e0 + c * C);
-    const int jo = opaque(j);
+    (void)n;
+    const uint32_t eb = (uint32_t)(e0 + c * C) + (uint32_t)opaque(j);
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const int idx = q * G + jo;
-      rawu[q] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
-      rawk[q] = buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB);
+      rawu[q] = buf_load<T>(ru, (eb + (uint32_t)(q * G)) * SZ);
+      rawk[q] = buf_load_i32(rk, (eb + (uint32_t)(q * G)) * 4u);
     }
   };
   auto to_tiles = [&]() {
-    const int jo = opaque(j);
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      tile[tile_pos<R>(q * G + jo)] = rawu[q];
-      tilek[tile_pos<R>(q * G + jo)] = __int_as_float(rawk[q]);
+      tp.at(tile, q) = rawu[q];
+      tp.at(tilek, q) = __int_as_float(rawk[q]);
     }
   };
   auto channel = [&](int b, int& e0, int& n) {
@@ -405,7 +423,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
         for (int q = 0; q < R; ++q) {
           const int idx = q * G + jo;
           const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
-          const float yv = tile[tile_pos<R>(idx)];
+          const float yv = tp.at(tile, q);
           buf_store<T>(ro, off, yv);
           if (HAS_Z) {
             const float zv = buf_load<T>(rz, off);
@@ -477,25 +495,26 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   // first before the parameter set-up, the next after a chunk's last use of
   // the tiles), so their latency overlaps other work. dout is loaded at the
   // top of its chunk and goes through the u tile once u has been read.
+  // Items past the channel's events load the next channel's values (or 0
+  // past E): they are padding, whose Δ and dout·u the item set-up forces to
+  // 0, and their outputs are never stored.
   float rawu[R];
   int rawk[R];
+  const TilePos<G, R> tp(j);
   auto issue = [&](int e0, int n, int c) {
-    const int cnt = min(max(n - c * C, 0), C);
-    const uint32_t eb = (uint32_t)(e0 + c * C);
-    const int jo = opaque(j);
+    (void)n;
+    const uint32_t eb = (uint32_t)(e0 + c * C) + (uint32_t)opaque(j);
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      const int idx = q * G + jo;
-      rawk[q] = buf_load_i32(rk, idx < cnt ? (eb + idx) * 4u : kBufOOB);
-      rawu[q] = buf_load<T>(ru, idx < cnt ? (eb + idx) * SZ : kBufOOB);
+      rawk[q] = buf_load_i32(rk, (eb + (uint32_t)(q * G)) * 4u);
+      rawu[q] = buf_load<T>(ru, (eb + (uint32_t)(q * G)) * SZ);
     }
   };
   auto to_tiles = [&]() {
-    const int jo = opaque(j);
 #pragma unroll
     for (int q = 0; q < R; ++q) {
-      tilek[tile_pos<R>(q * G + jo)] = __int_as_float(rawk[q]);
-      tile[tile_pos<R>(q * G + jo)] = rawu[q];
+      tp.at(tilek, q) = __int_as_float(rawk[q]);
+      tp.at(tile, q) = rawu[q];
     }
   };
   auto channel = [&](int b, int& e0, int& n) {
@@ -558,10 +577,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
         const int jo = opaque(j);
         float dlv[R], uvv[R], rawd[R];
 #pragma unroll
-        for (int q = 0; q < R; ++q) {
-          const int idx = q * G + jo;
-          rawd[q] = buf_load<T>(rdo, idx < cnt ? (eb + idx) * SZ : kBufOOB);
-        }
+        for (int q = 0; q < R; ++q) rawd[q] = buf_load<T>(rdo, (eb + (uint32_t)(q * G + jo)) * SZ);
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -590,13 +606,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
             buf_store<T>(rdz, off, dv * ov * sg * (1.0f + zv * (1.0f - sg)));
             dv *= zv * sg;
           }
-          tile[tile_pos<R>(idx)] = dv;
+          tp.at(tile, q) = dv;
         }
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           du2[r] = dlv[r] * uvv[r] * uvv[r];
-          doutu[r] = gg[r] * uvv[r];
+          doutu[r] = r < nv ? gg[r] * uvv[r] : 0.0f;
           acc1[r] = 0.0f;
           acc2[r] = 0.0f;
         }
@@ -742,8 +758,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
         float uvv[R], fu[R], fd[R];
 #pragma unroll
         for (int q = 0; q < R; ++q) {  // both loads in flight together
-          const int idx = q * G + jo;
-          const uint32_t off = idx < cnt ? (eb + idx) * SZ : kBufOOB;
+          const uint32_t off = (eb + (uint32_t)(q * G + jo)) * SZ;
           fu[q] = buf_load<T>(ru, off);
           fd[q] = buf_load<T>(rdo, off);
           if (HAS_Z) {
@@ -752,13 +767,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           }
         }
 #pragma unroll
-        for (int q = 0; q < R; ++q) tile[tile_pos<R>(q * G + jo)] = fu[q];
+        for (int q = 0; q < R; ++q) tp.at(tile, q) = fu[q];
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) uvv[r] = gg[r];
         wave_sync();
 #pragma unroll
-        for (int q = 0; q < R; ++q) tile[tile_pos<R>(q * G + jo)] = fd[q];
+        for (int q = 0; q < R; ++q) tp.at(tile, q) = fd[q];
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -776,7 +791,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
 #pragma unroll
         for (int q = 0; q < R; ++q) {
           const int idx = q * G + jo;
-          buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, tile[tile_pos<R>(idx)]);
+          buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, tp.at(tile, q));
         }
       }
       if (c > 0) {  // the previous chunk's loads, now that the tiles are free
