@@ -230,11 +230,14 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
 // scattered.
 __global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_rows, const float* __restrict__ head,
                                                          const float* __restrict__ tail,
-                                                         const int32_t* __restrict__ tend, float* __restrict__ dy) {
+                                                         const int32_t* __restrict__ tend, float* __restrict__ dy,
+                                                         int64_t n_events) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nT * n_rows) return;
   const int32_t e_end = tend[i];
-  if (e_end < 0) return;  // no event in the tile: its head belongs to an earlier tile's owner
+  // no event in the tile (its head belongs to an earlier tile's owner); an
+  // index outside dy (a workspace the tile pass did not fill) is never stored
+  if (e_end <= 0 || e_end > n_events) return;
   float acc = tail[i];
   for (int64_t q = i + n_rows; q < nT * n_rows; q += n_rows) {
     acc += head[q];
@@ -342,7 +345,7 @@ int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_
   rc = check_launch(fn);
   if (rc) return rc;
   hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, hs(stream),
-                     nT, n_rows, head, tail, tend, dy);
+                     nT, n_rows, head, tail, tend, dy, n_events);
   return check_launch(fn);
 }
 
