@@ -45,6 +45,10 @@ SIGNATURES = {
     "bcm_extract_count": (c_i32, [c_p, c_i32, c_i64, c_i64, c_f32, c_p, c_p, c_p]),
     "bcm_extract_scan": (c_i32, [c_p, c_i64, c_p, c_p, c_p]),
     "bcm_extract_fill": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
+    "bcm_extract_block_sums_bytes": (c_i64, [c_i64]),
+    "bcm_extract_count_blocks": (c_i32, [c_p, c_i32, c_i64, c_i64, c_f32, c_p, c_p, c_p, c_p]),
+    "bcm_extract_fill_blocks": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p, c_p, c_p, c_p,
+                                        c_p, c_p, c_p]),
     "bcm_expand_events": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p, c_p, c_p, c_p]),
     "bcm_seqlen_max": (c_i32, [c_p, c_i64, c_p, c_p]),
     "bcm_gather_fwd": (c_i32, [c_p, c_i32, c_i64, c_i64, c_p, c_p, c_i64, c_p, c_p]),

@@ -19,13 +19,35 @@
 namespace bcm {
 
 // ------------------------------------------------------------------ count
+// Sum and maximum of the block's row counts (one value per wave, uniform in
+// the wave) to bsum[blockIdx] / bmax[blockIdx]. Every wave of the block
+// calls it once (rows past the end with 0).
+__device__ __forceinline__ void block_totals(int cnt, int32_t* bsum, int32_t* bmax) {
+  __shared__ int s_c[4];
+  if (lane_id() == 0) s_c[threadIdx.x / kWave] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int sm = 0, mx = 0;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+      sm += s_c[w];
+      mx = max(mx, s_c[w]);
+    }
+    bsum[blockIdx.x] = sm;
+    bmax[blockIdx.x] = mx;
+  }
+}
+
 // One wave per row. A batch of up to 8 groups (8 x 16 bytes per lane) is
 // loaded before any of it is used, so a row of 2048 fp32 steps is one round
 // trip to memory.
-template <typename T, bool VEC>
+// BLK: each block also writes its rows' event sum and maximum row count to
+// bsum[blk] / bmax[blk] (one barrier, no atomics), which the fill pass turns
+// into row offsets itself (no separate offsets scan).
+template <typename T, bool VEC, bool BLK>
 __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t n_rows, int64_t L, float thr,
                                                uint32_t* __restrict__ bitmask, int64_t W,
-                                               int32_t* __restrict__ counts) {
+                                               int32_t* __restrict__ counts, int32_t* __restrict__ bsum,
+                                               int32_t* __restrict__ bmax) {
   constexpr int PER = 16 / sizeof(T);  // steps per lane per group
   constexpr int GS = kWave * PER;      // steps per group
   constexpr int LPW = 32 / PER;        // lanes per 32-bit word
@@ -33,59 +55,63 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   constexpr int BATCH = 8;
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  if (row >= n_rows) return;
-  const T* xr = x + row * L;
-  uint32_t* br = bitmask + row * W;
-  int cnt = 0;
-  const int64_t ng = (L + GS - 1) / GS;
-  for (int64_t g0 = 0; g0 < ng; g0 += BATCH) {
-    uint32_t bits[BATCH];
-    if (VEC && (g0 + BATCH) * GS <= L) {
-      uint4 raw[BATCH];
+  // the row's bits and event count (0 for a row past the end)
+  auto count_row = [&]() {
+    const T* xr = x + row * L;
+    uint32_t* br = bitmask + row * W;
+    int cnt = 0;
+    const int64_t ng = (L + GS - 1) / GS;
+    for (int64_t g0 = 0; g0 < ng; g0 += BATCH) {
+      uint32_t bits[BATCH];
+      if (VEC && (g0 + BATCH) * GS <= L) {
+        uint4 raw[BATCH];
 #pragma unroll
-      for (int i = 0; i < BATCH; ++i) {
-        const u32x4 t = ld_stream(reinterpret_cast<const u32x4*>(xr + (g0 + i) * GS + lane * PER));
-        __builtin_memcpy(&raw[i], &t, 16);
-      }
+        for (int i = 0; i < BATCH; ++i) {
+          const u32x4 t = ld_stream(reinterpret_cast<const u32x4*>(xr + (g0 + i) * GS + lane * PER));
+          __builtin_memcpy(&raw[i], &t, 16);
+        }
 #pragma unroll
-      for (int i = 0; i < BATCH; ++i) {
-        const T* v = reinterpret_cast<const T*>(&raw[i]);
-        bits[i] = 0;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
-      }
-    } else {  // tail batch: full groups still use 16-byte loads
-#pragma unroll
-      for (int i = 0; i < BATCH; ++i) {
-        const int64_t t0 = (g0 + i) * GS + (int64_t)lane * PER;
-        bits[i] = 0;
-        if (VEC && t0 + PER <= L) {
-          const u32x4 raw = ld_stream(reinterpret_cast<const u32x4*>(xr + t0));
-          const T* v = reinterpret_cast<const T*>(&raw);
+        for (int i = 0; i < BATCH; ++i) {
+          const T* v = reinterpret_cast<const T*>(&raw[i]);
+          bits[i] = 0;
 #pragma unroll
           for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
-        } else {
+        }
+      } else {  // tail batch: full groups still use 16-byte loads
 #pragma unroll
-          for (int e = 0; e < PER; ++e)
-            if (t0 + e < L) bits[i] |= (uint32_t)(to_f(xr[t0 + e]) > thr) << e;
+        for (int i = 0; i < BATCH; ++i) {
+          const int64_t t0 = (g0 + i) * GS + (int64_t)lane * PER;
+          bits[i] = 0;
+          if (VEC && t0 + PER <= L) {
+            const u32x4 raw = ld_stream(reinterpret_cast<const u32x4*>(xr + t0));
+            const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+            for (int e = 0; e < PER; ++e) bits[i] |= (uint32_t)(to_f(v[e]) > thr) << e;
+          } else {
+#pragma unroll
+            for (int e = 0; e < PER; ++e)
+              if (t0 + e < L) bits[i] |= (uint32_t)(to_f(xr[t0 + e]) > thr) << e;
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) {
+        if (g0 + i < ng) {
+          cnt += __popc(bits[i]);
+          // pack the lanes' PER-bit pieces of one 32-step word (DPP, no LDS)
+          uint32_t w = bits[i] << (PER * (lane % LPW));
+          if constexpr (LPW >= 2) w |= dpp<kDppXor1>(w);
+          if constexpr (LPW >= 4) w |= dpp<kDppXor2>(w);
+          if constexpr (LPW >= 8) w |= dpp<kDppHalfMirror>(w);
+          if (lane % LPW == 0) br[(g0 + i) * WPG + lane / LPW] = w;
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < BATCH; ++i) {
-      if (g0 + i < ng) {
-        cnt += __popc(bits[i]);
-        // pack the lanes' PER-bit pieces of one 32-step word (DPP, no LDS)
-        uint32_t w = bits[i] << (PER * (lane % LPW));
-        if constexpr (LPW >= 2) w |= dpp<kDppXor1>(w);
-        if constexpr (LPW >= 4) w |= dpp<kDppXor2>(w);
-        if constexpr (LPW >= 8) w |= dpp<kDppHalfMirror>(w);
-        if (lane % LPW == 0) br[(g0 + i) * WPG + lane / LPW] = w;
-      }
-    }
-  }
-  cnt = wave_sum(cnt);
-  if (lane == 0) counts[row] = cnt;
+    return wave_sum(cnt);
+  };
+  const int cnt = row < n_rows ? count_row() : 0;
+  if (row < n_rows && lane == 0) counts[row] = cnt;
+  if constexpr (BLK) block_totals(cnt, bsum, bmax);  // every wave, one barrier
 }
 
 // ------------------------------------------------------------------- scan
@@ -155,32 +181,94 @@ __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict_
 // ------------------------------------------------------------------- fill
 constexpr int kFillSeg = 64 * 32;  // steps per segment (one word per lane)
 
-template <typename T, bool GATHER, bool TILES>
+// BLK: the row offsets come from the count pass's block sums (bsum/bmax,
+// one per 4 rows): the block adds up the sums of the blocks before it and
+// the counts of its rows before each row, and writes cu_seqlens itself.
+// Block 0 also writes meta = (E, max count) (one 64-bit store written
+// through to memory, so a host may poll it while the fill runs).
+template <typename T, bool GATHER, bool TILES, bool BLK>
 __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitmask, int64_t W,
                                               const int32_t* __restrict__ base_cu, int64_t n_rows, int64_t L,
                                               int expand, const T* __restrict__ x, int32_t* __restrict__ ch_ids,
                                               int32_t* __restrict__ t_steps, int32_t* __restrict__ k_flat,
                                               T* __restrict__ x_ev, int32_t* __restrict__ tile_start, int64_t nT,
-                                              int32_t* __restrict__ head_flags) {
+                                              int32_t* __restrict__ head_flags, const int32_t* __restrict__ counts,
+                                              const int32_t* __restrict__ bsum, const int32_t* __restrict__ bmax,
+                                              int32_t* __restrict__ meta, int32_t* __restrict__ cu_out) {
   __shared__ int32_t s_t[4][kFillSeg];
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int64_t c = (int64_t)blockIdx.x * 4 + wave;
-  if (c >= n_rows) return;
-  const int32_t cu0 = base_cu[c];
-  const int32_t n = base_cu[c + 1] - cu0;
+  // the first segment's bitmask word does not depend on the offsets: its
+  // load is in flight while they are worked out
+  const bool live = c < n_rows;
+  const int64_t nwords = (L + 31) / 32;
+  const uint32_t* br = bitmask + (live ? c : 0) * W;
+  const uint32_t word_first = (live && lane < nwords) ? br[lane] : 0u;
+  int32_t cu0, n;
+  if constexpr (BLK) {
+    __shared__ int s_part[4][2];
+    const int64_t r0 = (int64_t)blockIdx.x * 4;
+    int cb[4];  // the block's row counts
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cb[q] = r0 + q < n_rows ? counts[r0 + q] : 0;
+    const int64_t nblk = (n_rows + 3) / 4;
+    const bool first = blockIdx.x == 0;
+    int sm = 0, mx = 0;  // blocks before this one (all blocks for block 0's totals)
+    const int64_t lim = first ? nblk : (int64_t)blockIdx.x;
+    for (int64_t i0 = 0; i0 < lim; i0 += 8 * (int64_t)blockDim.x) {  // 8 independent loads per thread in flight
+      int vs[8], vm[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int64_t i = i0 + q * (int64_t)blockDim.x + threadIdx.x;
+        vs[q] = i < lim ? bsum[i] : 0;
+        vm[q] = (first && i < lim) ? bmax[i] : 0;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        sm += vs[q];
+        mx = max(mx, vm[q]);
+      }
+    }
+    sm = wave_sum(sm);
+    mx = wave_max(mx);
+    if (lane == 0) {
+      s_part[wave][0] = sm;
+      s_part[wave][1] = mx;
+    }
+    __syncthreads();
+    int before = 0, total_max = 0;
+    for (int w = 0; w < 4; ++w) {
+      before += s_part[w][0];
+      total_max = max(total_max, s_part[w][1]);
+    }
+    if (first && threadIdx.x == 0) {
+      const uint64_t packed = (uint64_t)(uint32_t)before | ((uint64_t)(uint32_t)total_max << 32);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(meta), packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    if (first) before = 0;
+    if (!live) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) before += q < wave ? cb[q] : 0;
+    cu0 = before;
+    n = cb[wave];
+    for (int r = lane; r < expand; r += kWave) cu_out[c * expand + r] = cu0 * expand + r * n;
+    if (c == n_rows - 1 && lane == 0) cu_out[n_rows * expand] = (cu0 + n) * expand;
+  } else {
+    if (!live) return;
+    cu0 = base_cu[c];
+    n = base_cu[c + 1] - cu0;
+  }
   if (TILES && lane == 0) {
     for (int r = 0; r < expand; ++r)
       tile_start[(c * expand + r) * (nT + 1) + nT] = cu0 * expand + r * n + n;
   }
   if (n <= 0 && !TILES) return;
-  const uint32_t* br = bitmask + c * W;
-  const int64_t nwords = (L + 31) / 32;
   int32_t* st = s_t[wave];
   int prev_t = -1;
   int off = 0;
   for (int64_t w0 = 0; w0 < nwords; w0 += kWave) {
     const int64_t w = w0 + lane;
-    const uint32_t word = w < nwords ? br[w] : 0u;
+    const uint32_t word = w0 == 0 ? word_first : (w < nwords ? br[w] : 0u);
     const int pc = __popc(word);
     const int incl = wave_incl_sum(pc);
     const int excl = incl - pc;
@@ -414,8 +502,12 @@ int bcm_extract_count(const void* membrane, int dtype, int64_t n_rows, int64_t L
   auto go = [&](auto tag) {
     using T = decltype(tag);
     const T* x = static_cast<const T*>(membrane);
-    if (vec) hipLaunchKernelGGL((k_count<T, true>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W, counts);
-    else hipLaunchKernelGGL((k_count<T, false>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W, counts);
+    if (vec)
+      hipLaunchKernelGGL((k_count<T, true, false>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W,
+                         counts, nullptr, nullptr);
+    else
+      hipLaunchKernelGGL((k_count<T, false, false>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W,
+                         counts, nullptr, nullptr);
   };
   if (dtype == BCM_U8) go(uint8_t{});
   else dispatch_dtype(dtype, go);
@@ -454,13 +546,79 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_
     using T = decltype(tag);
     constexpr bool G = decltype(gather)::value;
     constexpr bool TT = decltype(tiles)::value;
-    hipLaunchKernelGGL((k_fill<T, G, TT>), grid, block, 0, hs(stream), bitmask, W, base_cu, n_rows, L, ex,
+    hipLaunchKernelGGL((k_fill<T, G, TT, false>), grid, block, 0, hs(stream), bitmask, W, base_cu, n_rows, L, ex,
                        static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
-                       head_flags);
+                       head_flags, nullptr, nullptr, nullptr, nullptr, nullptr);
   };
   using Y = std::true_type;
   using N = std::false_type;
   if (!k_flat) return set_error(BCM_EINVAL, "%s: null output pointer", fn);
+  if (x) {
+    dispatch_dtype(x_dtype, [&](auto tag) {
+      if (tile_start) launch(tag, Y{}, Y{});
+      else launch(tag, Y{}, N{});
+    });
+  } else {
+    if (tile_start) launch(float{}, N{}, Y{});
+    else launch(float{}, N{}, N{});
+  }
+  return check_launch(fn);
+}
+
+int64_t bcm_extract_block_sums_bytes(int64_t n_rows) { return n_rows < 0 ? 0 : 8 * ((n_rows + 3) / 4); }
+
+int bcm_extract_count_blocks(const void* membrane, int dtype, int64_t n_rows, int64_t L, float threshold,
+                             uint32_t* bitmask, int32_t* counts, int32_t* block_sums, bcm_stream_t stream) {
+  const char* fn = "bcm_extract_count_blocks";
+  if (!dtype_ok(dtype) && dtype != BCM_U8) return set_error(BCM_EINVAL, "%s: membrane must be fp32, fp16, bf16 or u8", fn);
+  if (n_rows < 1 || L < 1) return set_error(BCM_EINVAL, "%s: n_rows and L must be positive", fn);
+  if (!membrane || !bitmask || !counts || !block_sums) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_rows * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: n_rows * L must fit in int32", fn);
+  const int64_t W = bitmask_words(L), nblk = (n_rows + 3) / 4;
+  const bool vec = aligned(membrane, 16) && ((L * (int64_t)dtype_size(dtype)) % 16 == 0);
+  const dim3 grid((unsigned)nblk), block(256);
+  auto go = [&](auto tag) {
+    using T = decltype(tag);
+    const T* x = static_cast<const T*>(membrane);
+    if (vec)
+      hipLaunchKernelGGL((k_count<T, true, true>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W,
+                         counts, block_sums, block_sums + nblk);
+    else
+      hipLaunchKernelGGL((k_count<T, false, true>), grid, block, 0, hs(stream), x, n_rows, L, threshold, bitmask, W,
+                         counts, block_sums, block_sums + nblk);
+  };
+  if (dtype == BCM_U8) go(uint8_t{});
+  else dispatch_dtype(dtype, go);
+  return check_launch(fn);
+}
+
+int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts, const int32_t* block_sums,
+                            int32_t* meta, int64_t n_rows, int64_t L, int64_t expand, const void* x, int x_dtype,
+                            int32_t* cu_seqlens, int32_t* ch_ids, int32_t* t_steps, int32_t* k_flat,
+                            void* x_events, int32_t* tile_start, bcm_stream_t stream) {
+  const char* fn = "bcm_extract_fill_blocks";
+  if (n_rows < 1 || L < 1 || expand < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (!bitmask || !counts || !block_sums || !meta || !cu_seqlens || !k_flat)
+    return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!aligned(meta, 8)) return set_error(BCM_EINVAL, "%s: meta must be 8-byte aligned", fn);
+  if ((x == nullptr) != (x_events == nullptr))
+    return set_error(BCM_EINVAL, "%s: x and x_events must both be given or both be NULL", fn);
+  if (x && !dtype_ok(x_dtype)) return set_error(BCM_EINVAL, "%s: x must be fp32, fp16 or bf16", fn);
+  if (n_rows * expand * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: rows * expand * L must fit in int32", fn);
+  if (tile_start && !aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  const int64_t W = bitmask_words(L), nT = tile_count(L), nblk = (n_rows + 3) / 4;
+  const dim3 grid((unsigned)nblk), block(256);
+  const int ex = (int)expand;
+  auto launch = [&](auto tag, auto gather, auto tiles) {
+    using T = decltype(tag);
+    constexpr bool G = decltype(gather)::value;
+    constexpr bool TT = decltype(tiles)::value;
+    hipLaunchKernelGGL((k_fill<T, G, TT, true>), grid, block, 0, hs(stream), bitmask, W, nullptr, n_rows, L, ex,
+                       static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
+                       nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens);
+  };
+  using Y = std::true_type;
+  using N = std::false_type;
   if (x) {
     dispatch_dtype(x_dtype, [&](auto tag) {
       if (tile_start) launch(tag, Y{}, Y{});

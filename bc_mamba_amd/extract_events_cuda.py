@@ -165,19 +165,10 @@ def gather_events_bwd(grad_x, channel_ids, time_steps, NC, L):
     return [dx]
 
 
-def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True):
-    """Fused extraction for the block forward (no reference counterpart; the
-    reference composes extract_base_events + expand_base_events +
-    gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
-    max_seqlen as a Python int, x_events or None, event_index) where
-    event_index = (bitmask, tile_start, expand) feeds the restore and the
-    row-wise gather backward. With positions=False channel_ids and
-    time_steps are None and never written (the indexed restore and gather
-    do not use them). One host sync (E and max_seqlen together)."""
-    _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
-           "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
+def _extract_indexed_exact(base_input, threshold, expand, x, positions):
+    """extract_events_indexed with the separate offsets pass: E is read
+    before the fill, which then writes exactly E events."""
     B, Dm, L = base_input.shape
-    expand = int(expand)
     dev = base_input.device
     with torch.cuda.device(dev):
         x2d = base_input.view(B * Dm, L)
@@ -194,12 +185,64 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
         k = _empty_i32(E, dev)
         ch, t = (_empty_i32(E, dev), _empty_i32(E, dev)) if positions else (None, None)
         tile_start = torch.empty((NCi, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
-        xe = None
-        if x is not None:
-            _check(x.is_cuda and x.is_contiguous() and tuple(x.shape) == (B, Dm * expand, L),
-                   "x must be a contiguous CUDA tensor [B, d_model*expand, L]")
-            xe = torch.empty(E, dtype=x.dtype, device=dev)
-        _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(base_cu), B * Dm, L, expand,
-                  _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(ch), _nat.ptr(t),
-                  _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), None, s)
+        xe = torch.empty(E, dtype=x.dtype, device=dev) if x is not None else None
+        if B * Dm > 0 and L > 0:
+            _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(base_cu), B * Dm, L, expand,
+                      _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(ch), _nat.ptr(t),
+                      _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), None, s)
+        return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)
+
+
+def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True, exact_alloc=False):
+    """Fused extraction for the block forward (no reference counterpart; the
+    reference composes extract_base_events + expand_base_events +
+    gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
+    max_seqlen as a Python int, x_events or None, event_index) where
+    event_index = (bitmask, tile_start, expand) feeds the restore and the
+    row-wise gather backward. With positions=False channel_ids and
+    time_steps are None and never written (the indexed restore and gather
+    do not use them). One host sync (E and max_seqlen together).
+
+    By default the fill derives the row offsets itself from the count pass's
+    block sums (no offsets kernel) and is enqueued before E is known, so its
+    event outputs are allocated for every possible event (B*d_model*expand*L)
+    and returned as views of the first E. exact_alloc=True runs the separate
+    offsets pass, reads E first and allocates exactly E."""
+    _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
+           "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
+    B, Dm, L = base_input.shape
+    expand = int(expand)
+    dev = base_input.device
+    NC = B * Dm
+    if x is not None:
+        _check(x.is_cuda and x.is_contiguous() and tuple(x.shape) == (B, Dm * expand, L),
+               "x must be a contiguous CUDA tensor [B, d_model*expand, L]")
+    if exact_alloc or NC == 0 or L == 0:
+        return _extract_indexed_exact(base_input, threshold, expand, x, positions)
+    with torch.cuda.device(dev):
+        x2d = base_input.view(NC, L)
+        s = _nat.stream_of(x2d)
+        NCi, cap = NC * expand, NC * expand * L
+        bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
+        counts = _empty_i32(NC, dev)
+        bsums = _empty_i32(_nat.lib().bcm_extract_block_sums_bytes(NC) // 4, dev)
+        cu = _empty_i32(NCi + 1, dev)
+        k = _empty_i32(cap, dev)
+        ch, t = (_empty_i32(cap, dev), _empty_i32(cap, dev)) if positions else (None, None)
+        tile_start = torch.empty((NCi, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
+        xe = torch.empty(cap, dtype=x.dtype, device=dev) if x is not None else None
+        meta = _nat.HostMeta()
+        meta.arm()
+        _nat.call("bcm_extract_count_blocks", _nat.ptr(x2d), _nat.dtype_code(base_input.dtype), NC, L,
+                  float(threshold), _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), s)
+        _nat.call("bcm_extract_fill_blocks", _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), meta.ptr(), NC,
+                  L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(cu),
+                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
+        E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
+        E = E_base * expand
+        k = k[:E]
+        if positions:
+            ch, t = ch[:E], t[:E]
+        if xe is not None:
+            xe = xe[:E]
         return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)

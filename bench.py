@@ -2,7 +2,8 @@
 
 One step = one fwd+bwd pass of the whole path over the config's synthetic
 batch, inputs resident in HBM:
-  forward : extract (count -> offsets -> fill, with x_conv gathered at the
+  forward : extract (count -> fill, the fill deriving the row offsets
+            from the count pass's block sums, with x_conv gathered at the
             events and the event index built in the same pass; the host
             reads E while fill runs) -> flat selective scan ->
             zero-order-hold restore
@@ -29,7 +30,7 @@ PROBE_STEPS = 5
 CAL_BYTES = 256 << 20  # device-to-device copy that calibrates the PMC byte counters
 
 # device kernels behind each stage of Path.KERNELS (symbol substrings)
-STAGE_KERNELS = {"count": ["k_count"], "offsets": ["k_scan_counts"], "fill": ["k_fill"],
+STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
                  "scan_fwd": ["k_scan_fwd"], "restore_fwd": ["k_restore_fwd"],
                  "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"], "scan_bwd": ["k_scan_bwd"],
                  "gather_bwd": ["k_gather_bwd_rows"]}
@@ -60,10 +61,11 @@ class Path:
 
     Event buffers are sized for the largest possible event count (every
     step of every channel), so the fill kernel can be enqueued before the
-    host has read E: the host waits on an event recorded after the offsets
-    kernel while fill runs, and the GPU never idles on the round trip."""
+    host has read E: the fill writes E and max_seqlen to pinned memory early,
+    the host polls it while fill runs, and the GPU never idles on the round
+    trip."""
 
-    KERNELS = ["count", "offsets", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd", "gather_bwd"]
+    KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd", "gather_bwd"]
 
     def __init__(self, w, dev):
         import torch
@@ -76,6 +78,7 @@ class Path:
         self.counts = torch.empty(self.NC, **i32)
         self.cu = torch.empty(self.NC + 1, **i32)
         self.meta_h = nat.HostMeta()
+        self.bsums = torch.empty(nat.lib().bcm_extract_block_sums_bytes(self.NC) // 4, **i32)
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
@@ -125,16 +128,17 @@ class Path:
                 fn()
 
         B, D, L = w.B, w.D, w.L
-        mark("count", lambda: nat.call("bcm_extract_count", P(w.membrane), nat.dtype_code(w.membrane.dtype),
-                                       self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), s))
-        # (E, max_seqlen) go straight to pinned host memory: no copy kernel,
-        # no event (the host polls while fill runs)
+        # count also writes per-block sums; fill derives the row offsets from
+        # them, writes cu and sends (E, max_seqlen) straight to pinned host
+        # memory (no offsets kernel, no copy kernel, no event: the host polls
+        # while fill runs)
         self.meta_h.arm()
-        mark("offsets", lambda: nat.call("bcm_extract_scan", P(self.counts), self.NC, P(self.cu), self.meta_h.ptr(),
-                                         s))
-        mark("fill", lambda: nat.call("bcm_extract_fill", P(self.bitmask), P(self.cu), self.NC, L, 1, P(w.x_conv),
-                                      nat.dtype_code(w.dtype), None, None, P(self.k), P(self.u),
-                                      P(self.tile_start), None, s))
+        mark("count", lambda: nat.call("bcm_extract_count_blocks", P(w.membrane), nat.dtype_code(w.membrane.dtype),
+                                       self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), P(self.bsums),
+                                       s))
+        mark("fill", lambda: nat.call("bcm_extract_fill_blocks", P(self.bitmask), P(self.counts), P(self.bsums),
+                                      self.meta_h.ptr(), self.NC, L, 1, P(w.x_conv), nat.dtype_code(w.dtype),
+                                      P(self.cu), None, None, P(self.k), P(self.u), P(self.tile_start), s))
         E, ms = self.meta_h.wait(t.cuda.current_stream())  # fill keeps the GPU busy meanwhile
         if E != self.E or ms != self.ms:
             self.E, self.ms = E, ms
@@ -318,7 +322,7 @@ def main():
     alg = algorithmic_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su)
     total_bytes = sum(alg.values())
     # algorithmic bytes of one launch of each kernel (its share of the API-contract traffic)
-    kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC, "offsets": 8 * path.NC,
+    kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC,
                     "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
                     "restore_fwd": alg["fwd_restore"], "restore_bwd": alg["bwd_restore"],
                     "scan_bwd": alg["bwd_scan"], "gather_bwd": alg["bwd_gather"]}

@@ -94,6 +94,33 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu,
                      int32_t* tile_start, int32_t* head_flags,
                      bcm_stream_t stream);
 
+/* Passes 1-3 without a separate offsets pass (no reference counterpart: it
+ * replaces the DeviceScan of extract_events_cuda.cu:361-372 in the fused
+ * model path, one kernel fewer).
+ * bcm_extract_count_blocks: as bcm_extract_count; each block of 4 rows also
+ * writes its rows' event sum and maximum count to block_sums
+ * [2][ceil(n_rows/4)] int32 (bcm_extract_block_sums_bytes).
+ * bcm_extract_fill_blocks: as bcm_extract_fill, each block deriving its
+ * rows' offsets from block_sums and counts; it writes cu_seqlens
+ * [n_rows*expand+1] (logical channels) and meta = (E_base, max count) as
+ * bcm_extract_scan does (one 64-bit store written through to memory: a host
+ * that set meta[0] = -1 may poll pinned meta while the fill runs). Since E
+ * is not known when the fill is enqueued, its event outputs must be sized
+ * for every possible event (n_rows*expand*L). ch_ids, t_steps, x / x_events
+ * and tile_start are optional (NULL to skip). */
+int64_t bcm_extract_block_sums_bytes(int64_t n_rows);
+int bcm_extract_count_blocks(const void* membrane, int dtype, int64_t n_rows,
+                             int64_t L, float threshold, uint32_t* bitmask,
+                             int32_t* counts, int32_t* block_sums,
+                             bcm_stream_t stream);
+int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts,
+                            const int32_t* block_sums, int32_t* meta,
+                            int64_t n_rows, int64_t L, int64_t expand,
+                            const void* x, int x_dtype, int32_t* cu_seqlens,
+                            int32_t* ch_ids, int32_t* t_steps,
+                            int32_t* k_flat, void* x_events,
+                            int32_t* tile_start, bcm_stream_t stream);
+
 /* expand_base_events (extract_events_cuda.cu:529-603): logical cu_seqlens
  * [n_rows*expand+1] and expanded streams [E_base*expand]. */
 int bcm_expand_events(const int32_t* base_ch, const int32_t* base_t,

@@ -156,3 +156,36 @@ def test_gather_bwd_rows_matches_scatter(cuda_device):
     nat.call("bcm_gather_bwd_rows", nat.ptr(g), nat.F32, nat.ptr(bitmask), expand, nat.ptr(tile_start),
              B * Dm * expand, L, nat.ptr(dx), nat.stream_of(g))
     assert torch.equal(dx, ee.gather_events_bwd(g, ch, t, B * Dm * expand, L)[0])
+
+
+@pytest.mark.parametrize("NC,L,p,expand", [(1, 1, 0.5, 1), (3, 100, 0.3, 1), (64, 2048, 0.15, 1), (65, 64, 0.9, 2),
+                                           (1001, 333, 0.2, 1), (8192, 64, 0.15, 1), (10, 700, 0.25, 3)])
+def test_block_offsets_match_scan(cuda_device, NC, L, p, expand):
+    """count with per-block sums + fill deriving its own row offsets give the
+    cu_seqlens, k, gathered x, tile table and (E, max) of the composition
+    with the separate offsets scan."""
+    from bc_mamba_amd import _native as nat
+    mem = _membrane(1, NC, L, p, torch.float32, 31).to(cuda_device)
+    x = torch.randn(1, NC * expand, L, generator=torch.Generator().manual_seed(32)).to(cuda_device)
+    ch, t, k, cu, ms, xe, (bitmask, tile_start, _) = ee.extract_events_indexed(mem, 0.5, expand, x,
+                                                                                exact_alloc=True)
+    E = k.numel()
+    s = nat.stream_of(mem)
+    i32 = dict(dtype=torch.int32, device=cuda_device)
+    bm = torch.empty((NC, nat.bitmask_words(L)), **i32)
+    counts = torch.empty(NC, **i32)
+    bsums = torch.empty(nat.lib().bcm_extract_block_sums_bytes(NC) // 4, **i32)
+    cap = NC * expand * L
+    cu2, k2 = torch.empty(NC * expand + 1, **i32), torch.empty(cap, **i32)
+    xe2 = torch.empty(cap, dtype=x.dtype, device=cuda_device)
+    ts2 = torch.empty_like(tile_start)
+    meta = nat.HostMeta()
+    meta.arm()
+    nat.call("bcm_extract_count_blocks", nat.ptr(mem), nat.F32, NC, L, 0.5, nat.ptr(bm), nat.ptr(counts),
+             nat.ptr(bsums), s)
+    nat.call("bcm_extract_fill_blocks", nat.ptr(bm), nat.ptr(counts), nat.ptr(bsums), meta.ptr(), NC, L, expand,
+             nat.ptr(x), nat.F32, nat.ptr(cu2), None, None, nat.ptr(k2), nat.ptr(xe2), nat.ptr(ts2), s)
+    E2, ms2 = meta.wait(torch.cuda.current_stream(cuda_device))
+    assert E2 * expand == E and ms2 == ms
+    assert torch.equal(cu2, cu) and torch.equal(k2[:E], k) and torch.equal(xe2[:E], xe)
+    assert torch.equal(ts2, tile_start)
