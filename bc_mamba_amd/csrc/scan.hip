@@ -57,7 +57,8 @@ struct FwdLds {
   int N, nw, G, R, nslots;
   bool tbl;
   int64_t bytes() const {
-    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 3ll * N + 2ll * nw * kWave * (R + 1) +
+    (void)tbl;  // the decay table is static LDS
+    return 4ll * (3ll * N + 2ll * nw * kWave * (R + 1) +
                   (int64_t)nslots * 2 * N);
   }
 };
@@ -66,7 +67,8 @@ struct BwdLds {
   int N, nw, G, R, nslots;
   bool tbl;
   int64_t bytes() const {
-    return 4ll * ((tbl ? (int64_t)N * kTabStride : 0) + 6ll * N + 2ll * nw * kWave * (R + 1) +
+    (void)tbl;  // the decay table is static LDS
+    return 4ll * (6ll * N + 2ll * nw * kWave * (R + 1) +
                   (int64_t)nslots * (2 * N + 3 * N + 3));
   }
 };
@@ -232,9 +234,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   const int nslots = nw * CPW;
   const int slot = wave * CPW + grp;
 
+  // the decay table is static LDS: its address is a compile-time constant,
+  // which the table reads take as their instruction offset
+  __shared__ float sTab[TBL ? kTabMaxN * kTabStride : 1];
   extern __shared__ float smem[];
-  float* sT = smem;
-  float* sAl = sT + (TBL ? N * kTabStride : 0);
+  float* sT = sTab;
+  float* sAl = smem;
   float* sWB = sAl + N;
   float* sWBC = sWB + N;
   // the group's staging tiles for u and k (the u tile also stages y)
@@ -459,9 +464,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   const int slot = wave * CPW + grp;
   const int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
 
+  // the decay table is static LDS: its address is a compile-time constant,
+  // which the table reads take as their instruction offset
+  __shared__ float sTab[TBL ? kTabMaxN * kTabStride : 1];
   extern __shared__ float smem[];
-  float* sT = smem;
-  float* sAl = sT + (TBL ? N * kTabStride : 0);
+  float* sT = sTab;
+  float* sAl = smem;
   float* sWB = sAl + N;
   float* sWC = sWB + N;
   float* sWBC = sWC + N;
