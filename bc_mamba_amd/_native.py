@@ -35,6 +35,19 @@ class ScanArgs(ctypes.Structure):
     ]
 
 
+class ScanBC(ctypes.Structure):
+    """Mirror of bcm_scan_bc (field order and types must match the header)."""
+
+    _fields_ = [
+        ("layout", c_i32), ("b_per_event", c_i32), ("c_per_event", c_i32), ("tile_chunk_size", c_i32),
+        ("b_row_stride", c_i64), ("c_row_stride", c_i64), ("n_tiles", c_i64),
+        ("tile_offsets", c_p), ("B", c_p), ("C", c_p), ("dB", c_p), ("dC", c_p),
+        ("db_row_stride", c_i64), ("dc_row_stride", c_i64),
+    ]
+
+
+BC_LEGACY, BC_TILED = 1, 2
+
 # name -> (restype, argtypes); exactly the functions declared in the header.
 SIGNATURES = {
     "bcm_abi_version": (c_i32, []),
@@ -56,6 +69,9 @@ SIGNATURES = {
     "bcm_gather_bwd_rows": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p]),
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_scan_var_fwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p]),
+    "bcm_scan_var_workspace_bytes": (c_i64, [c_i64, c_i32]),
+    "bcm_scan_var_bwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p, c_i64, c_p]),
     "bcm_build_event_index": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p, c_p, c_i64, c_p]),
     "bcm_restore_fwd": (c_i32, [c_p, c_i32, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_p]),
     "bcm_restore_bwd_workspace_bytes": (c_i64, [c_i64, c_i64]),

@@ -3,11 +3,19 @@
 backed by the HIP scan kernels of libbcm_event_scan.so.
 
 fwd_flat_ch / bwd_flat_ch keep the reference's keyword names, defaults,
-return lists and check messages. Implemented mode: depthwise B/C
-(is_depthwise_bc=True, the only mode the BC_mamba block uses), with optional
-D and z. The legacy [dstate, E] variable-B/C layout, the tiled layout and the
-pointwise pw_B/pw_C mixing raise RuntimeError. The dense `fwd` / `bwd`
-entry points of the reference module are not part of this build.
+return lists and check messages, in every B/C mode the reference accepts:
+  depthwise (is_depthwise_bc=True)  B, C = W_B, W_C [dim, dstate]; the
+      BC_mamba block's mode, on the tuned kernels bcm_scan_fwd / _bwd;
+  depthwise + pointwise (pw_B, pw_C [dim, dim])  the scan runs on
+      W_eff = pw @ W (selective_scan_fwd_kernel.cuh:486-509) and the
+      backward maps dW_eff to dW = pw^T dW_eff and dpw = dW_eff W^T
+      (selective_scan_bwd_kernel.cuh:1122-1166); the two small products are
+      plain library GEMMs;
+  legacy (is_depthwise_bc=False)  B, C [dstate, E] per event (the backward
+      also takes [dstate, dim] per model channel);
+  tiled (tile_offsets given)  B, C [n_tiles, dstate, tile_chunk_size];
+the last two on bcm_scan_var_fwd / _bwd. The dense `fwd` / `bwd` entry
+points of the reference module are not part of this build.
 """
 import torch
 
@@ -32,7 +40,9 @@ def n_chunks_for(max_seqlen):
 
 
 def _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D,
-                   tile_offsets, is_depthwise_bc, pw_B, pw_C, extra_cuda=()):
+                   tile_offsets, is_depthwise_bc, pw_B, pw_C, extra_cuda=(), bwd=False, tile_chunk_size=0):
+    """The reference's checks (selective_scan.cpp:697-781, 939-998); returns
+    (dim, dstate, mode) with mode "depthwise", "tiled" or "legacy"."""
     _check(u_flat.dtype in _FLOATS, f"{fn}: u_flat must be fp16/bf16/fp32")
     _check(A.dtype == torch.float32, f"{fn}: A must be float32")
     _check(B.dtype == torch.float32, f"{fn}: B must be float32")
@@ -54,22 +64,76 @@ def _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_activ
     _check(dstate <= 256, f"{fn}: dstate must be <= 256")
     _check(tuple(dt_idle.shape) == (dim,), f"{fn}: dt_idle must have shape ({dim},)")
     _check(tuple(dt_active.shape) == (dim,), f"{fn}: dt_active must have shape ({dim},)")
+    E = int(u_flat.size(0))
     use_tiled = tile_offsets is not None
-    if use_tiled or not is_depthwise_bc:
-        raise RuntimeError(f"{fn}: only the depthwise B/C mode (is_depthwise_bc=True, no tile_offsets) "
-                           "is implemented by the MI355X build")
-    _check(B.dim() == 2 and C.dim() == 2, f"{fn} (depthwise): W_B/W_C must be 2-D [dim, dstate]")
-    _check(tuple(B.shape) == (dim, dstate), f"{fn} (depthwise): W_B must be [dim, dstate]")
-    _check(tuple(C.shape) == (dim, dstate), f"{fn} (depthwise): W_C must be [dim, dstate]")
-    _check(B.is_contiguous() and C.is_contiguous(), f"{fn} (depthwise): W_B/W_C must be contiguous")
-    if pw_B is not None or pw_C is not None:
-        raise RuntimeError(f"{fn}: pointwise pw_B/pw_C mixing is not implemented by the MI355X build")
+    if is_depthwise_bc and not use_tiled:
+        _check(B.dim() == 2 and C.dim() == 2, f"{fn} (depthwise): W_B/W_C must be 2-D [dim, dstate]")
+        _check(tuple(B.shape) == (dim, dstate), f"{fn} (depthwise): W_B must be [dim, dstate]")
+        _check(tuple(C.shape) == (dim, dstate), f"{fn} (depthwise): W_C must be [dim, dstate]")
+        _check(B.is_contiguous() and C.is_contiguous(), f"{fn} (depthwise): W_B/W_C must be contiguous")
+        if pw_B is not None:
+            _check(pw_C is not None, f"{fn}: pw_C is required with pw_B")
+            _check(pw_B.dtype == torch.float32 and pw_C.dtype == torch.float32, f"{fn}: pw_B/pw_C must be float32")
+            _check(pw_B.is_cuda and pw_C.is_cuda and pw_B.is_contiguous() and pw_C.is_contiguous(),
+                   f"{fn}: pw_B/pw_C must be CUDA and contiguous")
+            _check(pw_B.dim() == 2 and tuple(pw_B.shape) == (dim, dim), f"{fn}: pw_B must be [dim, dim]")
+            _check(pw_C.dim() == 2 and tuple(pw_C.shape) == (dim, dim), f"{fn}: pw_C must be [dim, dim]")
+        mode = "depthwise"
+    elif use_tiled:
+        _check(B.dim() == 3 and C.dim() == 3, f"{fn}: tiled B/C must be 3-D [N_tiles, dstate, tile_chunk_size]")
+        _check(B.size(1) == dstate and C.size(1) == dstate, f"{fn}: tiled B/C dim-1 must equal dstate")
+        _check(B.is_contiguous() and C.is_contiguous(), f"{fn}: tiled B/C must be contiguous")
+        _check(int(tile_chunk_size) >= 1 and B.size(2) == int(tile_chunk_size) and C.size(2) == int(tile_chunk_size),
+               f"{fn}: tiled B/C dim-2 must equal tile_chunk_size (>= 1)")
+        _check(B.size(0) == C.size(0), f"{fn}: tiled B and C must have the same number of tiles")
+        _check(tile_offsets.is_cuda and tile_offsets.dtype == torch.int32 and tile_offsets.dim() == 1
+               and tile_offsets.is_contiguous() and tile_offsets.size(0) >= cu_seqlens.size(0) - 1,
+               f"{fn}: tile_offsets must be a contiguous int32 CUDA tensor with one entry per channel")
+        mode = "tiled"
+    else:
+        if not bwd:
+            _check(B.dim() == 2 and C.dim() == 2, f"{fn}: B/C must be 2-D (dstate, E) [transposed layout]")
+            _check(tuple(B.shape) == (dstate, E), f"{fn}: B must have shape ({dstate}, {E})")
+            _check(tuple(C.shape) == (dstate, E), f"{fn}: C must have shape ({dstate}, {E})")
+            _check(B.stride(1) == 1 and C.stride(1) == 1,
+                   f"{fn}: B/C must have contiguous last dimension (stride(1) == 1)")
+        else:
+            _check(B.dim() == 2 and C.dim() == 2, f"{fn}: B/C must be 2-D [dstate, E] or [dstate, dim]")
+            _check(B.stride(1) == 1 and C.stride(1) == 1, f"{fn}: B/C must have contiguous last dimension")
+            for name, t in (("B", B), ("C", C)):
+                _check(t.size(0) == dstate and t.size(1) in (E, dim),
+                       f"{fn}: {name} must have shape ({dstate}, {E}) or ({dstate}, {dim})")
+        mode = "legacy"
     if D is not None:
         _check(D.dtype == torch.float32, f"{fn}: D must be float32")
         _check(D.is_cuda and D.is_contiguous(), f"{fn}: D must be a contiguous CUDA tensor")
         _check(tuple(D.shape) == (dim,), f"{fn}: D must have shape ({dim},)")
     _check(int(max_seqlen) >= 0, f"{fn}: max_seqlen must be non-negative")
-    return dim, dstate
+    return dim, dstate, mode
+
+
+def _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB=None, dC=None):
+    """bcm_scan_bc of the legacy / tiled modes. Legacy B/C are per event when
+    their second dimension is E, else per model channel, as
+    set_ssm_params_flat_seg_fwd decides (selective_scan.cpp:304-305)."""
+    bc = _nat.ScanBC()
+    bc.B, bc.C = B.data_ptr(), C.data_ptr()
+    if mode == "tiled":
+        bc.layout = _nat.BC_TILED
+        bc.b_per_event = bc.c_per_event = 1
+        bc.tile_chunk_size = int(tile_chunk_size)
+        bc.n_tiles = int(B.size(0))
+        bc.tile_offsets = tile_offsets.data_ptr()
+    else:
+        bc.layout = _nat.BC_LEGACY
+        bc.b_per_event = int(B.size(1) == E)
+        bc.c_per_event = int(C.size(1) == E)
+        bc.b_row_stride, bc.c_row_stride = int(B.stride(0)), int(C.stride(0))
+    if dB is not None:
+        bc.dB, bc.dC = dB.data_ptr(), dC.data_ptr()
+        if mode == "legacy":
+            bc.db_row_stride, bc.dc_row_stride = int(dB.stride(0)), int(dC.stride(0))
+    return bc
 
 
 def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D, z):
@@ -83,7 +147,9 @@ def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D
     a.dtype = _nat.dtype_code(u_flat.dtype)
     a.u, a.k, a.cu_seqlens = u_flat.data_ptr(), k_flat.data_ptr(), cu_seqlens.data_ptr()
     a.dt_idle, a.dt_active = dt_idle.data_ptr(), dt_active.data_ptr()
-    a.A, a.W_B, a.W_C = A.data_ptr(), B.data_ptr(), C.data_ptr()
+    a.A = A.data_ptr()
+    a.W_B = B.data_ptr() if B is not None else None
+    a.W_C = C.data_ptr() if C is not None else None
     a.D = D.data_ptr() if D is not None else None
     a.z = z.data_ptr() if z is not None else None
     return a
@@ -97,33 +163,40 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     fn = "selective_scan_fwd_flat_ch"
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous(),
            f"{fn}: u_flat/k_flat/cu_seqlens must be contiguous")
-    _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D,
-                   tile_offsets, is_depthwise_bc, pw_B, pw_C)
+    _, dstate, mode = _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D,
+                                     tile_offsets, is_depthwise_bc, pw_B, pw_C, tile_chunk_size=tile_chunk_size)
     if z is not None:
         _check(z.dtype == u_flat.dtype, f"{fn}: z must have same dtype as u_flat")
         _check(z.is_cuda and z.is_contiguous(), f"{fn}: z must be a contiguous CUDA tensor")
         _check(z.dim() == 1 and z.size(0) == u_flat.size(0), f"{fn}: z must have shape (E,)")
     dev = u_flat.device
     n_ch = int(cu_seqlens.size(0)) - 1
-    dstate = int(A.size(1))
     out = torch.empty_like(u_flat)
     x = torch.empty((n_ch, n_chunks_for(max_seqlen), dstate * 2), dtype=torch.float32, device=dev)
     out_z = torch.empty_like(u_flat) if z is not None else None
-    a = _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle.contiguous(), dt_active.contiguous(),
-              A.contiguous(), B, C, D, z)
-    a.out, a.x = out.data_ptr(), x.data_ptr()
-    a.out_z = out_z.data_ptr() if out_z is not None else None
     with torch.cuda.device(dev):
-        _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
+        if mode == "depthwise" and pw_B is not None:
+            B, C = pw_B @ B, pw_C @ C  # W_eff [dim, dstate]
+        a = _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle.contiguous(), dt_active.contiguous(),
+                  A.contiguous(), B if mode == "depthwise" else None, C if mode == "depthwise" else None, D, z)
+        a.out, a.x = out.data_ptr(), x.data_ptr()
+        a.out_z = out_z.data_ptr() if out_z is not None else None
+        if mode == "depthwise":
+            _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
+        else:
+            bc = _bc(mode, B, C, int(u_flat.size(0)), tile_offsets, tile_chunk_size)
+            _nat.call("bcm_scan_var_fwd", a, bc, _nat.stream_of(u_flat))
     return [out, x] if z is None else [out, x, out_z]
 
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
                 pw_B=None, pw_C=None):
-    """Flat per-channel scan backward -> [du, dA, dW_B, dW_C, ddt_idle,
-    ddt_active, (dD), (dz)] (selective_scan.cpp:890-1153). Parameter
-    gradients are reduced deterministically inside the kernel."""
+    """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
+    ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
+    dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
+    shape of B / C otherwise. Parameter gradients are reduced
+    deterministically inside the kernels."""
     fn = "selective_scan_bwd_flat_ch"
     _check(dout_flat.dtype == u_flat.dtype, f"{fn}: dout_flat must match u_flat dtype")
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous()
@@ -131,8 +204,9 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     _check(u_flat.dim() == 1 and k_flat.dim() == 1 and cu_seqlens.dim() == 1 and dout_flat.dim() == 1,
            f"{fn}: u_flat/k_flat/cu_seqlens/dout_flat must be 1-D")
     _check(dout_flat.size(0) == u_flat.size(0), f"{fn}: dout_flat must match u_flat shape")
-    dim, dstate = _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D,
-                                 tile_offsets, is_depthwise_bc, pw_B, pw_C, extra_cuda=(dout_flat, x))
+    dim, dstate, mode = _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D,
+                                       tile_offsets, is_depthwise_bc, pw_B, pw_C, extra_cuda=(dout_flat, x),
+                                       bwd=True, tile_chunk_size=tile_chunk_size)
     n_ch = int(cu_seqlens.size(0)) - 1
     _check(x.dtype == torch.float32, f"{fn}: x must be float32")
     _check(x.is_contiguous(), f"{fn}: x must be contiguous")
@@ -148,26 +222,49 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                f"{fn}: z/out must be contiguous CUDA tensors")
         _check(z.size(0) == u_flat.size(0) and out.size(0) == u_flat.size(0), f"{fn}: z/out must have shape (E,)")
     dev = u_flat.device
+    E = int(u_flat.size(0))
     f32 = dict(dtype=torch.float32, device=dev)
     du = torch.empty_like(u_flat)
     dA = torch.empty((dim, dstate), **f32)
-    dW_B, dW_C = torch.empty((dim, dstate), **f32), torch.empty((dim, dstate), **f32)
     ddt_idle, ddt_active = torch.empty(dim, **f32), torch.empty(dim, **f32)
     dD = torch.empty(dim, **f32) if D is not None else None
     dz = torch.empty_like(u_flat) if has_z else None
-    a = _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle.contiguous(), dt_active.contiguous(),
-              A.contiguous(), B, C, D, z)
-    a.dout, a.x_saved = dout_flat.data_ptr(), x.data_ptr()
-    a.out_saved = out.data_ptr() if has_z else None
-    a.du, a.dA, a.dW_B, a.dW_C = du.data_ptr(), dA.data_ptr(), dW_B.data_ptr(), dW_C.data_ptr()
-    a.ddt_idle, a.ddt_active = ddt_idle.data_ptr(), ddt_active.data_ptr()
-    a.dD = dD.data_ptr() if dD is not None else None
-    a.dz = dz.data_ptr() if dz is not None else None
+    dpw_B = dpw_C = None
     with torch.cuda.device(dev):
-        _nat.call("bcm_scan_bwd", a, _nat.stream_of(u_flat))
-    res = [du, dA, dW_B, dW_C, ddt_idle, ddt_active]
+        s = _nat.stream_of(u_flat)
+        if mode == "depthwise":
+            W_B, W_C = (pw_B @ B, pw_C @ C) if pw_B is not None else (B, C)
+            dB, dC = torch.empty((dim, dstate), **f32), torch.empty((dim, dstate), **f32)
+        else:
+            W_B = W_C = None
+            # tiled entries that no event maps to stay zero (the reference
+            # zero-fills and accumulates, :1055-1056)
+            dB = torch.zeros(B.shape, **f32) if mode == "tiled" else torch.empty(B.shape, **f32)
+            dC = torch.zeros(C.shape, **f32) if mode == "tiled" else torch.empty(C.shape, **f32)
+        a = _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle.contiguous(), dt_active.contiguous(),
+                  A.contiguous(), W_B, W_C, D, z)
+        a.dout, a.x_saved = dout_flat.data_ptr(), x.data_ptr()
+        a.out_saved = out.data_ptr() if has_z else None
+        a.du, a.dA = du.data_ptr(), dA.data_ptr()
+        a.ddt_idle, a.ddt_active = ddt_idle.data_ptr(), ddt_active.data_ptr()
+        a.dD = dD.data_ptr() if dD is not None else None
+        a.dz = dz.data_ptr() if dz is not None else None
+        if mode == "depthwise":
+            a.dW_B, a.dW_C = dB.data_ptr(), dC.data_ptr()
+            _nat.call("bcm_scan_bwd", a, s)
+            if pw_B is not None:  # dB, dC hold dW_eff here
+                dpw_B, dpw_C = dB @ B.t(), dC @ C.t()
+                dB, dC = pw_B.t() @ dB, pw_C.t() @ dC
+        else:
+            bc = _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB, dC)
+            nbytes = int(_nat.lib().bcm_scan_var_workspace_bytes(E, dstate))
+            ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
+            _nat.call("bcm_scan_var_bwd", a, bc, ws.data_ptr(), nbytes, s)
+    res = [du, dA, dB, dC, ddt_idle, ddt_active]
     if D is not None:
         res.append(dD)
     if has_z:
         res.append(dz)
+    if dpw_B is not None:
+        res.extend([dpw_B, dpw_C])
     return res

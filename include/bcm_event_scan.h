@@ -206,6 +206,48 @@ int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream);
  * selective_scan_bwd_kernel.cuh:635-1169). */
 int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream);
 
+/* B and C of the non-depthwise modes of fwd_flat_ch / bwd_flat_ch
+ * (selective_scan.cpp:760-776, 840-848, 969-990, 1085-1090):
+ *   BCM_BC_LEGACY  per event: B[s*b_row_stride + e]  ([dstate, E])
+ *                  per model channel: B[s*b_row_stride + d]  ([dstate, dim])
+ *   BCM_BC_TILED   per event: B[((tile_offsets[ch] + p/T)*dstate + s)*T + p%T]
+ *                  for the event at position p of channel ch, T =
+ *                  tile_chunk_size; tiles outside [0, n_tiles) read 0.
+ * C alike. The recurrence is h_i = a_i h_{i-1} + B_i Δ_i u_i and
+ * y_i = D u_i + Σ_s C_i h_i (W_B / W_C of bcm_scan_args are not read). */
+enum bcm_bc_layout { BCM_BC_LEGACY = 1, BCM_BC_TILED = 2 };
+typedef struct bcm_scan_bc {
+  int32_t layout;           /* bcm_bc_layout */
+  int32_t b_per_event;      /* legacy: 1 = [dstate, E], 0 = [dstate, dim]; tiled: 1 */
+  int32_t c_per_event;
+  int32_t tile_chunk_size;  /* tiled: T >= 1 */
+  int64_t b_row_stride;     /* legacy: elements between the rows of B */
+  int64_t c_row_stride;
+  int64_t n_tiles;          /* tiled: leading dimension of B and C */
+  const int32_t* tile_offsets;  /* tiled: [n_channels] first tile of each channel */
+  const float* B;
+  const float* C;
+  /* backward outputs, the layouts of B and C. Per-event entries are written
+   * for every event; tiled entries that no event maps to are not written
+   * (zero-fill them); per-model-channel entries are fully written. */
+  float* dB;
+  float* dC;
+  int64_t db_row_stride;    /* legacy */
+  int64_t dc_row_stride;
+} bcm_scan_bc;
+
+/* selective_scan_fwd_flat_ch with legacy or tiled B/C (selective_scan.cpp
+ * :760-776, selective_scan_fwd_kernel.cuh:566-686). Outputs as bcm_scan_fwd. */
+int bcm_scan_var_fwd(const bcm_scan_args* args, const bcm_scan_bc* bc, bcm_stream_t stream);
+/* Workspace of bcm_scan_var_bwd: the forward states, 4*E*dstate bytes. */
+int64_t bcm_scan_var_workspace_bytes(int64_t n_events, int dstate);
+/* selective_scan_bwd_flat_ch with legacy or tiled B/C (selective_scan.cpp
+ * :969-990, selective_scan_bwd_kernel.cuh:902-1112): du, dA, ddt_*, dD, dz
+ * in args; dB and dC in bc. Recomputes the forward states into the
+ * workspace first (x_saved is not read). */
+int bcm_scan_var_bwd(const bcm_scan_args* args, const bcm_scan_bc* bc, void* workspace,
+                     int64_t workspace_bytes, bcm_stream_t stream);
+
 /* ---- (3) zero-order-hold restore ---------------------------------------- */
 /* Event index of sorted per-channel time steps (the restore kernels' input
  * when the caller has no bitmask): bitmask [n_rows, words], tile_start

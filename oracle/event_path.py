@@ -19,6 +19,14 @@ How each function is pinned (tests/test_oracle.py):
                        differences, closed-form one-event gradients
   restore_fwd / _bwd   brute-force per-position loops on small inputs,
                        adjointness <restore(y), g> == <y, restore_bwd(g)>
+  scan_var_fwd / _bwd  with B_i = u_i W_B and C_i = u_i W_C they reproduce the
+                       depthwise scan_fwd / scan_bwd (the chain rule through
+                       B and C gives du, dW_B and dW_C); finite differences
+                       of every input on random per-event B and C
+  bc_per_event /       brute-force loops over events for the legacy,
+  bc_grad_layout       constant and tiled layouts; adjointness of the two
+  pw_effective /       finite differences of the composed scan loss in pw
+  pw_grads             and in W
 """
 import math
 
@@ -223,6 +231,186 @@ def scan_bwd(u, k, cu, max_seqlen, dt_idle, dt_active, A, W_B, W_C, dout, D=None
 
     return (du[valid], per_dim(dA_c), per_dim(dWB_c), per_dim(dWC_c), per_dim(ddti_c), per_dim(ddta_c),
             per_dim(dD_c) if D is not None else None, dz)
+
+
+# ------------------------------------------- scan with per-event B and C
+def bc_per_event(Bt, cu, dim, N, tile_offsets=None, tile_chunk_size=0):
+    """Per-event values [E, N] of a non-depthwise B or C operand of
+    fwd_flat_ch / bwd_flat_ch (selective_scan.cpp:768-776, 840-848):
+      legacy [N, E]    B[s, e]                       (selective_scan_fwd_kernel.cuh:588-591)
+      constant [N, dim] B[s, ch % dim] for every event (:592-598, bwd only)
+      tiled [NT, N, T]  B[tile_offsets[ch] + p // T, s, p % T] for the
+                        event at position p of channel ch (:580-587)."""
+    Bt = np.asarray(Bt, np.float64)
+    cu = np.asarray(cu, np.int64)
+    NC = len(cu) - 1
+    E = int(cu[-1])
+    ch = np.repeat(np.arange(NC), np.diff(cu))
+    if tile_offsets is not None:
+        T = int(tile_chunk_size)
+        p = np.arange(E) - cu[ch]
+        tiles = np.asarray(tile_offsets, np.int64)[ch] + p // T
+        return Bt[tiles, :, p % T]
+    if Bt.shape[1] == E:
+        return Bt.T.copy()
+    assert Bt.shape[1] == dim
+    return Bt[:, ch % dim].T.copy()
+
+
+def bc_grad_layout(dev, like_shape, cu, dim, tile_offsets=None, tile_chunk_size=0):
+    """Inverse of bc_per_event for gradients: per-event [E, N] values into
+    the operand's layout (legacy: transpose; constant: summed over the events
+    of each d; tiled: scattered, zeros where no event maps)."""
+    cu = np.asarray(cu, np.int64)
+    NC = len(cu) - 1
+    E = int(cu[-1])
+    ch = np.repeat(np.arange(NC), np.diff(cu))
+    if tile_offsets is not None:
+        T = int(tile_chunk_size)
+        p = np.arange(E) - cu[ch]
+        tiles = np.asarray(tile_offsets, np.int64)[ch] + p // T
+        out = np.zeros(like_shape)
+        out[tiles, :, p % T] = dev
+        return out
+    if like_shape[1] == E:
+        return dev.T.copy()
+    out = np.zeros(like_shape)
+    np.add.at(out.T, ch % dim, dev)
+    return out
+
+
+def scan_var_fwd(u, k, cu, max_seqlen, dt_idle, dt_active, A, Bev, Cev, D=None, z=None):
+    """flat_ch forward with per-event B and C (selective_scan_fwd_kernel.cuh
+    :566-686, the variable-B/C branch):
+      h_i = exp2(clamp(Δ_i A log2e)) h_{i-1} + B_i Δ_i u_i      :650-652
+      y_i = D u_i + Σ_s C_i h_i                                 :680-685
+    Bev, Cev: [E, N] per-event values (bc_per_event). x as in scan_fwd."""
+    f8 = np.float64
+    NC = len(cu) - 1
+    dim, N = A.shape
+    d = np.arange(NC) % dim
+    U, valid, n = _padded(cu, np.asarray(u, dtype=f8), 0.0, f8)
+    K, _, _ = _padded(cu, k, 1, np.int64)
+    nmax = U.shape[1]
+    Bp = np.zeros((NC, nmax, N))
+    Cp = np.zeros((NC, nmax, N))
+    src = np.asarray(cu[:-1], np.int64)[:, None] + np.arange(nmax)[None, :]
+    Bp[valid] = np.asarray(Bev, f8)[src[valid]]
+    Cp[valid] = np.asarray(Cev, f8)[src[valid]]
+    dt_i, dt_a = np.asarray(dt_idle, f8)[d], np.asarray(dt_active, f8)[d]
+    delta = dt_i[:, None] * (K - 1) + dt_a[:, None]
+    Al = np.asarray(A, f8)[d] * LOG2E
+    Dv = np.asarray(D, f8)[d] if D is not None else np.zeros(NC)
+    n_chunks = max(1, math.ceil(int(max_seqlen) / CHUNK))
+    x = np.zeros((NC, n_chunks, 2 * N))
+    h = np.zeros((NC, N))
+    P = np.ones((NC, N))
+    Y = np.zeros((NC, nmax))
+    for i in range(nmax):
+        v = valid[:, i]
+        a = _decay(delta[:, i, None], Al)
+        hn = a * h + Bp[:, i] * (delta[:, i] * U[:, i])[:, None]
+        h = np.where(v[:, None], hn, h)
+        P = np.where(v[:, None], P * a, P)
+        Y[:, i] = Dv * U[:, i] + (Cp[:, i] * h).sum(axis=1)
+        c = i // CHUNK
+        at_end = v & (((i + 1) % CHUNK == 0) | (i + 1 == n))
+        rows = np.nonzero(at_end & (c < n_chunks))[0]
+        x[rows, c, 0::2] = P[rows]
+        x[rows, c, 1::2] = h[rows]
+    out = Y[valid]
+    if z is None:
+        return out, x
+    zf = np.asarray(z, f8)
+    return out, x, out * (zf / (1.0 + np.exp(-zf)))
+
+
+def scan_var_bwd(u, k, cu, max_seqlen, dt_idle, dt_active, A, Bev, Cev, dout, D=None, z=None, out=None):
+    """flat_ch backward with per-event B and C (selective_scan_bwd_kernel.cuh
+    :902-1044, the variable-B/C branch):
+      dh_i  = C_i dout_i + a_{i+1} dh_{i+1}
+      dC_i  = dout_i h_i;   dB_i = dh_i Δ_i u_i
+      du_i  = D dout_i + Σ_s dh_i B_i Δ_i
+      dΔ_i  = Σ_s [dh_i B_i u_i + dh_i A a_i h_{i-1}]
+      dA   += dh_i Δ_i a_i h_{i-1};  dD, ddt_* and the z gate as scan_bwd.
+    Returns (du, dA, dBev [E, N], dCev [E, N], ddt_idle, ddt_active,
+    dD or None, dz or None)."""
+    f8 = np.float64
+    NC = len(cu) - 1
+    dim, N = A.shape
+    d = np.arange(NC) % dim
+    U, valid, n = _padded(cu, np.asarray(u, f8), 0.0, f8)
+    K, _, _ = _padded(cu, k, 1, np.int64)
+    DO, _, _ = _padded(cu, np.asarray(dout, f8), 0.0, f8)
+    nmax = U.shape[1]
+    Bp = np.zeros((NC, nmax, N))
+    Cp = np.zeros((NC, nmax, N))
+    src = np.asarray(cu[:-1], np.int64)[:, None] + np.arange(nmax)[None, :]
+    Bp[valid] = np.asarray(Bev, f8)[src[valid]]
+    Cp[valid] = np.asarray(Cev, f8)[src[valid]]
+    dz = None
+    if z is not None:
+        Z, _, _ = _padded(cu, np.asarray(z, f8), 0.0, f8)
+        O, _, _ = _padded(cu, np.asarray(out, f8), 0.0, f8)
+        sg = 1.0 / (1.0 + np.exp(-Z))
+        dz = (DO * O * sg * (1.0 + Z * (1.0 - sg)))[valid]
+        DO = DO * Z * sg
+    dt_i, dt_a = np.asarray(dt_idle, f8)[d], np.asarray(dt_active, f8)[d]
+    delta = dt_i[:, None] * (K - 1) + dt_a[:, None]
+    Araw = np.asarray(A, f8)[d]
+    Al = Araw * LOG2E
+    Dv = np.asarray(D, f8)[d] if D is not None else np.zeros(NC)
+    a_all = np.ones((NC, nmax, N))
+    h_all = np.zeros((NC, nmax, N))
+    h = np.zeros((NC, N))
+    for i in range(nmax):
+        v = valid[:, i, None]
+        a = _decay(delta[:, i, None], Al)
+        hn = a * h + Bp[:, i] * (delta[:, i] * U[:, i])[:, None]
+        a_all[:, i] = np.where(v, a, 1.0)
+        h = np.where(v, hn, h)
+        h_all[:, i] = h
+    du = np.zeros((NC, nmax))
+    ddelta = np.zeros((NC, nmax))
+    dBp, dCp = np.zeros((NC, nmax, N)), np.zeros((NC, nmax, N))
+    dA_c = np.zeros((NC, N))
+    dh = np.zeros((NC, N))
+    for i in range(nmax - 1, -1, -1):
+        v = valid[:, i, None]
+        a_next = a_all[:, i + 1] if i + 1 < nmax else np.ones((NC, N))
+        dh = np.where(v, Cp[:, i] * DO[:, i, None] + a_next * dh, 0.0)
+        hprev = h_all[:, i - 1] if i > 0 else np.zeros((NC, N))
+        ah = a_all[:, i] * hprev
+        du[:, i] = Dv * DO[:, i] + (dh * Bp[:, i]).sum(1) * delta[:, i]
+        ddelta[:, i] = (dh * Bp[:, i]).sum(1) * U[:, i] + (dh * Araw * ah).sum(1)
+        dA_c += dh * delta[:, i, None] * ah
+        dBp[:, i] = dh * (delta[:, i] * U[:, i])[:, None]
+        dCp[:, i] = np.where(v, DO[:, i, None] * h_all[:, i], 0.0)
+    ddelta = np.where(valid, ddelta, 0.0)
+    dD_c = (DO * U).sum(1)
+    ddti_c = (ddelta * (K - 1)).sum(1)
+    ddta_c = ddelta.sum(1)
+
+    def per_dim(v):
+        outv = np.zeros((dim,) + v.shape[1:])
+        np.add.at(outv, d, v)
+        return outv
+
+    return (du[valid], per_dim(dA_c), dBp[valid], dCp[valid], per_dim(ddti_c), per_dim(ddta_c),
+            per_dim(dD_c) if D is not None else None, dz)
+
+
+def pw_effective(pw, W):
+    """Depthwise + pointwise mode (selective_scan_fwd_kernel.cuh:486-509):
+    W_eff[d, s] = Σ_{d'} pw[d, d'] W[d', s]."""
+    return np.asarray(pw, np.float64) @ np.asarray(W, np.float64)
+
+
+def pw_grads(pw, W, dW_eff):
+    """Chain rule of pw_effective (selective_scan_bwd_kernel.cuh:1122-1166):
+    dW[d', s] = Σ_d pw[d, d'] dW_eff[d, s],  dpw[d, d'] = Σ_s dW_eff[d, s] W[d', s]."""
+    pw, W, g = (np.asarray(v, np.float64) for v in (pw, W, dW_eff))
+    return pw.T @ g, g @ W.T
 
 
 # ------------------------------------------------------------------ restore

@@ -23,8 +23,8 @@ def header_functions():
     return set(re.findall(r"\b(bcm_[a-z0-9_]+)\s*\(", _header_text()))
 
 
-def header_struct_fields():
-    body = re.search(r"typedef struct bcm_scan_args \{(.*?)\} bcm_scan_args;", _header_text(), re.S).group(1)
+def header_struct_fields(name="bcm_scan_args"):
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), _header_text(), re.S).group(1)
     return [m.group(1) for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*;", body)]
 
 
@@ -51,6 +51,12 @@ def test_scan_args_layout_matches_header():
     assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 24 * 8
 
 
+def test_scan_bc_layout_matches_header():
+    assert [f for f, _ in nat.ScanBC._fields_] == header_struct_fields("bcm_scan_bc")
+    # 4 int32 + 3 int64 + 5 pointers + 2 int64
+    assert ctypes.sizeof(nat.ScanBC) == 4 * 4 + 3 * 8 + 5 * 8 + 2 * 8
+
+
 def test_host_helpers(lib):
     assert lib.bcm_abi_version() == 1
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64
@@ -73,3 +79,20 @@ def test_invalid_arguments_are_rejected_before_launch(lib):
     assert "divisible" in lib.bcm_last_error().decode()
     assert lib.bcm_restore_fwd(None, 1, 0, None, 1, None, 8, 4, 8, None, 0, None) == 1
     assert "fp16 input only supports fp16 output" in lib.bcm_last_error().decode()
+
+
+def test_scan_var_arguments_are_rejected_before_launch(lib):
+    a = nat.ScanArgs()
+    a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 4, 2, 16, 10, 1, 0
+    a.cu_seqlens = a.dt_idle = a.dt_active = a.A = 16  # never dereferenced: rejected first
+    bc = nat.ScanBC()
+    bc.layout = 7
+    assert lib.bcm_scan_var_fwd(a, bc, None) == 1 and "layout" in lib.bcm_last_error().decode()
+    bc.layout, bc.B, bc.C = nat.BC_TILED, 16, 16
+    bc.b_per_event = bc.c_per_event = 1
+    assert lib.bcm_scan_var_fwd(a, bc, None) == 1 and "tile_chunk_size" in lib.bcm_last_error().decode()
+    bc.layout, bc.b_row_stride, bc.c_row_stride = nat.BC_LEGACY, 0, 1
+    assert lib.bcm_scan_var_fwd(a, bc, None) == 1 and "row strides" in lib.bcm_last_error().decode()
+    assert lib.bcm_scan_var_workspace_bytes(1000, 16) == 64000
+    assert lib.bcm_scan_var_bwd(a, None, None, 0, None) == 1
+    assert lib.bcm_last_error().decode().startswith("bcm_scan_var_bwd")

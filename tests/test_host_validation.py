@@ -42,12 +42,25 @@ def test_scan_dtype_and_shape_checks(field, bad, msg, fake_cuda):
         ssc.fwd_flat_ch(**args, is_depthwise_bc=True)
 
 
-def test_scan_unsupported_modes_raise(fake_cuda):
+def test_scan_mode_shape_checks(fake_cuda):
+    """Legacy, tiled and pointwise modes check their operand shapes like
+    selective_scan.cpp:760-776, 840-848, 969-990 before any device work."""
     a = _scan_inputs()
-    with pytest.raises(RuntimeError, match="only the depthwise B/C mode"):
-        ssc.fwd_flat_ch(**a, is_depthwise_bc=False)
-    with pytest.raises(RuntimeError, match="pointwise"):
-        ssc.fwd_flat_ch(**a, is_depthwise_bc=True, pw_B=torch.eye(2), pw_C=torch.eye(2))
+    with pytest.raises(RuntimeError, match="B must have shape \\(4, 5\\)"):
+        ssc.fwd_flat_ch(**a, is_depthwise_bc=False)  # [dim, dstate] is not a legacy [dstate, E] operand
+    leg = dict(a, B=torch.randn(4, 5)[:, :5], C=torch.randn(5, 4).t())
+    with pytest.raises(RuntimeError, match="stride\\(1\\) == 1"):
+        ssc.fwd_flat_ch(**leg, is_depthwise_bc=False)
+    with pytest.raises(RuntimeError, match="tiled B/C must be 3-D"):
+        ssc.fwd_flat_ch(**a, tile_offsets=torch.zeros(2, dtype=i32), tile_chunk_size=4)
+    til = dict(a, B=torch.randn(3, 4, 8), C=torch.randn(3, 4, 8))
+    with pytest.raises(RuntimeError, match="dim-2 must equal tile_chunk_size"):
+        ssc.fwd_flat_ch(**til, tile_offsets=torch.zeros(2, dtype=i32), tile_chunk_size=4)
+    with pytest.raises(RuntimeError, match="pw_B must be \\[dim, dim\\]"):
+        ssc.fwd_flat_ch(**a, is_depthwise_bc=True, pw_B=torch.eye(3), pw_C=torch.eye(2))
+    with pytest.raises(RuntimeError, match="must have shape \\(4, 5\\) or \\(4, 2\\)"):
+        ssc.bwd_flat_ch(**dict(a, B=torch.randn(4, 3), C=torch.randn(4, 5)), dout_flat=torch.randn(5),
+                        x=torch.zeros(2, 1, 8), is_depthwise_bc=False)
 
 
 def test_bwd_checks_x_chunks():

@@ -231,6 +231,113 @@ def test_scan_bwd_one_event_closed_form():
     assert np.allclose(dA[0], 0.0) and dD[0] == pytest.approx(uu)
 
 
+# ------------------------------------------- scan with per-event B and C
+@pytest.mark.parametrize("with_z", [False, True])
+def test_scan_var_reduces_to_depthwise(with_z):
+    """B_i = u_i W_B[d], C_i = u_i W_C[d] is the depthwise mode: same out and
+    x, and the chain rule through B and C gives the depthwise du, dW_B, dW_C."""
+    ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, z = _bwd_case(2, 4, 70, 5, 0.3, with_z, RNG)
+    f8 = lambda v: np.asarray(v, np.float64)
+    d = ch % 4
+    Bev = f8(u)[:, None] * f8(WB)[d]
+    Cev = f8(u)[:, None] * f8(WC)[d]
+    ref = orc.scan_fwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, z)
+    got = orc.scan_var_fwd(u, k, cu, ms, dt_i, dt_a, A, Bev, Cev, Dv, z)
+    for a, b in zip(got, ref):
+        assert_close(a, b, rtol=1e-12, atol_rel=1e-14, name="fwd")
+    out = ref[0]
+    rb = orc.scan_bwd(u, k, cu, ms, dt_i, dt_a, A, WB, WC, dout, Dv, z, out if with_z else None)
+    du, dA, dBev, dCev, ddti, ddta, dD, dz = orc.scan_var_bwd(u, k, cu, ms, dt_i, dt_a, A, Bev, Cev, dout, Dv, z,
+                                                              out if with_z else None)
+    du_chain = du + (dBev * f8(WB)[d]).sum(1) + (dCev * f8(WC)[d]).sum(1)
+    dWB = np.zeros((4, 5))
+    dWC = np.zeros((4, 5))
+    np.add.at(dWB, d, dBev * f8(u)[:, None])
+    np.add.at(dWC, d, dCev * f8(u)[:, None])
+    for name, a, b in [("du", du_chain, rb[0]), ("dA", dA, rb[1]), ("dW_B", dWB, rb[2]), ("dW_C", dWC, rb[3]),
+                       ("ddt_idle", ddti, rb[4]), ("ddt_active", ddta, rb[5]), ("dD", dD, rb[6])] + \
+            ([("dz", dz, rb[7])] if with_z else []):
+        assert_close(a, b, rtol=1e-11, atol_rel=1e-13, name=name)
+
+
+def test_scan_var_bwd_finite_difference():
+    ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, _ = _bwd_case(1, 2, 40, 3, 0.4, False, RNG)
+    E = len(u)
+    Bev = RNG.standard_normal((E, 3))
+    Cev = RNG.standard_normal((E, 3))
+    f8 = lambda v: np.asarray(v, np.float64)
+    du, dA, dBev, dCev, ddti, ddta, dD, _ = orc.scan_var_bwd(u, k, cu, ms, dt_i, dt_a, A, Bev, Cev, dout, Dv)
+
+    def loss(uu=f8(u), AA=f8(A), BB=Bev, CC=Cev, ti=f8(dt_i), ta=f8(dt_a)):
+        return float(np.dot(orc.scan_var_fwd(uu, k, cu, ms, ti, ta, AA, BB, CC, Dv)[0], f8(dout)))
+
+    eps = 1e-6
+
+    def fd(name, base, idx, grad):
+        p_, m_ = base.copy(), base.copy()
+        p_[idx] += eps
+        m_[idx] -= eps
+        num = (loss(**{name: p_}) - loss(**{name: m_})) / (2 * eps)
+        assert num == pytest.approx(grad, rel=1e-6, abs=1e-9), (name, idx)
+
+    for i in (0, E // 2, E - 1):
+        fd("uu", f8(u), i, du[i])
+        fd("BB", Bev, (i, 1), dBev[i, 1])
+        fd("CC", Cev, (i, 2), dCev[i, 2])
+    fd("AA", f8(A), (1, 2), dA[1, 2])
+    fd("ti", f8(dt_i), 1, ddti[1])
+    fd("ta", f8(dt_a), 0, ddta[0])
+
+
+def test_bc_layouts_brute_force_and_adjoint():
+    cu = np.array([0, 5, 5, 12, 30], np.int64)
+    E, NC, dim, N, T = 30, 4, 2, 3, 4
+    legacy = RNG.standard_normal((N, E))
+    const = RNG.standard_normal((N, dim))
+    n = np.diff(cu)
+    tile_off = np.concatenate([[0], np.cumsum((n + T - 1) // T)])[:-1] + 1   # one unused leading tile
+    tiled = RNG.standard_normal((int(tile_off[-1] + (n[-1] + T - 1) // T) + 1, N, T))
+    for X, kw in [(legacy, {}), (const, {}), (tiled, dict(tile_offsets=tile_off, tile_chunk_size=T))]:
+        got = orc.bc_per_event(X, cu, dim, N, **kw)
+        want = np.zeros((E, N))
+        for c in range(NC):
+            for p in range(int(n[c])):
+                e = int(cu[c]) + p
+                if "tile_offsets" in kw:
+                    want[e] = X[tile_off[c] + p // T, :, p % T]
+                elif X.shape[1] == E:
+                    want[e] = X[:, e]
+                else:
+                    want[e] = X[:, c % dim]
+        assert np.array_equal(got, want)
+        G = RNG.standard_normal((E, N))
+        back = orc.bc_grad_layout(G, X.shape, cu, dim, **kw)
+        assert np.dot(got.ravel(), G.ravel()) == pytest.approx(np.dot(X.ravel(), back.ravel()), rel=1e-12)
+
+
+def test_pw_grads_finite_difference():
+    ch, t, k, cu, ms, dt_i, dt_a, A, WB, WC, Dv, u, dout, _ = _bwd_case(1, 3, 40, 4, 0.4, False, RNG)
+    pwB = RNG.standard_normal((3, 3))
+    pwC = RNG.standard_normal((3, 3))
+    f8 = lambda v: np.asarray(v, np.float64)
+
+    def loss(pB=pwB, pC=pwC, B_=f8(WB), C_=f8(WC)):
+        y = orc.scan_fwd(u, k, cu, ms, dt_i, dt_a, A, orc.pw_effective(pB, B_), orc.pw_effective(pC, C_), Dv)[0]
+        return float(np.dot(y, f8(dout)))
+
+    r = orc.scan_bwd(u, k, cu, ms, dt_i, dt_a, A, orc.pw_effective(pwB, WB), orc.pw_effective(pwC, WC), dout, Dv)
+    dWB, dpwB = orc.pw_grads(pwB, WB, r[2])
+    dWC, dpwC = orc.pw_grads(pwC, WC, r[3])
+    eps = 1e-6
+    for name, base, idx, g in [("pB", pwB, (0, 2), dpwB), ("pC", pwC, (2, 1), dpwC), ("B_", f8(WB), (1, 3), dWB),
+                               ("C_", f8(WC), (2, 0), dWC)]:
+        p_, m_ = base.copy(), base.copy()
+        p_[idx] += eps
+        m_[idx] -= eps
+        num = (loss(**{name: p_}) - loss(**{name: m_})) / (2 * eps)
+        assert num == pytest.approx(g[idx], rel=1e-6, abs=1e-9), name
+
+
 # ---------------------------------------------------------------- restore
 def test_restore_fwd_brute_force():
     B, D, L = 2, 3, 45
