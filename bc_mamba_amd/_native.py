@@ -31,7 +31,7 @@ class ScanArgs(ctypes.Structure):
         ("out", c_p), ("out_z", c_p), ("x", c_p),
         ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
-        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p),
+        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p),
     ]
 
 
@@ -69,6 +69,8 @@ SIGNATURES = {
     "bcm_gather_bwd_rows": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p]),
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_scan_chunking": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(c_i32), ctypes.POINTER(c_i32),
+                                  ctypes.POINTER(c_i32)]),
     "bcm_scan_var_fwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p]),
     "bcm_scan_var_workspace_bytes": (c_i64, [c_i64, c_i32]),
     "bcm_scan_var_bwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p, c_i64, c_p]),
@@ -94,7 +96,7 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.bcm_abi_version() != 1:
+        if handle.bcm_abi_version() != 2:
             raise RuntimeError("bc_mamba_amd: ABI version mismatch")
         _lib = handle
     return _lib
@@ -129,6 +131,14 @@ def bitmask_words(L):
 
 def tile_count(L):
     return (L + 63) // 64
+
+
+def scan_chunking(a):
+    """(pass_len, n_pass, needs_chunk_g) of the scan kernels for ScanArgs `a`
+    (bcm_scan_chunking): the caller sizes chunk_g as [NC, n_pass, dstate]."""
+    p, q, r = c_i32(), c_i32(), c_i32()
+    call("bcm_scan_chunking", a, ctypes.byref(p), ctypes.byref(q), ctypes.byref(r))
+    return p.value, q.value, bool(r.value)
 
 
 class HostMeta:

@@ -53,6 +53,7 @@ constexpr int kTabK = 64;           // gaps k = 1..kTabK come from the decay tab
 constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
 constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
 constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
+constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
 
 struct FwdLds {
   int N, nw, G, R, nslots;
@@ -226,6 +227,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
       const int cnt = min(max(n - c * C, 0), C);
       const int nv = cnt - j * R;                 // events among this lane's R items
       const uint32_t eb = (uint32_t)(e0 + c * C);  // event index of the chunk's first item
+      // x holds the state after each 2048-event chunk and after the
+      // channel's last event, whatever the pass length C
+      const int cend = min(n, (c + 1) * C);
+      const int xc = (cend - 1) / kXChunk;
+      const bool xsave = c < nch && (cend % kXChunk == 0 || cend == n) && xc < nck;
       if (b0 > 0 || c > 0) {
         issue(e0, n, c);
         to_tiles();
@@ -302,7 +308,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
           const float Pn = P0 * P;
           carry[s] = Pn;
           carry[N + s] = gend;
-          if (c < nck) reinterpret_cast<float2*>(a.x + (ch * nck + c) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
+          if (xsave) reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
+          if (a.chunk_g && c + 1 < nch) a.chunk_g[(ch * ((a.max_seqlen + C - 1) / C) + c + 1) * N + s] = gend * sWB[s];
         }
       };
       auto states = [&](auto exact_tag) {
@@ -347,7 +354,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
     }
     // chunks past the channel's end keep the reference's zero state
     if (act) {
-      for (int c = nch; c < nck; ++c)
+      for (int c = (n + kXChunk - 1) / kXChunk; c < nck; ++c)
         for (int s = j; s < 2 * N; s += G) a.x[(ch * nck + c) * 2 * N + s] = 0.0f;
     }
   }
@@ -474,10 +481,17 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       const int cnt = min(max(n - c * C, 0), C);
       const int nv = cnt - j * R;
       const uint32_t eb = (uint32_t)(e0 + c * C);
-      // chunk-start state in g = h / W_B form (saved h of the previous chunk)
+      // chunk-start state in g = h / W_B form from the h the forward saved:
+      // chunk_g (pass-start h, row c) or x (2048-event passes: h after the
+      // previous chunk, row c - 1); the source is uniform, one code path
       if (c > 0) {
+        const bool pg = a.chunk_g != nullptr;
+        const float* src = pg ? a.chunk_g : a.x_saved + 1;
+        const int64_t rows = pg ? (a.max_seqlen + C - 1) / C : nck;
+        const int64_t row = c - (pg ? 0 : 1);
+        const int64_t rstride = pg ? N : 2 * N, sstride = pg ? 1 : 2;
         for (int s = j; s < N; s += G) {
-          const float h0 = (c - 1 < nck) ? a.x_saved[(ch * nck + (c - 1)) * 2 * N + 2 * s + 1] : 0.0f;
+          const float h0 = (cact && row < rows) ? src[(ch * rows + row) * rstride + s * sstride] : 0.0f;
           const float wb = sWB[s];
           cg0[s] = wb != 0.0f ? h0 / wb : 0.0f;
         }
@@ -776,28 +790,60 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
   return check_launch(fn);
 }
 
-// Lane-group shape (G lanes x R items per channel chunk) by dstate and the
-// longest channel; channels longer than one pass loop over 2048-event chunks.
-template <typename T, bool Z, bool BWD, bool TBL>
-static int dispatch_len(const bcm_scan_args& a, hipStream_t s, const char* fn) {
+// Lane-group shape (G lanes x R items per pass of a channel). Up to 512
+// events the longest channel fits one pass. Longer channels loop over
+// passes whose length follows the mean channel length (a few bursty
+// channels then cost extra passes instead of padding every channel to the
+// longest one); passes shorter than 2048 events need chunk_g in the
+// backward, 2048-event passes re-seed from x like the reference.
+enum ShapeId { S16x4, S16x8, S16x16, S16x24, S32x16, S64x4, S64x8, S64x16, S64x32 };
+constexpr int kShapeG[] = {16, 16, 16, 16, 32, 64, 64, 64, 64};
+constexpr int kShapeR[] = {4, 8, 16, 24, 16, 4, 8, 16, 32};
+
+static ShapeId pick_shape(const bcm_scan_args& a) {
   const int m = a.max_seqlen;
-  if (TBL) {
-    if (m <= 64) return launch<16, 4, T, Z, BWD, TBL>(a, s, fn);
-    if (m <= 128) return launch<16, 8, T, Z, BWD, TBL>(a, s, fn);
-    if (m <= 256) return launch<16, 16, T, Z, BWD, TBL>(a, s, fn);
-    if (m <= 384) return launch<16, 24, T, Z, BWD, TBL>(a, s, fn);
-    if (m <= 512) return launch<32, 16, T, Z, BWD, TBL>(a, s, fn);
+  const bool tbl = a.dstate <= kTabMaxN;
+  if (tbl) {
+    if (m <= 64) return S16x4;
+    if (m <= 128) return S16x8;
+    if (m <= 256) return S16x16;
+    if (m <= 384) return S16x24;
+    if (m <= 512) return S32x16;
   } else {
-    if (m <= 256) return launch<64, 4, T, Z, BWD, TBL>(a, s, fn);
-    if (m <= 512) return launch<64, 8, T, Z, BWD, TBL>(a, s, fn);
+    if (m <= 256) return S64x4;
+    if (m <= 512) return S64x8;
   }
-  if (m <= 1024) return launch<64, 16, T, Z, BWD, TBL>(a, s, fn);
-  return launch<64, 32, T, Z, BWD, TBL>(a, s, fn);
+  const double mean = (double)a.n_events / (a.n_channels > 0 ? a.n_channels : 1);
+  if (mean <= 256) return tbl ? S16x16 : S64x4;
+  if (mean <= 512) return tbl ? S16x16 : S64x8;
+  if (mean <= 1024) return S64x16;
+  return S64x32;
+}
+
+static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* needs_chunk_g) {
+  const ShapeId id = pick_shape(a);
+  const int C = kShapeG[id] * kShapeR[id];
+  *pass_len = C;
+  *n_pass = a.max_seqlen > 0 ? (a.max_seqlen + C - 1) / C : 1;
+  *needs_chunk_g = (*n_pass > 1 && C < kXChunk) ? 1 : 0;
 }
 
 template <typename T, bool Z, bool BWD>
 static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn) {
-  return a.dstate <= kTabMaxN ? dispatch_len<T, Z, BWD, true>(a, s, fn) : dispatch_len<T, Z, BWD, false>(a, s, fn);
+  switch (pick_shape(a)) {
+    case S16x4: return launch<16, 4, T, Z, BWD, true>(a, s, fn);
+    case S16x8: return launch<16, 8, T, Z, BWD, true>(a, s, fn);
+    case S16x16: return launch<16, 16, T, Z, BWD, true>(a, s, fn);
+    case S16x24: return launch<16, 24, T, Z, BWD, true>(a, s, fn);
+    case S32x16: return launch<32, 16, T, Z, BWD, true>(a, s, fn);
+    case S64x4: return launch<64, 4, T, Z, BWD, false>(a, s, fn);
+    case S64x8: return launch<64, 8, T, Z, BWD, false>(a, s, fn);
+    default: break;
+  }
+  const bool tbl = a.dstate <= kTabMaxN;
+  if (pick_shape(a) == S64x16)
+    return tbl ? launch<64, 16, T, Z, BWD, true>(a, s, fn) : launch<64, 16, T, Z, BWD, false>(a, s, fn);
+  return tbl ? launch<64, 32, T, Z, BWD, true>(a, s, fn) : launch<64, 32, T, Z, BWD, false>(a, s, fn);
 }
 
 template <bool BWD>
@@ -825,7 +871,12 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
     if (!a.dA || !a.dW_B || !a.dW_C || !a.ddt_idle || !a.ddt_active)
       return set_error(BCM_EINVAL, "%s: null gradient pointer", fn);
     if (a.n_events > 0 && (!a.dout || !a.du)) return set_error(BCM_EINVAL, "%s: null dout/du pointer", fn);
-    if (a.max_seqlen > 2048 && !a.x_saved) return set_error(BCM_EINVAL, "%s: x required for multi-chunk", fn);
+    int pass_len, n_pass, needs_g;
+    chunking(a, &pass_len, &n_pass, &needs_g);
+    if (needs_g && !a.chunk_g)
+      return set_error(BCM_EINVAL, "%s: chunk_g required (passes of %d events; run the forward with chunk_g)", fn,
+                       pass_len);
+    if (n_pass > 1 && !a.chunk_g && !a.x_saved) return set_error(BCM_EINVAL, "%s: x required for multi-chunk", fn);
     if (z && a.n_events > 0 && (!a.out_saved || !a.dz))
       return set_error(BCM_EINVAL, "%s: out and dz required with z", fn);
   }
@@ -848,6 +899,17 @@ int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream) {
 
 int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream) {
   return bcm::scan_entry<true>(args, stream, "bcm_scan_bwd");
+}
+
+int bcm_scan_chunking(const bcm_scan_args* args, int32_t* pass_len, int32_t* n_pass, int32_t* needs_chunk_g) {
+  if (!args || !pass_len || !n_pass || !needs_chunk_g)
+    return bcm::set_error(BCM_EINVAL, "bcm_scan_chunking: null argument");
+  int p, q, r;
+  bcm::chunking(*args, &p, &q, &r);
+  *pass_len = p;
+  *n_pass = q;
+  *needs_chunk_g = r;
+  return BCM_OK;
 }
 
 }  // extern "C"

@@ -136,6 +136,21 @@ def _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB=None, dC=None):
     return bc
 
 
+def chunk_states_buffer(u_flat, cu_seqlens, max_seqlen, A):
+    """float32 [n_channels, n_pass, dstate] buffer for the depthwise scan's
+    pass-start states h, or None when every channel fits one pass (or passes
+    are 2048 events, which re-seed from x)."""
+    a = _nat.ScanArgs()
+    a.n_events = int(u_flat.size(0))
+    a.n_channels = int(cu_seqlens.size(0)) - 1
+    a.dim, a.dstate = int(A.size(0)), int(A.size(1))
+    a.max_seqlen = int(max_seqlen)
+    _, n_pass, needs = _nat.scan_chunking(a)
+    if not needs:
+        return None
+    return torch.empty((a.n_channels, n_pass, a.dstate), dtype=torch.float32, device=u_flat.device)
+
+
 def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D, z):
     dim, dstate = A.shape
     a = _nat.ScanArgs()
@@ -156,10 +171,13 @@ def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D
 
 
 def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D=None, z=None,
-                tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False, pw_B=None, pw_C=None):
+                tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False, pw_B=None, pw_C=None, _chunk_g=None):
     """Flat per-channel scan forward -> [out, x] or [out, x, out_z]
     (selective_scan.cpp:674-884). x is [n_channels, n_chunks, 2*dstate]
-    float32 holding, per 2048-event chunk and state, (prod of decays, h)."""
+    float32 holding, per 2048-event chunk and state, (prod of decays, h).
+    `_chunk_g` (not in the reference signature): a float32 tensor from
+    chunk_states_buffer() that receives the pass-start states, so that
+    bwd_flat_ch need not recompute them (depthwise mode)."""
     fn = "selective_scan_fwd_flat_ch"
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous(),
            f"{fn}: u_flat/k_flat/cu_seqlens must be contiguous")
@@ -182,6 +200,8 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.out, a.x = out.data_ptr(), x.data_ptr()
         a.out_z = out_z.data_ptr() if out_z is not None else None
         if mode == "depthwise":
+            if _chunk_g is not None:
+                a.chunk_g = _chunk_g.data_ptr()
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
         else:
             bc = _bc(mode, B, C, int(u_flat.size(0)), tile_offsets, tile_chunk_size)
@@ -191,7 +211,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
-                pw_B=None, pw_C=None):
+                pw_B=None, pw_C=None, _chunk_g=None):
     """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
     ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
     dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
@@ -251,6 +271,20 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.dz = dz.data_ptr() if dz is not None else None
         if mode == "depthwise":
             a.dW_B, a.dW_C = dB.data_ptr(), dC.data_ptr()
+            _, _, needs_g = _nat.scan_chunking(a)
+            if needs_g and _chunk_g is None:
+                # passes shorter than 2048 events start from the forward's
+                # pass states: recompute them with a forward run
+                _chunk_g = chunk_states_buffer(u_flat, cu_seqlens, max_seqlen, A)
+                f = _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle.contiguous(), dt_active.contiguous(),
+                          A.contiguous(), W_B, W_C, D, z)
+                scratch_out = torch.empty_like(u_flat)
+                f.out, f.x = scratch_out.data_ptr(), torch.empty_like(x).data_ptr()
+                f.out_z = torch.empty_like(u_flat).data_ptr() if has_z else None
+                f.chunk_g = _chunk_g.data_ptr()
+                _nat.call("bcm_scan_fwd", f, s)
+            if _chunk_g is not None:
+                a.chunk_g = _chunk_g.data_ptr()
             _nat.call("bcm_scan_bwd", a, s)
             if pw_B is not None:  # dB, dC hold dW_eff here
                 dpw_B, dpw_C = dB @ B.t(), dC @ C.t()

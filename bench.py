@@ -144,6 +144,11 @@ class Path:
             self.E, self.ms = E, ms
             a = self.args
             a.n_events, a.max_seqlen, a.n_chunks = E, ms, max(1, -(-ms // 2048))
+            # pass-start states of channels longer than one pass (written by
+            # the forward, read by the backward)
+            _, n_pass, needs = nat.scan_chunking(a)
+            self.chunk_g = t.empty((self.NC, n_pass, w.N), dtype=t.float32, device=self.u.device) if needs else None
+            a.chunk_g = self.chunk_g.data_ptr() if needs else None
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define BCM_ABI_VERSION 1
+#define BCM_ABI_VERSION 2
 
 typedef struct ihipStream_t* bcm_stream_t; /* == hipStream_t */
 
@@ -197,8 +197,20 @@ typedef struct bcm_scan_args {
   float* ddt_active;           /* [dim] */
   float* dD;                   /* [dim] or NULL */
   void* dz;                    /* [E] when z != NULL */
+  /* [NC, n_pass, dstate] state h at the start of every pass of a channel
+   * (pass 0 unused), n_pass from bcm_scan_chunking. The forward
+   * writes it when non-NULL; the backward needs it when the pass is shorter
+   * than 2048 events (n_pass > 1 and pass_len < 2048), else it re-seeds
+   * from x_saved as the reference does. */
+  float* chunk_g;
 } bcm_scan_args;
 
+/* Events per pass of a channel (pass_len) and passes of the longest channel
+ * (n_pass) for these arguments (max_seqlen, n_events, n_channels, dstate):
+ * channels longer than one pass carry their state between passes. Returns
+ * BCM_OK; *needs_chunk_g = 1 when the backward must be given chunk_g. */
+int bcm_scan_chunking(const bcm_scan_args* args, int32_t* pass_len, int32_t* n_pass,
+                      int32_t* needs_chunk_g);
 /* selective_scan_fwd_flat_ch, depthwise mode (selective_scan.cpp:674-884,
  * selective_scan_fwd_kernel.cuh:403-728). */
 int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream);

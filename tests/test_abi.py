@@ -47,8 +47,8 @@ def test_library_exports_every_header_symbol(lib):
 
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
-    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 24 pointers
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 24 * 8
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 25 pointers
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 25 * 8
 
 
 def test_scan_bc_layout_matches_header():
@@ -58,7 +58,7 @@ def test_scan_bc_layout_matches_header():
 
 
 def test_host_helpers(lib):
-    assert lib.bcm_abi_version() == 1
+    assert lib.bcm_abi_version() == 2
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64
     assert lib.bcm_bitmask_words(1) == 32 and lib.bcm_bitmask_words(1025) == 64
     assert lib.bcm_tile_count(2048) == nat.tile_count(2048) == 32

@@ -17,9 +17,14 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float32: (1e-4, 1e-5), torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3)}
 
 
-def _case(B, D, L, p, N, dtype, seed, with_z=False, with_D=True, empty_every=0, dim=None):
+def _case(B, D, L, p, N, dtype, seed, with_z=False, with_D=True, empty_every=0, dim=None, p_short=None,
+          long_every=2):
     g = torch.Generator().manual_seed(seed)
     mem = (torch.rand(B, D, L, generator=g) < p).float()
+    if p_short is not None:  # bursty mix: one channel in long_every keeps density p
+        rows = mem.view(B * D, L)
+        short = torch.arange(B * D) % long_every != 0
+        rows[short] = (torch.rand(int(short.sum()), L, generator=g) < p_short).float()
     if empty_every:
         mem.view(B * D, L)[::empty_every] = 0.0
     ch, t, k, cu, counts, ms = orc.extract_base_events(mem.numpy(), 0.5)
@@ -159,3 +164,51 @@ def test_scan_is_deterministic(cuda_device):
     r1, g1 = _run_and_check(c, torch.float32, cuda_device)
     r2, g2 = _run_and_check(c, torch.float32, cuda_device)
     assert all(torch.equal(a, b) for a, b in zip(r1, r2)) and all(torch.equal(a, b) for a, b in zip(g1, g2))
+
+
+# Long channels among short ones: max_seqlen > 512 with a mean channel length
+# of at most 512 selects passes shorter than the 2048-event saved-state chunk
+# (16 lanes x 16 items with the decay table, 64 x 8 without), carried through
+# chunk_g; x still holds the state after every 2048 events.
+BURSTY = [  # B, D, L, p_long, p_short, long_every, N
+    (2, 8, 1200, 0.6, 0.02, 2, 16),   # ~720-event channels: three 256-event passes
+    (2, 6, 4500, 0.6, 0.01, 6, 16),   # ~2700-event channels: x has two chunks
+    (2, 4, 1500, 0.5, 0.02, 2, 80),   # no decay table: 512-event passes
+]
+
+
+@pytest.mark.parametrize("B,D,L,p,ps,le,N", BURSTY)
+def test_scan_multipass_chunk_states(cuda_device, B, D, L, p, ps, le, N):
+    print(f"multipass case B={B} D={D} L={L} p={p}/{ps} every {le} N={N}", flush=True)
+    c = _case(B, D, L, p, N, torch.float32, seed=L + N, p_short=ps, long_every=le, with_z=True)
+    ms, E, NC = int(c["ms"]), len(c["ch"]), B * D
+    assert ms > 512 and E / NC <= 512
+    a = ssc._nat.ScanArgs()
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen = E, NC, D, N, ms
+    pass_len, n_pass, needs = ssc._nat.scan_chunking(a)
+    assert needs and pass_len < 2048 and n_pass > 1
+    # direct API: the backward recomputes the pass states
+    _, gb_direct = _run_and_check(c, torch.float32, cuda_device)
+    # autograd: the forward's pass states are kept for the backward
+    dev = cuda_device
+    leaves = {n: c[n].to(dev).requires_grad_(True) for n in ("u", "dt_i", "dt_a", "A", "WB", "WC", "D", "z")}
+    k_t, cu_t = torch.from_numpy(c["k"]).to(dev), torch.from_numpy(c["cu"]).to(dev)
+    out, x = ssi.selective_scan_flat_ch_fn(leaves["u"], k_t, cu_t, ms, leaves["dt_i"], leaves["dt_a"], leaves["A"],
+                                           leaves["WB"], leaves["WC"], D=leaves["D"], z=leaves["z"],
+                                           is_depthwise_bc=True)
+    out.backward(c["dout"].to(dev))
+    for name, g in zip(("u", "A", "WB", "WC", "dt_i", "dt_a", "D", "z"), gb_direct):
+        assert torch.equal(leaves[name].grad, g), name  # same pass states either way
+
+
+def test_scan_backward_requires_chunk_states(cuda_device):
+    """The C ABI refuses a multi-pass backward without chunk_g instead of
+    reading states it was not given."""
+    c = _case(2, 8, 1200, 0.6, 16, torch.float32, seed=3, p_short=0.02)
+    a = ssc._nat.ScanArgs()
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen = len(c["ch"]), 16, 8, 16, int(c["ms"])
+    a.n_chunks, a.dtype = 1, 0
+    a.cu_seqlens = a.dt_idle = a.dt_active = a.A = a.W_B = a.W_C = a.u = a.k = 16
+    a.dA = a.dW_B = a.dW_C = a.ddt_idle = a.ddt_active = a.dout = a.du = 16
+    lib = ssc._nat.lib()
+    assert lib.bcm_scan_bwd(a, None) == 1 and "chunk_g required" in lib.bcm_last_error().decode()
