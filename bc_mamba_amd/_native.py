@@ -31,7 +31,7 @@ class ScanArgs(ctypes.Structure):
         ("out", c_p), ("out_z", c_p), ("x", c_p),
         ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
-        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p),
+        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("split_ws", c_p),
     ]
 
 
@@ -69,6 +69,7 @@ SIGNATURES = {
     "bcm_gather_bwd_rows": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p]),
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_scan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(ScanArgs)]),
     "bcm_scan_chunking": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(c_i32), ctypes.POINTER(c_i32),
                                   ctypes.POINTER(c_i32)]),
     "bcm_scan_var_fwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p]),

@@ -42,6 +42,7 @@
 #include "bcm_common.hpp"
 #include "scan_group.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -126,6 +127,17 @@ __device__ __forceinline__ bool exact_products(const float* sAl, int N, float dt
   return f;
 }
 
+// Value i of model channel d's parameter-gradient block (dA[d, :],
+// dW_B[d, :], dW_C[d, :], ddt_idle[d], ddt_active[d], dD[d]).
+__device__ __forceinline__ void store_param_grad(const bcm_scan_args& a, int d, int N, int i, float v) {
+  if (i < N) a.dA[(int64_t)d * N + i] = v;
+  else if (i < 2 * N) a.dW_B[(int64_t)d * N + (i - N)] = v;
+  else if (i < 3 * N) a.dW_C[(int64_t)d * N + (i - 2 * N)] = v;
+  else if (i == 3 * N) a.ddt_idle[d] = v;
+  else if (i == 3 * N + 1) a.ddt_active[d] = v;
+  else if (a.dD) a.dD[d] = v;
+}
+
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a) {
   using Ops = Grp<G>;
@@ -135,7 +147,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
-  const int d = blockIdx.x;
+  // S workgroups per model channel d (S = gridDim.x / dim); workgroup sp
+  // takes the rounds of channels sp, sp + S, sp + 2S, ...
+  const int d = blockIdx.x % a.dim;
+  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
   const int nw = blockDim.x / kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / G, j = lane % G;
@@ -200,8 +215,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
   };
   int e0, n;
-  channel(slot, e0, n);
-  if (n_per_d > 0) issue(e0, n, 0);
+  const int b_first = sp * nslots, b_step = nslots * S;
+  channel(b_first + slot, e0, n);
+  if (n_per_d > b_first) issue(e0, n, 0);
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
@@ -212,15 +228,14 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
     sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
   }
   if (TBL) build_decay_table(sT, a, d, dti, dta);
-  if (n_per_d > 0) to_tiles();
+  if (n_per_d > b_first) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
-  (void)nslots;
 
-  for (int b0 = 0; b0 < n_per_d; b0 += nw * CPW) {
+  for (int b0 = b_first; b0 < n_per_d; b0 += b_step) {
     const int b = b0 + slot;
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    if (b0 > 0) channel(b, e0, n);
+    if (b0 > b_first) channel(b, e0, n);
     const int nch = n > 0 ? (n + C - 1) / C : 0;
     const int wmax = wave_max_dpp(nch);
     for (int c = 0; c < wmax; ++c) {
@@ -232,7 +247,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
       const int cend = min(n, (c + 1) * C);
       const int xc = (cend - 1) / kXChunk;
       const bool xsave = c < nch && (cend % kXChunk == 0 || cend == n) && xc < nck;
-      if (b0 > 0 || c > 0) {
+      if (b0 > b_first || c > 0) {
         issue(e0, n, c);
         to_tiles();
       }
@@ -370,7 +385,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
-  const int d = blockIdx.x;
+  // S workgroups per model channel d (S = gridDim.x / dim); workgroup sp
+  // takes the rounds of channels sp, sp + S, sp + 2S, ...
+  const int d = blockIdx.x % a.dim;
+  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
   const int nw = blockDim.x / kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / G, j = lane % G;
@@ -446,10 +464,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
   };
   int e0, n;
-  channel(slot, e0, n);
+  const int b_first = sp * nslots, b_step = nslots * S;
+  channel(b_first + slot, e0, n);
   int nch = n > 0 ? (n + C - 1) / C : 0;
   int wmax = wave_max_dpp(nch);
-  if (n_per_d > 0 && wmax > 0) issue(e0, n, wmax - 1);
+  if (n_per_d > b_first && wmax > 0) issue(e0, n, wmax - 1);
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
@@ -465,10 +484,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   }
   for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   if (TBL) build_decay_table(sT, a, d, dti, dta);
-  if (n_per_d > 0 && wmax > 0) to_tiles();
+  if (n_per_d > b_first && wmax > 0) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
-  for (int b0 = 0; b0 < n_per_d; b0 += nslots) {
+  for (int b0 = b_first; b0 < n_per_d; b0 += b_step) {
     const int b = b0 + slot;
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
@@ -738,8 +757,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       cacc[3 * N + 1] += ddta_l;
       cacc[3 * N + 2] += dD_l;
     }
-    if (b0 + nslots < n_per_d) {  // the next channel of this lane group
-      channel(b + nslots, e0, n);
+    if (b0 + b_step < n_per_d) {  // the next channel of this lane group
+      channel(b + b_step, e0, n);
       nch = n > 0 ? (n + C - 1) / C : 0;
       wmax = wave_max_dpp(nch);
       if (wmax > 0) {
@@ -753,18 +772,32 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   for (int i = threadIdx.x; i < NA; i += blockDim.x) {
     float v = 0.0f;
     for (int sl = 0; sl < nslots; ++sl) v += sacc[sl * NA + i];
-    if (i < N) a.dA[(int64_t)d * N + i] = v;
-    else if (i < 2 * N) a.dW_B[(int64_t)d * N + (i - N)] = v;
-    else if (i < 3 * N) a.dW_C[(int64_t)d * N + (i - 2 * N)] = v;
-    else if (i == 3 * N) a.ddt_idle[d] = v;
-    else if (i == 3 * N + 1) a.ddt_active[d] = v;
-    else if (a.dD) a.dD[d] = v;
+    if (S > 1) a.split_ws[((int64_t)sp * a.dim + d) * NA + i] = v;  // summed by k_scan_param_reduce
+    else store_param_grad(a, d, N, i, v);
   }
 }
 
+// Parameter gradients of S workgroups per model channel: the S partials of
+// each value summed in split order (deterministic).
+__global__ __launch_bounds__(256) void k_scan_param_reduce(const bcm_scan_args a, int S) {
+  const int N = a.dstate, NA = 3 * N + 3;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)a.dim * NA) return;
+  const int d = (int)(t / NA), i = (int)(t % NA);
+  float v = 0.0f;
+  for (int sp = 0; sp < S; ++sp) v += a.split_ws[((int64_t)sp * a.dim + d) * NA + i];
+  store_param_grad(a, d, N, i, v);
+}
+
 // ------------------------------------------------------------ host dispatch
+struct Plan {
+  int nw;      // waves per workgroup
+  int64_t lds; // dynamic LDS bytes
+  int S;       // workgroups per model channel
+};
+
 template <int G, int R, typename T, bool Z, bool BWD, bool TBL>
-static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
+static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* query) {
   constexpr int CPW = kWave / G;
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
   int nw = (per_d + CPW - 1) / CPW;
@@ -783,10 +816,27 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn) {
   }
   if (lds > cap) return set_error(BCM_EINVAL, "%s: dstate %d needs %lld bytes of LDS (> %lld)", fn, a.dstate,
                                   (long long)lds, (long long)cap);
-  if (BWD)
-    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
-  else
-    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), dim3(a.dim), dim3(nw * kWave), (size_t)lds, s, a);
+  // fewer model channels than CUs and several rounds of channels each:
+  // split each model channel's rounds over S workgroups
+  const int rounds = (per_d + nw * CPW - 1) / (nw * CPW);
+  const int cus = device_cus();
+  int S = 1;
+  if (a.dim < cus && rounds > 1) S = std::min(rounds, std::max(1, cus / a.dim));
+  if (query) {
+    *query = Plan{nw, lds, S};
+    return BCM_OK;
+  }
+  if (BWD && !a.split_ws) S = 1;  // no workspace for the partials: one workgroup per model channel
+  const dim3 grid((unsigned)((int64_t)a.dim * S));
+  if (BWD) {
+    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a);
+    int rc = check_launch(fn);
+    if (rc || S == 1) return rc;
+    const int64_t tot = (int64_t)a.dim * (3 * a.dstate + 3);
+    hipLaunchKernelGGL(k_scan_param_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a, S);
+  } else {
+    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a);
+  }
   return check_launch(fn);
 }
 
@@ -829,21 +879,21 @@ static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* ne
 }
 
 template <typename T, bool Z, bool BWD>
-static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn) {
+static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q = nullptr) {
   switch (pick_shape(a)) {
-    case S16x4: return launch<16, 4, T, Z, BWD, true>(a, s, fn);
-    case S16x8: return launch<16, 8, T, Z, BWD, true>(a, s, fn);
-    case S16x16: return launch<16, 16, T, Z, BWD, true>(a, s, fn);
-    case S16x24: return launch<16, 24, T, Z, BWD, true>(a, s, fn);
-    case S32x16: return launch<32, 16, T, Z, BWD, true>(a, s, fn);
-    case S64x4: return launch<64, 4, T, Z, BWD, false>(a, s, fn);
-    case S64x8: return launch<64, 8, T, Z, BWD, false>(a, s, fn);
+    case S16x4: return launch<16, 4, T, Z, BWD, true>(a, s, fn, q);
+    case S16x8: return launch<16, 8, T, Z, BWD, true>(a, s, fn, q);
+    case S16x16: return launch<16, 16, T, Z, BWD, true>(a, s, fn, q);
+    case S16x24: return launch<16, 24, T, Z, BWD, true>(a, s, fn, q);
+    case S32x16: return launch<32, 16, T, Z, BWD, true>(a, s, fn, q);
+    case S64x4: return launch<64, 4, T, Z, BWD, false>(a, s, fn, q);
+    case S64x8: return launch<64, 8, T, Z, BWD, false>(a, s, fn, q);
     default: break;
   }
   const bool tbl = a.dstate <= kTabMaxN;
   if (pick_shape(a) == S64x16)
-    return tbl ? launch<64, 16, T, Z, BWD, true>(a, s, fn) : launch<64, 16, T, Z, BWD, false>(a, s, fn);
-  return tbl ? launch<64, 32, T, Z, BWD, true>(a, s, fn) : launch<64, 32, T, Z, BWD, false>(a, s, fn);
+    return tbl ? launch<64, 16, T, Z, BWD, true>(a, s, fn, q) : launch<64, 16, T, Z, BWD, false>(a, s, fn, q);
+  return tbl ? launch<64, 32, T, Z, BWD, true>(a, s, fn, q) : launch<64, 32, T, Z, BWD, false>(a, s, fn, q);
 }
 
 template <bool BWD>
@@ -899,6 +949,22 @@ int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream) {
 
 int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream) {
   return bcm::scan_entry<true>(args, stream, "bcm_scan_bwd");
+}
+
+int64_t bcm_scan_bwd_workspace_bytes(const bcm_scan_args* args) {
+  if (!args || !bcm::dtype_ok(args->dtype) || args->dim < 1 || args->dstate < 1 || args->dstate > 256 ||
+      args->n_channels < 1)
+    return 0;
+  bcm::Plan q{1, 0, 1};
+  int rc = BCM_OK;
+  const bool z = args->z != nullptr;
+  bcm::dispatch_dtype(args->dtype, [&](auto tag) {
+    using T = decltype(tag);
+    rc = z ? bcm::dispatch_shape<T, true, true>(*args, nullptr, "bcm_scan_bwd_workspace_bytes", &q)
+           : bcm::dispatch_shape<T, false, true>(*args, nullptr, "bcm_scan_bwd_workspace_bytes", &q);
+  });
+  if (rc || q.S <= 1) return 0;
+  return 4 * (int64_t)q.S * args->dim * (3 * args->dstate + 3);
 }
 
 int bcm_scan_chunking(const bcm_scan_args* args, int32_t* pass_len, int32_t* n_pass, int32_t* needs_chunk_g) {

@@ -285,6 +285,9 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 _nat.call("bcm_scan_fwd", f, s)
             if _chunk_g is not None:
                 a.chunk_g = _chunk_g.data_ptr()
+            split_bytes = int(_nat.lib().bcm_scan_bwd_workspace_bytes(a))
+            split_ws = torch.empty(split_bytes // 4, dtype=torch.float32, device=dev) if split_bytes else None
+            a.split_ws = split_ws.data_ptr() if split_ws is not None else None
             _nat.call("bcm_scan_bwd", a, s)
             if pw_B is not None:  # dB, dC hold dW_eff here
                 dpw_B, dpw_C = dB @ B.t(), dC @ C.t()

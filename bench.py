@@ -28,6 +28,8 @@ METRIC = "fwd+bwd events/s & achieved HBM GB/s, B32 D256 L2048 N16 at 15% densit
 HBM_PEAK_GBS = 8000.0
 PROBE_STEPS = 5
 CAL_BYTES = 256 << 20  # device-to-device copy that calibrates the PMC byte counters
+FLUSH_BYTES = 512 << 20  # written before each cold step: more than L2 plus the 256 MB MALL
+COLD_REPS = 11
 
 # device kernels behind each stage of Path.KERNELS (symbol substrings)
 STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
@@ -149,6 +151,10 @@ class Path:
             _, n_pass, needs = nat.scan_chunking(a)
             self.chunk_g = t.empty((self.NC, n_pass, w.N), dtype=t.float32, device=self.u.device) if needs else None
             a.chunk_g = self.chunk_g.data_ptr() if needs else None
+            # parameter-gradient partials when model channels are split over workgroups
+            nb = int(nat.lib().bcm_scan_bwd_workspace_bytes(a))
+            self.split_ws = t.empty(max(nb, 4) // 4, dtype=t.float32, device=self.u.device) if nb else None
+            a.split_ws = self.split_ws.data_ptr() if nb else None
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense),
@@ -321,6 +327,7 @@ def main():
         path.step(timed=(dominant,))
     torch.cuda.synchronize()
     dom_ms = path.kernel_ms(dominant)
+    cold_ms = cold_step_ms(path, dev, COLD_REPS)
 
     E, ms = path.E, path.ms
     su = torch.tensor([], dtype=w.dtype).element_size()
@@ -352,6 +359,10 @@ def main():
         "algorithmic_bytes": total_bytes,
         "path_frac_of_hbm_peak": total_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": per_kernel,
+        # one step after a 512 MiB write has flushed L2 and the 256 MB MALL
+        # (median of COLD_REPS, HIP events); ms_per_step is back-to-back steps
+        "cold_ms_per_step": cold_ms,
+        "cold_events_per_s": E / (cold_ms * 1e-3),
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None, "launch_ms": dom_ms,
                      "bytes_per_launch": kernel_bytes[dominant]},
@@ -365,6 +376,24 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cfg, args.cpu_batches)
     print(json.dumps(result), flush=True)
+
+
+def cold_step_ms(path, dev, reps):
+    """Median time of one step, each after writing a 512 MiB scratch buffer
+    (larger than L2 plus the 256 MB MALL), HIP events around the step only."""
+    import torch
+    scratch = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
+    times = []
+    for _ in range(reps):
+        scratch.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        path.step()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    del scratch
+    return sorted(times)[len(times) // 2]
 
 
 def api_path_ms(w, dev, steps, warmup):

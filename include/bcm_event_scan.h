@@ -203,6 +203,11 @@ typedef struct bcm_scan_args {
    * than 2048 events (n_pass > 1 and pass_len < 2048), else it re-seeds
    * from x_saved as the reference does. */
   float* chunk_g;
+  /* backward workspace of bcm_scan_bwd_workspace_bytes(args) bytes, or
+   * NULL: with it, model channels with many channels each are split over
+   * several workgroups whose parameter-gradient partials are summed in a
+   * fixed order (same results either way up to that order). */
+  float* split_ws;
 } bcm_scan_args;
 
 /* Events per pass of a channel (pass_len) and passes of the longest channel
@@ -211,6 +216,9 @@ typedef struct bcm_scan_args {
  * BCM_OK; *needs_chunk_g = 1 when the backward must be given chunk_g. */
 int bcm_scan_chunking(const bcm_scan_args* args, int32_t* pass_len, int32_t* n_pass,
                       int32_t* needs_chunk_g);
+/* Bytes of bcm_scan_args.split_ws for a backward with these arguments (0:
+ * no split, split_ws may stay NULL). */
+int64_t bcm_scan_bwd_workspace_bytes(const bcm_scan_args* args);
 /* selective_scan_fwd_flat_ch, depthwise mode (selective_scan.cpp:674-884,
  * selective_scan_fwd_kernel.cuh:403-728). */
 int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream);

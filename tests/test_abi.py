@@ -47,8 +47,8 @@ def test_library_exports_every_header_symbol(lib):
 
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
-    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 25 pointers
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 25 * 8
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 26 pointers
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 26 * 8
 
 
 def test_scan_bc_layout_matches_header():

@@ -212,3 +212,22 @@ def test_scan_backward_requires_chunk_states(cuda_device):
     a.dA = a.dW_B = a.dW_C = a.ddt_idle = a.ddt_active = a.dout = a.du = 16
     lib = ssc._nat.lib()
     assert lib.bcm_scan_bwd(a, None) == 1 and "chunk_g required" in lib.bcm_last_error().decode()
+
+
+@pytest.mark.parametrize("B,D,L,p,ps,N", [
+    (96, 2, 300, 0.5, None, 16),    # 96 channels per model channel: three rounds of 32
+    (64, 2, 1200, 0.6, 0.02, 16),   # bursty multi-pass, two rounds
+])
+def test_scan_split_workgroups(cuda_device, B, D, L, p, ps, N):
+    """Few model channels with many channels each: the backward splits every
+    model channel over several workgroups (bcm_scan_bwd_workspace_bytes > 0)
+    and sums their parameter-gradient partials in a fixed order."""
+    print(f"split case B={B} D={D} L={L} p={p}/{ps} N={N}", flush=True)
+    c = _case(B, D, L, p, N, torch.float32, seed=B + L, p_short=ps)
+    a = ssc._nat.ScanArgs()
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen = len(c["ch"]), B * D, D, N, int(c["ms"])
+    a.n_chunks, a.dtype = max(1, -(-int(c["ms"]) // 2048)), 0
+    assert ssc._nat.lib().bcm_scan_bwd_workspace_bytes(a) > 0
+    r1, g1 = _run_and_check(c, torch.float32, cuda_device)
+    r2, g2 = _run_and_check(c, torch.float32, cuda_device)
+    assert all(torch.equal(x, y) for x, y in zip(g1, g2))  # deterministic
