@@ -26,12 +26,14 @@ try:
     from . import _native as _nat
     from . import extract_events_cuda as _ee_cuda
     from . import restore_dense_cuda_nodecay
+    from .causal_conv1d import causal_conv1d_fn
     from .runtime_breakdown import cuda_stage
     from .selective_scan_interface import selective_scan_flat_ch_fn
 except ImportError:  # imported with this directory on sys.path
     import _native as _nat
     import extract_events_cuda as _ee_cuda
     import restore_dense_cuda_nodecay
+    from causal_conv1d import causal_conv1d_fn
     from runtime_breakdown import cuda_stage
     from selective_scan_interface import selective_scan_flat_ch_fn
 
@@ -248,6 +250,11 @@ class Mamba(nn.Module):
         return channel_ids, time_steps, k_flat, cu_seqlens, max_seqlen, x_conv_flat
 
     def _conv(self, x, seqlen):
+        """silu(conv1d(x)[..., :L]) (e_model.py:442-451). The fused path runs
+        it as the HIP causal conv (causal_conv1d_fn, the reference's fast
+        path); the reference composition keeps nn.Conv1d, its fallback."""
+        if self.fused_event_path:
+            return causal_conv1d_fn(x, self.conv1d.weight[:, 0, :], self.conv1d.bias, activation="silu")
         return self.act(self.conv1d(x)[..., :seqlen])
 
     def forward(self, hidden_states, inference_params=None):

@@ -293,6 +293,9 @@ def main():
     from bc_mamba_amd.workloads import make_workload
     _native.lib()
     dev = torch.device("cuda:0")
+    if args.cfg == 4:
+        print(json.dumps(model_step_bench(args, dev)), flush=True)
+        return
     w = make_workload(args.cfg).to(dev)
     path = Path(w, dev)
 
@@ -376,6 +379,49 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cfg, args.cpu_batches)
     print(json.dumps(result), flush=True)
+
+
+def model_step_bench(args, dev):
+    """Config 4: one training step (forward, cross-entropy loss, backward) of
+    the 6-layer model, B=50 L=1024, random init and byte tokens. events/s
+    counts the events every layer's extraction routes (its input spikes,
+    times expand) per step."""
+    import torch
+    from bc_mamba_amd.workloads import make_model_workload
+    model, tokens, labels = make_model_workload(device=dev)
+    events = []
+    hooks = [blk.core.register_forward_pre_hook(
+        lambda mod, inp: events.append(int((inp[0] > mod.threshold).sum()) * mod.expand)) for blk in model.blocks]
+
+    def step():
+        loss = torch.nn.functional.cross_entropy(model(tokens), labels)
+        loss.backward()
+        for p in model.parameters():
+            p.grad = None
+
+    step()
+    for h in hooks:
+        h.remove()
+    per_layer = list(events)
+    E = sum(per_layer)
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    return {
+        "metric": METRIC, "value": E / (ms * 1e-3), "unit": "events/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config 4: 6-layer model training step (fwd + CE loss + bwd), d_model 256, "
+                               "d_inner 512, N 16, L 1024, B 50, byte tokens, random init",
+                   "events_per_step": E, "events_per_layer": per_layer,
+                   "density_per_layer": [e / (50 * 1024 * 512) for e in per_layer]},
+        "roofline": None,
+    }
 
 
 def cold_step_ms(path, dev, reps):

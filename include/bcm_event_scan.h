@@ -268,6 +268,19 @@ int64_t bcm_scan_var_workspace_bytes(int64_t n_events, int dstate);
 int bcm_scan_var_bwd(const bcm_scan_args* args, const bcm_scan_bc* bc, void* workspace,
                      int64_t workspace_bytes, bcm_stream_t stream);
 
+/* ---- causal depthwise conv1d (+ SiLU): the producer of x_conv ---------- */
+/* e_model.py:442-451 (silu(conv1d(x)[..., :L]), groups = channels, padding
+ * K-1; or causal_conv1d_fn(x, w, bias, activation="silu")). x, out:
+ * [B, D, L] contiguous (dtype); weight [D, K] and bias [D] fp32 (bias may be
+ * NULL); K <= 8. silu = 0 gives the plain convolution. */
+int bcm_causal_conv1d_fwd(const void* x, int dtype, const float* weight, const float* bias, int64_t B,
+                          int64_t D, int64_t L, int K, int silu, void* out, bcm_stream_t stream);
+/* Backward: dx [B, D, L] (dtype), dweight [D, K] and dbias [D] (fp32, fully
+ * written; dbias may be NULL), the SiLU derivative recomputed from x. */
+int bcm_causal_conv1d_bwd(const void* x, int dtype, const float* weight, const float* bias, const void* dout,
+                          int64_t B, int64_t D, int64_t L, int K, int silu, void* dx, float* dweight,
+                          float* dbias, bcm_stream_t stream);
+
 /* ---- (3) zero-order-hold restore ---------------------------------------- */
 /* Event index of sorted per-channel time steps (the restore kernels' input
  * when the caller has no bitmask): bitmask [n_rows, words], tile_start

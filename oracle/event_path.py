@@ -27,6 +27,8 @@ How each function is pinned (tests/test_oracle.py):
   bc_grad_layout       constant and tiled layouts; adjointness of the two
   pw_effective /       finite differences of the composed scan loss in pw
   pw_grads             and in W
+  conv1d_fwd / _bwd    torch.nn.functional.conv1d (groups = D, padding K-1,
+                       the reference's own fallback) and float64 autograd
 """
 import math
 
@@ -411,6 +413,42 @@ def pw_grads(pw, W, dW_eff):
     dW[d', s] = Σ_d pw[d, d'] dW_eff[d, s],  dpw[d, d'] = Σ_s dW_eff[d, s] W[d', s]."""
     pw, W, g = (np.asarray(v, np.float64) for v in (pw, W, dW_eff))
     return pw.T @ g, g @ W.T
+
+
+# ------------------------------------------------- causal conv1d + SiLU
+def conv1d_fwd(x, w, bias=None, silu=True):
+    """e_model.py:442-451: out[b,d,t] = act(bias[d] + Σ_k w[d,k] x[b,d,t-(K-1)+k]),
+    x = 0 before t = 0, act = SiLU or identity. x [B, D, L], w [D, K]."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    B, D, L = x.shape
+    K = w.shape[1]
+    xp = np.concatenate([np.zeros((B, D, K - 1)), x], axis=2)
+    pre = np.zeros((B, D, L)) + (np.asarray(bias, np.float64)[None, :, None] if bias is not None else 0.0)
+    for k in range(K):
+        pre += w[None, :, k, None] * xp[:, :, k:k + L]
+    return pre / (1.0 + np.exp(-pre)) if silu else pre
+
+
+def conv1d_bwd(x, w, bias, dout, silu=True):
+    """Gradients of conv1d_fwd: (dx, dw [D, K], dbias [D])."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    B, D, L = x.shape
+    K = w.shape[1]
+    pre = conv1d_fwd(x, w, bias, silu=False)
+    g = np.asarray(dout, np.float64)
+    if silu:
+        sg = 1.0 / (1.0 + np.exp(-pre))
+        g = g * sg * (1.0 + pre * (1.0 - sg))
+    xp = np.concatenate([np.zeros((B, D, K - 1)), x], axis=2)
+    gp = np.concatenate([g, np.zeros((B, D, K - 1))], axis=2)
+    dx = np.zeros((B, D, L))
+    dw = np.zeros((D, K))
+    for k in range(K):
+        dx += w[None, :, k, None] * gp[:, :, K - 1 - k:K - 1 - k + L]
+        dw[:, k] = (g * xp[:, :, k:k + L]).sum(axis=(0, 2))
+    return dx, dw, g.sum(axis=(0, 2))
 
 
 # ------------------------------------------------------------------ restore

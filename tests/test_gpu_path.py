@@ -56,7 +56,8 @@ def test_mamba_block_fused_matches_reference_composition(cuda_device, expand):
         (o * torch.linspace(-1, 1, o.numel(), device=cuda_device).view_as(o)).sum().backward()
         outs.append(o.detach())
         grads.append({n: p.grad.detach().clone() for n, p in blk.named_parameters() if p.grad is not None})
-    assert_close(outs[0].cpu(), outs[1].cpu().numpy(), 1e-6, 1e-7, "block out")
+    # the two paths differ in conv and scan rounding order: the fp32 parity bar
+    assert_close(outs[0].cpu(), outs[1].cpu().numpy(), 1e-4, 1e-5, "block out")
     assert grads[0].keys() == grads[1].keys() and "W_BC" in grads[0] and "A_log" in grads[0]
     for n in grads[0]:
         assert_close(grads[0][n].cpu(), grads[1][n].cpu().numpy(), 1e-4, 1e-5, n)
@@ -103,3 +104,25 @@ def test_config1_full_size_properties(cuda_device):
                          is_depthwise_bc=True)
     for a, b2 in zip(gb, g2):
         assert_close(n(b2), 2.0 * n(a), 1e-5, 1e-6, "linearity")
+
+
+def test_config4_model_fused_matches_reference_composition(cuda_device):
+    """The config-4 model (lra_impl.py:1429-1615 composition, small sizes):
+    a training step through every block's fused event path (HIP extraction,
+    conv, scan, restore) matches the reference composition (nn.Conv1d,
+    reference-order extraction and restore) in loss and every gradient."""
+    from bc_mamba_amd.workloads import make_model_workload
+    model, tokens, labels = make_model_workload(seed=3, B=2, L=200, device=cuda_device, d_model=32, n_layers=2)
+    losses, grads = [], []
+    for fused in (True, False):
+        for blk in model.blocks:
+            blk.core.fused_event_path = fused
+        model.zero_grad()
+        loss = torch.nn.functional.cross_entropy(model(tokens), labels)
+        loss.backward()
+        losses.append(float(loss))
+        grads.append({n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None})
+    assert np.isfinite(losses[0]) and losses[0] == pytest.approx(losses[1], rel=1e-5)
+    assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 10
+    for n in grads[0]:
+        assert_close(grads[0][n].cpu(), grads[1][n].cpu().numpy(), 1e-3, 1e-4, n)

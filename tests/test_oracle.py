@@ -338,6 +338,29 @@ def test_pw_grads_finite_difference():
         assert num == pytest.approx(g[idx], rel=1e-6, abs=1e-9), name
 
 
+# --------------------------------------------------- causal conv1d + SiLU
+@pytest.mark.parametrize("K,silu,with_bias", [(4, True, True), (4, False, False), (1, True, True), (7, True, False)])
+def test_conv1d_matches_torch_conv_and_autograd(K, silu, with_bias):
+    B, D, L = 2, 5, 37
+    x = RNG.standard_normal((B, D, L))
+    w = RNG.standard_normal((D, K))
+    bias = RNG.standard_normal(D) if with_bias else None
+    dout = RNG.standard_normal((B, D, L))
+    xt = torch.tensor(x, requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    bt = torch.tensor(bias, requires_grad=True) if with_bias else None
+    y = torch.nn.functional.conv1d(xt, wt[:, None, :], bt, padding=K - 1, groups=D)[..., :L]
+    if silu:
+        y = torch.nn.functional.silu(y)
+    y.backward(torch.tensor(dout))
+    assert_close(orc.conv1d_fwd(x, w, bias, silu), y.detach().numpy(), rtol=1e-12, atol_rel=1e-14, name="out")
+    dx, dw, db = orc.conv1d_bwd(x, w, bias, dout, silu)
+    assert_close(dx, xt.grad.numpy(), rtol=1e-12, atol_rel=1e-14, name="dx")
+    assert_close(dw, wt.grad.numpy(), rtol=1e-12, atol_rel=1e-14, name="dw")
+    if with_bias:
+        assert_close(db, bt.grad.numpy(), rtol=1e-12, atol_rel=1e-14, name="dbias")
+
+
 # ---------------------------------------------------------------- restore
 def test_restore_fwd_brute_force():
     B, D, L = 2, 3, 45
