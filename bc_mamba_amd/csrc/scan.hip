@@ -840,34 +840,44 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
   return check_launch(fn);
 }
 
-// Lane-group shape (G lanes x R items per pass of a channel). Up to 512
-// events the longest channel fits one pass. Longer channels loop over
-// passes whose length follows the mean channel length (a few bursty
-// channels then cost extra passes instead of padding every channel to the
-// longest one); passes shorter than 2048 events need chunk_g in the
-// backward, 2048-event passes re-seed from x like the reference.
+// Lane-group shape (G lanes x R items per pass of a channel), by a cost
+// model in item slots: a single pass of C >= max_seqlen costs C per channel;
+// passes of C < max_seqlen (C dividing 2048, so x's chunk ends fall on pass
+// ends) cost about (mean/C + 1/2) passes of C per channel. Each pass of a
+// state also pays the group scans, sums and lane products, about
+// kLaneCost items' worth of VALU per lane, i.e. kLaneCost * G slots.
+// Multi-pass shapes shorter than 2048 events need chunk_g in the backward.
 enum ShapeId { S16x4, S16x8, S16x16, S16x24, S32x16, S64x4, S64x8, S64x16, S64x32 };
 constexpr int kShapeG[] = {16, 16, 16, 16, 32, 64, 64, 64, 64};
 constexpr int kShapeR[] = {4, 8, 16, 24, 16, 4, 8, 16, 32};
+constexpr double kLaneCost = 6.0;
 
 static ShapeId pick_shape(const bcm_scan_args& a) {
   const int m = a.max_seqlen;
   const bool tbl = a.dstate <= kTabMaxN;
-  if (tbl) {
-    if (m <= 64) return S16x4;
-    if (m <= 128) return S16x8;
-    if (m <= 256) return S16x16;
-    if (m <= 384) return S16x24;
-    if (m <= 512) return S32x16;
-  } else {
-    if (m <= 256) return S64x4;
-    if (m <= 512) return S64x8;
-  }
   const double mean = (double)a.n_events / (a.n_channels > 0 ? a.n_channels : 1);
-  if (mean <= 256) return tbl ? S16x16 : S64x4;
-  if (mean <= 512) return tbl ? S16x16 : S64x8;
-  if (mean <= 1024) return S64x16;
-  return S64x32;
+  static const ShapeId tab_shapes[] = {S16x4, S16x8, S16x16, S16x24, S32x16, S64x16, S64x32};
+  static const ShapeId plain_shapes[] = {S64x4, S64x8, S64x16, S64x32};
+  const ShapeId* cand = tbl ? tab_shapes : plain_shapes;
+  const int ncand = tbl ? 7 : 4;
+  ShapeId best = cand[ncand - 1];
+  double best_cost = 1e300;
+  for (int i = 0; i < ncand; ++i) {
+    const int C = kShapeG[cand[i]] * kShapeR[cand[i]];
+    const double pass = C + kLaneCost * kShapeG[cand[i]];
+    double cost;
+    if (m <= C) {
+      cost = pass;                                             // one pass per channel
+    } else {
+      if (kXChunk % C != 0) continue;                          // multi-pass needs C | 2048
+      cost = (mean / C + 0.5) * pass;
+    }
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = cand[i];
+    }
+  }
+  return best;
 }
 
 static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* needs_chunk_g) {

@@ -93,6 +93,9 @@ SHAPES = [  # B, D, L, density, N  (max_seqlen lands in each kernel-shape bucket
     # widest lane groups, whose LDS use sits at the per-workgroup limit
     (8, 2, 2600, 0.6, 64),
     (8, 2, 5000, 0.7, 64),    # and two 2048-event chunks (config-3 scale)
+    # no decay table and ~3000-event channels: 2048-event passes that re-seed
+    # from the saved x (no chunk_g), as the reference does
+    (1, 2, 6000, 0.5, 80),
 ]
 
 
