@@ -52,11 +52,14 @@ class CausalConv1dFn(torch.autograd.Function):
         dx = torch.empty_like(x)
         dw = torch.empty_like(w)
         db = torch.empty(D, dtype=torch.float32, device=x.device) if ctx.has_bias else None
+        K = int(w.size(1))
         with torch.cuda.device(x.device):
+            nbytes = int(_nat.lib().bcm_causal_conv1d_bwd_workspace_bytes(B, D, L, K))
+            ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=x.device) if nbytes else None
             _nat.call("bcm_causal_conv1d_bwd", x.data_ptr(), _nat.dtype_code(x.dtype), w.data_ptr(),
-                      b.data_ptr() if b is not None else None, dout.data_ptr(), B, D, L, int(w.size(1)),
+                      b.data_ptr() if b is not None else None, dout.data_ptr(), B, D, L, K,
                       int(ctx.silu), dx.data_ptr(), dw.data_ptr(), db.data_ptr() if db is not None else None,
-                      _nat.stream_of(x))
+                      ws.data_ptr() if ws is not None else None, nbytes, _nat.stream_of(x))
         return dx, dw.to(ctx.wdtype), (db.to(ctx.wdtype) if db is not None else None), None
 
 

@@ -27,6 +27,7 @@ int zero_bytes(void* ptr, int64_t bytes, hipStream_t s, const char* fn);
 inline int64_t bitmask_words(int64_t L) { return ((L + 1023) / 1024) * 32; }
 inline int64_t tile_count(int64_t L) { return (L + kTile - 1) / kTile; }
 inline hipStream_t hs(bcm_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // Compute units of the current device.
 inline int device_cus() {
   int dev = 0, v = 0;

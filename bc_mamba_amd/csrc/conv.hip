@@ -11,121 +11,167 @@
 //   dx[b,d,t] = sum_k w[d,k] * g[b,d,t+(K-1)-k]   (terms past L vanish)
 //   dw[d,k]   = sum_{b,t} g[b,d,t] * x[b,d,t-(K-1)+k],  dbias[d] = sum_{b,t} g
 //
-// MI355X design: rows (b, d) of L steps are contiguous. The forward gives
-// each thread 4 consecutive steps of one row (the K-1 halo values come from
-// the neighbouring lanes' lines in L1), so a wave covers 256 contiguous
-// steps. The backward runs one workgroup per channel d over its B rows: g is
-// recomputed from x (no saved pre-activation), dx is written per row, and
-// dw / dbias accumulate in registers and reduce in LDS in a fixed order
-// (deterministic, no atomics, no workspace). HBM-bound: x and dout read
-// once, out / dx written once.
+// MI355X design: rows (b, d) of L steps are contiguous. Each thread takes 4
+// consecutive steps of one row, read and written as whole 16-byte (fp32) or
+// 8-byte (fp16/bf16) vectors when L is a multiple of 4, with the K-1 halo
+// steps from the neighbouring vectors (L1 hits), so a wave covers 256
+// contiguous steps. The backward recomputes g from x (no saved
+// pre-activation); workgroup (d, p) takes every P-th batch row of channel d
+// (P chosen to fill the chip), writes dx, and reduces its dw / dbias
+// partials in registers and LDS in a fixed order; a small kernel sums the P
+// partials in group order (deterministic, no atomics). HBM-bound: x and dout
+// read once, out / dx written once.
 #include "bcm_common.hpp"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace bcm {
 
 constexpr int kConvMaxK = 8;
 constexpr int kConvSteps = 4;  // consecutive steps per thread
+constexpr int kConvMaxSplit = 64;  // batch groups of the backward
 
-template <typename T, bool SILU>
+// x[t .. t+3] of a row as floats: one 16-byte (fp32) or 8-byte (fp16/bf16)
+// load when VEC (t a multiple of 4, rows aligned), zeros for t < 0 or t >= L
+// (whole vectors: L is a multiple of 4 then); else per element with bounds.
+template <typename T, bool VEC>
+__device__ __forceinline__ void load4(const T* __restrict__ r, int64_t t, int64_t L, float* v) {
+  if (VEC) {
+    if (t < 0 || t >= L) {
+      v[0] = v[1] = v[2] = v[3] = 0.0f;
+    } else if constexpr (sizeof(T) == 4) {
+      const float4 q = *reinterpret_cast<const float4*>(r + t);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(r + t);
+      const T* e = reinterpret_cast<const T*>(&q);
+      v[0] = to_f(e[0]); v[1] = to_f(e[1]); v[2] = to_f(e[2]); v[3] = to_f(e[3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (t + i >= 0 && t + i < L) ? to_f(r[t + i]) : 0.0f;
+  }
+}
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void store4(T* __restrict__ r, int64_t t, int64_t L, const float* v) {
+  if (VEC) {
+    if constexpr (sizeof(T) == 4) {
+      *reinterpret_cast<float4*>(r + t) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      T e[4] = {from_f<T>(v[0]), from_f<T>(v[1]), from_f<T>(v[2]), from_f<T>(v[3])};
+      *reinterpret_cast<uint2*>(r + t) = *reinterpret_cast<const uint2*>(e);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (t + i < L) r[t + i] = from_f<T>(v[i]);
+  }
+}
+
+// KM = 4: width exactly 4 (d_conv's default), straight-line code; KM = 8:
+// any width K <= 8 given at run time.
+template <typename T, bool SILU, bool VEC, int KM>
 __global__ __launch_bounds__(256) void k_conv_fwd(const T* __restrict__ x, const float* __restrict__ w,
                                                   const float* __restrict__ bias, T* __restrict__ out, int64_t rows,
-                                                  int D, int64_t L, int K, int64_t chunks) {
+                                                  int D, int64_t L, int K_, int64_t chunks) {
+  const int K = KM == 4 ? 4 : K_;
+  constexpr int PRE = (KM - 1 + 3) / 4 * 4;  // halo steps before t0, whole vectors
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= rows * chunks) return;
   const int64_t row = gid / chunks;
   const int64_t t0 = (gid - row * chunks) * kConvSteps;
   const int d = (int)(row % D);
   const T* xr = x + row * L;
-  float wk[kConvMaxK];
+  float wk[KM];
 #pragma unroll
-  for (int k = 0; k < kConvMaxK; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
+  for (int k = 0; k < KM; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
   const float b0 = bias ? bias[d] : 0.0f;
-  // window x[t0-(K-1) .. t0+3]
-  float xv[kConvMaxK - 1 + kConvSteps];
+  // window x[t0-PRE .. t0+3] (xv[i] = x[t0-PRE+i])
+  float xv[PRE + 4];
 #pragma unroll
-  for (int i = 0; i < kConvMaxK - 1 + kConvSteps; ++i) {
-    const int64_t t = t0 - (K - 1) + i;
-    xv[i] = (i < K - 1 + kConvSteps && t >= 0 && t < L) ? to_f(xr[t]) : 0.0f;
-  }
-  T* orow = out + row * L;
+  for (int v = 0; v < PRE / 4 + 1; ++v) load4<T, VEC>(xr, t0 - PRE + 4 * v, L, xv + 4 * v);
+  float o[kConvSteps];
 #pragma unroll
   for (int s = 0; s < kConvSteps; ++s) {
-    if (t0 + s >= L) break;
+    // step t0+s reads x[t0+s-(K-1)+k] = xv[PRE+s-(K-1)+k]
     float pre = b0;
 #pragma unroll
-    for (int k = 0; k < kConvMaxK; ++k)
-      if (k < K) pre = fmaf(wk[k], xv[s + k], pre);
-    const float v = SILU ? pre / (1.0f + __expf(-pre)) : pre;
-    orow[t0 + s] = from_f<T>(v);
+    for (int k = 0; k < KM; ++k)
+      if (k < K) pre = fmaf(wk[k], xv[PRE + s - (K - 1) + k], pre);
+    o[s] = SILU ? pre / (1.0f + __expf(-pre)) : pre;
   }
+  store4<T, VEC>(out + row * L, t0, L, o);
 }
 
-template <typename T, bool SILU>
+// Backward of a group of batch rows of channel d: workgroup (d, p) takes the
+// rows b = p, p + P, ... (P = gridDim.y); with P > 1 its dw / dbias partials
+// go to part[(p * D + d) * (K + 1) ...] for k_conv_bwd_reduce.
+template <typename T, bool SILU, bool VEC, int KM>
 __global__ __launch_bounds__(256) void k_conv_bwd(const T* __restrict__ x, const float* __restrict__ w,
                                                   const float* __restrict__ bias, const T* __restrict__ dout,
                                                   T* __restrict__ dx, float* __restrict__ dw,
-                                                  float* __restrict__ dbias, int B, int D, int64_t L, int K) {
+                                                  float* __restrict__ dbias, float* __restrict__ part, int B, int D,
+                                                  int64_t L, int K_) {
+  const int K = KM == 4 ? 4 : K_;  // KM = 4: width exactly 4
+  constexpr int PRE = (KM - 1 + 3) / 4 * 4;       // halo steps before t0, whole vectors
+  constexpr int NG = kConvSteps + KM - 1;          // g at t0 .. t0+NG-1
+  constexpr int NGV = (NG + 3) / 4 * 4;            // ... in whole vectors
+  constexpr int NX = PRE + NGV;                    // x at t0-PRE .. t0+NGV-1
   __shared__ float s_red[kConvMaxK + 1][256 / kWave];
-  const int d = blockIdx.x;
-  float wk[kConvMaxK];
+  const int d = blockIdx.x, p = blockIdx.y, P = gridDim.y;
+  float wk[KM];
 #pragma unroll
-  for (int k = 0; k < kConvMaxK; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
+  for (int k = 0; k < KM; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
   const float b0 = bias ? bias[d] : 0.0f;
   float aw[kConvMaxK], ab = 0.0f;  // this thread's dw / dbias partials
 #pragma unroll
   for (int k = 0; k < kConvMaxK; ++k) aw[k] = 0.0f;
-  // g at steps t0 .. t0+3+(K-1) needs x at t0-(K-1) .. t0+3+(K-1)
-  constexpr int NG = kConvSteps + kConvMaxK - 1;
-  constexpr int NX = NG + kConvMaxK - 1;
-  for (int b = 0; b < B; ++b) {
+  for (int b = p; b < B; b += P) {
     const int64_t row = (int64_t)b * D + d;
     const T* xr = x + row * L;
     const T* gr = dout + row * L;
     T* dxr = dx + row * L;
     for (int64_t t0 = (int64_t)threadIdx.x * kConvSteps; t0 < L; t0 += (int64_t)blockDim.x * kConvSteps) {
-      float xv[NX];
+      float xv[NX], go[NGV];  // xv[i] = x[t0-PRE+i], go[i] = dout[t0+i]
 #pragma unroll
-      for (int i = 0; i < NX; ++i) {
-        const int64_t t = t0 - (K - 1) + i;
-        xv[i] = (i < NG + K - 1 && t >= 0 && t < L) ? to_f(xr[t]) : 0.0f;
-      }
+      for (int v = 0; v < NX / 4; ++v) load4<T, VEC>(xr, t0 - PRE + 4 * v, L, xv + 4 * v);
+#pragma unroll
+      for (int v = 0; v < NGV / 4; ++v) load4<T, VEC>(gr, t0 + 4 * v, L, go + 4 * v);
+      // g at steps t0+i (zero past L: go is zero there)
       float g[NG];
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
-        const int64_t t = t0 + i;
-        float v = 0.0f;
-        if (i < kConvSteps + K - 1 && t < L) {
-          float pre = b0;
+        float pre = b0;
 #pragma unroll
-          for (int k = 0; k < kConvMaxK; ++k)
-            if (k < K) pre = fmaf(wk[k], xv[i + k], pre);
-          const float go = to_f(gr[t]);
-          if (SILU) {
-            const float sg = 1.0f / (1.0f + __expf(-pre));
-            v = go * sg * (1.0f + pre * (1.0f - sg));
-          } else {
-            v = go;
-          }
+        for (int k = 0; k < KM; ++k)
+          if (k < K) pre = fmaf(wk[k], xv[PRE + i - (K - 1) + k], pre);
+        if (SILU) {
+          const float sg = 1.0f / (1.0f + __expf(-pre));
+          g[i] = go[i] * sg * (1.0f + pre * (1.0f - sg));
+        } else {
+          g[i] = go[i];
         }
-        g[i] = v;
       }
+      float o[kConvSteps];
 #pragma unroll
       for (int s = 0; s < kConvSteps; ++s) {
-        if (t0 + s >= L) break;
         float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kConvMaxK; ++k)
+        for (int k = 0; k < KM; ++k)
           if (k < K) acc = fmaf(wk[k], g[s + (K - 1) - k], acc);
-        dxr[t0 + s] = from_f<T>(acc);
-        // dw[k] += g[t] x[t-(K-1)+k] over this thread's own steps
+        o[s] = acc;
+        // dw[k] += g[t] x[t-(K-1)+k] over this thread's own steps (g is 0 past L)
 #pragma unroll
-        for (int k = 0; k < kConvMaxK; ++k)
-          if (k < K) aw[k] = fmaf(g[s], xv[s + k], aw[k]);
+        for (int k = 0; k < KM; ++k)
+          if (k < K) aw[k] = fmaf(g[s], xv[PRE + s - (K - 1) + k], aw[k]);
         ab += g[s];
       }
+      store4<T, VEC>(dxr, t0, L, o);
     }
   }
-  // fixed-order reduction: waves by DPP-free shuffles, then the 4 wave sums in order
+  // fixed-order reduction: butterfly within each wave, then the waves in order
   const int wave = threadIdx.x / kWave, lane = lane_id();
 #pragma unroll
   for (int k = 0; k <= kConvMaxK; ++k) {
@@ -138,9 +184,31 @@ __global__ __launch_bounds__(256) void k_conv_bwd(const T* __restrict__ x, const
     const int k = threadIdx.x;
     float v = 0.0f;
     for (int q = 0; q < (int)(blockDim.x / kWave); ++q) v += s_red[k][q];
-    if (k < K) dw[(int64_t)d * K + k] = v;
-    else if (k == kConvMaxK && dbias) dbias[d] = v;
+    const int slot = k < kConvMaxK ? k : K;  // dbias after the K weights
+    if (k < K || k == kConvMaxK) {
+      if (P > 1) part[((int64_t)p * D + d) * (K + 1) + slot] = v;
+      else if (k < K) dw[(int64_t)d * K + k] = v;
+      else if (dbias) dbias[d] = v;
+    }
   }
+}
+
+// dw / dbias from the P batch groups' partials, summed in group order.
+__global__ __launch_bounds__(256) void k_conv_bwd_reduce(const float* __restrict__ part, int P, int D, int K,
+                                                         float* __restrict__ dw, float* __restrict__ dbias) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)D * (K + 1)) return;
+  float v = 0.0f;
+  for (int p = 0; p < P; ++p) v += part[(int64_t)p * D * (K + 1) + i];
+  const int d = (int)(i / (K + 1)), k = (int)(i % (K + 1));
+  if (k < K) dw[(int64_t)d * K + k] = v;
+  else if (dbias) dbias[d] = v;
+}
+
+// Batch groups of the backward: enough workgroups to fill the chip.
+inline int conv_split(int64_t B, int64_t D) {
+  const int64_t want = (8 * (int64_t)device_cus() + D - 1) / D;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({B, want, (int64_t)kConvMaxSplit}));
 }
 
 static int conv_checks(const char* fn, int dtype, int64_t B, int64_t D, int64_t L, int K) {
@@ -165,37 +233,75 @@ int bcm_causal_conv1d_fwd(const void* x, int dtype, const float* weight, const f
   const int64_t rows = B * D, chunks = (L + bcm::kConvSteps - 1) / bcm::kConvSteps;
   const int64_t n = rows * chunks;
   const dim3 grid((unsigned)((n + 255) / 256));
+  const bool vec = L % 4 == 0 && bcm::aligned16(x) && bcm::aligned16(out);
   bcm::dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (silu)
-      hipLaunchKernelGGL((bcm::k_conv_fwd<T, true>), grid, dim3(256), 0, bcm::hs(stream), static_cast<const T*>(x),
-                         weight, bias, static_cast<T*>(out), rows, (int)D, L, K, chunks);
-    else
-      hipLaunchKernelGGL((bcm::k_conv_fwd<T, false>), grid, dim3(256), 0, bcm::hs(stream), static_cast<const T*>(x),
-                         weight, bias, static_cast<T*>(out), rows, (int)D, L, K, chunks);
+    auto go = [&](auto s_, auto v_) {
+      constexpr bool S = decltype(s_)::value, V = decltype(v_)::value;
+      if (K == 4)
+        hipLaunchKernelGGL((bcm::k_conv_fwd<T, S, V, 4>), grid, dim3(256), 0, bcm::hs(stream),
+                           static_cast<const T*>(x), weight, bias, static_cast<T*>(out), rows, (int)D, L, K, chunks);
+      else
+        hipLaunchKernelGGL((bcm::k_conv_fwd<T, S, V, 8>), grid, dim3(256), 0, bcm::hs(stream),
+                           static_cast<const T*>(x), weight, bias, static_cast<T*>(out), rows, (int)D, L, K, chunks);
+    };
+    if (silu) {
+      if (vec) go(std::true_type{}, std::true_type{});
+      else go(std::true_type{}, std::false_type{});
+    } else {
+      if (vec) go(std::false_type{}, std::true_type{});
+      else go(std::false_type{}, std::false_type{});
+    }
   });
   return bcm::check_launch(fn);
 }
 
+int64_t bcm_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K) {
+  (void)L;
+  if (B < 1 || D < 1 || K < 1 || K > bcm::kConvMaxK) return 0;
+  const int P = bcm::conv_split(B, D);
+  return P > 1 ? 4 * (int64_t)P * D * (K + 1) : 0;
+}
+
 int bcm_causal_conv1d_bwd(const void* x, int dtype, const float* weight, const float* bias, const void* dout,
                           int64_t B, int64_t D, int64_t L, int K, int silu, void* dx, float* dweight, float* dbias,
-                          bcm_stream_t stream) {
+                          void* workspace, int64_t workspace_bytes, bcm_stream_t stream) {
   const char* fn = "bcm_causal_conv1d_bwd";
   int rc = bcm::conv_checks(fn, dtype, B, D, L, K);
   if (rc) return rc;
   if (!weight || !dweight) return bcm::set_error(BCM_EINVAL, "%s: null pointer", fn);
   if (B > 0 && L > 0 && (!x || !dout || !dx)) return bcm::set_error(BCM_EINVAL, "%s: null pointer", fn);
+  int P = B > 0 ? bcm::conv_split(B, D) : 1;
+  if (P > 1 && (!workspace || workspace_bytes < 4 * (int64_t)P * D * (K + 1))) P = 1;  // no room: one group
+  const bool vec = L % 4 == 0 && bcm::aligned16(x) && bcm::aligned16(dout) && bcm::aligned16(dx);
+  float* part = static_cast<float*>(workspace);
   bcm::dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (silu)
-      hipLaunchKernelGGL((bcm::k_conv_bwd<T, true>), dim3((unsigned)D), dim3(256), 0, bcm::hs(stream),
-                         static_cast<const T*>(x), weight, bias, static_cast<const T*>(dout), static_cast<T*>(dx),
-                         dweight, dbias, (int)B, (int)D, L, K);
-    else
-      hipLaunchKernelGGL((bcm::k_conv_bwd<T, false>), dim3((unsigned)D), dim3(256), 0, bcm::hs(stream),
-                         static_cast<const T*>(x), weight, bias, static_cast<const T*>(dout), static_cast<T*>(dx),
-                         dweight, dbias, (int)B, (int)D, L, K);
+    auto go = [&](auto s_, auto v_) {
+      constexpr bool S = decltype(s_)::value, V = decltype(v_)::value;
+      const dim3 grid((unsigned)D, (unsigned)P);
+      if (K == 4)
+        hipLaunchKernelGGL((bcm::k_conv_bwd<T, S, V, 4>), grid, dim3(256), 0, bcm::hs(stream),
+                           static_cast<const T*>(x), weight, bias, static_cast<const T*>(dout), static_cast<T*>(dx),
+                           dweight, dbias, part, (int)B, (int)D, L, K);
+      else
+        hipLaunchKernelGGL((bcm::k_conv_bwd<T, S, V, 8>), grid, dim3(256), 0, bcm::hs(stream),
+                           static_cast<const T*>(x), weight, bias, static_cast<const T*>(dout), static_cast<T*>(dx),
+                           dweight, dbias, part, (int)B, (int)D, L, K);
+    };
+    if (silu) {
+      if (vec) go(std::true_type{}, std::true_type{});
+      else go(std::true_type{}, std::false_type{});
+    } else {
+      if (vec) go(std::false_type{}, std::true_type{});
+      else go(std::false_type{}, std::false_type{});
+    }
   });
+  rc = bcm::check_launch(fn);
+  if (rc || P == 1) return rc;
+  const int64_t n = D * (K + 1);
+  hipLaunchKernelGGL(bcm::k_conv_bwd_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, bcm::hs(stream), part,
+                     P, (int)D, K, dweight, dbias);
   return bcm::check_launch(fn);
 }
 

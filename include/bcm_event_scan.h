@@ -276,10 +276,14 @@ int bcm_scan_var_bwd(const bcm_scan_args* args, const bcm_scan_bc* bc, void* wor
 int bcm_causal_conv1d_fwd(const void* x, int dtype, const float* weight, const float* bias, int64_t B,
                           int64_t D, int64_t L, int K, int silu, void* out, bcm_stream_t stream);
 /* Backward: dx [B, D, L] (dtype), dweight [D, K] and dbias [D] (fp32, fully
- * written; dbias may be NULL), the SiLU derivative recomputed from x. */
+ * written; dbias may be NULL), the SiLU derivative recomputed from x. With a
+ * workspace of bcm_causal_conv1d_bwd_workspace_bytes bytes the batch rows
+ * of a channel are split over several workgroups (partials summed in a
+ * fixed order); with NULL one workgroup per channel takes all of them. */
+int64_t bcm_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K);
 int bcm_causal_conv1d_bwd(const void* x, int dtype, const float* weight, const float* bias, const void* dout,
                           int64_t B, int64_t D, int64_t L, int K, int silu, void* dx, float* dweight,
-                          float* dbias, bcm_stream_t stream);
+                          float* dbias, void* workspace, int64_t workspace_bytes, bcm_stream_t stream);
 
 /* ---- (3) zero-order-hold restore ---------------------------------------- */
 /* Event index of sorted per-channel time steps (the restore kernels' input
