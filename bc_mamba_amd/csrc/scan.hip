@@ -407,9 +407,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
   float* sWBC = sWC + N;
   float* sWBCA = sWBC + N;
   float* sA = sWBCA + N;
-  // per lane, stride R+1 (conflict-free): the states g of the current state
-  // s (the group's staging tile outside the state loop), and the items' gap
-  // k-1 (0 for padding)
+  // per lane, stride R+1 (conflict-free): the group's staging tile (u, dout
+  // and outputs in transposed order), and the items' gap k-1 (0 for padding)
   float* tile = sA + N + wave * (kWave * RS) + grp * (G * RS);
   float* gg = tile + j * RS;
   float* tilek = tile + nw * kWave * RS;  // the k tile; then k-1 per lane
@@ -564,7 +563,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           acc1[r] = 0.0f;
           acc2[r] = 0.0f;
         }
-        wave_sync();  // the tile becomes the states g of the state loop
+        wave_sync();  // the staged dout is read; the tile is free until the per-item pass
       }
       // Σ Δ over each half chain's items, and over the items that follow
       // them (the next lane's first; nothing past the chunk: its carry
@@ -588,7 +587,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           // Each lane's R items run as two independent half chains (items
           // 0..HR-1 and HR..R-1), interleaved for instruction-level
           // parallelism and joined with the scan operator.
-          // forward: local folds, group scan, exact states (kept in LDS)
+          // forward: local folds, group scan, exact states (in registers)
           float Pa = 1.0f, Ha = 0.0f, Pb = 1.0f, Hb = 0.0f;
 #pragma unroll
           for (int i = 0; i < HR; ++i) {
@@ -614,14 +613,15 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           float P = Pa * Pb, H = fmaf(Pb, Ha, Hb);
           Ops::scan_up(P, H);
           const float gin = Ops::prev(fmaf(P, g0, H), g0);
+          float gs[R];  // the exact states of this state's items (registers only)
           {
             float ga = gin, gb = fmaf(Pa, gin, Ha);
 #pragma unroll
             for (int i = 0; i < HR; ++i) {
               ga = fmaf(av[i], ga, du2[i]);
               gb = fmaf(av[i + HR], gb, du2[i + HR]);
-              gg[i] = ga;
-              gg[i + HR] = gb;
+              gs[i] = ga;
+              gs[i + HR] = gb;
             }
           }
           // reverse: e_i = dout_i·u_i + a_{i+1}·e_{i+1}   (dx = W_C·e)
@@ -656,9 +656,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
             const int ra = HR - 1 - i, rb = R - 1 - i;
             const float ala = av[ra + 1];
             const float alb = (rb == R - 1) ? anext : av[rb + 1];
-            const float gra = gg[ra], grb = gg[rb];
-            const float gpa = ra > 0 ? gg[ra - 1] : gin;
-            const float gpb = gg[rb - 1];
+            const float gra = gs[ra], grb = gs[rb];
+            const float gpa = ra > 0 ? gs[ra - 1] : gin;
+            const float gpb = gs[rb - 1];
             ea = fmaf(ala, ea, doutu[ra]);
             eb = fmaf(alb, eb, doutu[rb]);
             acc1[ra] = fmaf(ea, wbc, acc1[ra]);       // Σ_s dx·W_B
