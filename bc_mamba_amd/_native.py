@@ -31,7 +31,8 @@ class ScanArgs(ctypes.Structure):
         ("out", c_p), ("out_z", c_p), ("x", c_p),
         ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
-        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("split_ws", c_p),
+        ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("chunk_g_bytes", c_i64),
+        ("split_ws", c_p), ("split_ws_bytes", c_i64),
     ]
 
 

@@ -826,7 +826,8 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
     *query = Plan{nw, lds, S};
     return BCM_OK;
   }
-  if (BWD && !a.split_ws) S = 1;  // no workspace for the partials: one workgroup per model channel
+  // no (or too small a) workspace for the partials: one workgroup per model channel
+  if (BWD && (!a.split_ws || a.split_ws_bytes < 4 * (int64_t)S * a.dim * (3 * a.dstate + 3))) S = 1;
   const dim3 grid((unsigned)((int64_t)a.dim * S));
   if (BWD) {
     hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a);
@@ -923,6 +924,14 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
   if (!a.cu_seqlens || !a.dt_idle || !a.dt_active || !a.A || !a.W_B || !a.W_C)
     return set_error(BCM_EINVAL, "%s: null input pointer", fn);
   if (a.n_events > 0 && (!a.u || !a.k)) return set_error(BCM_EINVAL, "%s: null u/k pointer", fn);
+  if (a.chunk_g) {
+    int pass_len, n_pass, needs_g;
+    chunking(a, &pass_len, &n_pass, &needs_g);
+    const int64_t need = 4ll * a.n_channels * n_pass * a.dstate;
+    if (a.chunk_g_bytes < need)
+      return set_error(BCM_EINVAL, "%s: chunk_g needs %lld bytes (n_channels x %d passes x dstate floats)", fn,
+                       (long long)need, n_pass);
+  }
   const bool z = a.z != nullptr;
   if (!BWD) {
     if (!a.x || (a.n_events > 0 && !a.out)) return set_error(BCM_EINVAL, "%s: null output pointer", fn);

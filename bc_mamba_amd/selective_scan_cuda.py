@@ -201,7 +201,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.out_z = out_z.data_ptr() if out_z is not None else None
         if mode == "depthwise":
             if _chunk_g is not None:
-                a.chunk_g = _chunk_g.data_ptr()
+                a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
         else:
             bc = _bc(mode, B, C, int(u_flat.size(0)), tile_offsets, tile_chunk_size)
@@ -281,13 +281,14 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 scratch_out = torch.empty_like(u_flat)
                 f.out, f.x = scratch_out.data_ptr(), torch.empty_like(x).data_ptr()
                 f.out_z = torch.empty_like(u_flat).data_ptr() if has_z else None
-                f.chunk_g = _chunk_g.data_ptr()
+                f.chunk_g, f.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
                 _nat.call("bcm_scan_fwd", f, s)
             if _chunk_g is not None:
-                a.chunk_g = _chunk_g.data_ptr()
+                a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
             split_bytes = int(_nat.lib().bcm_scan_bwd_workspace_bytes(a))
             split_ws = torch.empty(split_bytes // 4, dtype=torch.float32, device=dev) if split_bytes else None
             a.split_ws = split_ws.data_ptr() if split_ws is not None else None
+            a.split_ws_bytes = split_bytes
             _nat.call("bcm_scan_bwd", a, s)
             if pw_B is not None:  # dB, dC hold dW_eff here
                 dpw_B, dpw_C = dB @ B.t(), dC @ C.t()

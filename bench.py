@@ -151,10 +151,12 @@ class Path:
             _, n_pass, needs = nat.scan_chunking(a)
             self.chunk_g = t.empty((self.NC, n_pass, w.N), dtype=t.float32, device=self.u.device) if needs else None
             a.chunk_g = self.chunk_g.data_ptr() if needs else None
+            a.chunk_g_bytes = self.chunk_g.numel() * 4 if needs else 0
             # parameter-gradient partials when model channels are split over workgroups
             nb = int(nat.lib().bcm_scan_bwd_workspace_bytes(a))
             self.split_ws = t.empty(max(nb, 4) // 4, dtype=t.float32, device=self.u.device) if nb else None
             a.split_ws = self.split_ws.data_ptr() if nb else None
+            a.split_ws_bytes = nb
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense),

@@ -203,11 +203,13 @@ typedef struct bcm_scan_args {
    * than 2048 events (n_pass > 1 and pass_len < 2048), else it re-seeds
    * from x_saved as the reference does. */
   float* chunk_g;
+  int64_t chunk_g_bytes;       /* size of chunk_g (checked: too small is an error) */
   /* backward workspace of bcm_scan_bwd_workspace_bytes(args) bytes, or
    * NULL: with it, model channels with many channels each are split over
    * several workgroups whose parameter-gradient partials are summed in a
    * fixed order (same results either way up to that order). */
   float* split_ws;
+  int64_t split_ws_bytes;      /* size of split_ws (too small: no split) */
 } bcm_scan_args;
 
 /* Events per pass of a channel (pass_len) and passes of the longest channel

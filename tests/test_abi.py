@@ -47,8 +47,8 @@ def test_library_exports_every_header_symbol(lib):
 
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
-    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 26 pointers
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 26 * 8
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 26 pointers + 2 int64 sizes
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 26 * 8 + 2 * 8
 
 
 def test_scan_bc_layout_matches_header():
@@ -96,3 +96,16 @@ def test_scan_var_arguments_are_rejected_before_launch(lib):
     assert lib.bcm_scan_var_workspace_bytes(1000, 16) == 64000
     assert lib.bcm_scan_var_bwd(a, None, None, 0, None) == 1
     assert lib.bcm_last_error().decode().startswith("bcm_scan_var_bwd")
+
+
+def test_scan_chunk_states_size_is_checked(lib):
+    """A chunk_g smaller than n_channels x n_pass x dstate floats is refused
+    before any launch (the kernels would otherwise index past it)."""
+    a = nat.ScanArgs()
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 3000, 8, 4, 16, 1100, 1, 0
+    a.cu_seqlens = a.dt_idle = a.dt_active = a.A = a.W_B = a.W_C = a.u = a.k = 16
+    a.out = a.x = 16
+    pass_len, n_pass, needs = nat.scan_chunking(a)
+    assert needs and n_pass > 1
+    a.chunk_g, a.chunk_g_bytes = 16, 4 * 8 * n_pass * 16 - 4
+    assert lib.bcm_scan_fwd(a, None) == 1 and "chunk_g needs" in lib.bcm_last_error().decode()
