@@ -36,6 +36,12 @@ class ScanArgs(ctypes.Structure):
     ]
 
 
+class ScanRows(ctypes.Structure):
+    """Mirror of bcm_scan_rows (field order and types must match the header)."""
+
+    _fields_ = [("bitmask", c_p), ("mask_row_div", c_i64), ("tile_start", c_p), ("seqlen", c_i64), ("dx", c_p)]
+
+
 class ScanBC(ctypes.Structure):
     """Mirror of bcm_scan_bc (field order and types must match the header)."""
 
@@ -70,6 +76,7 @@ SIGNATURES = {
     "bcm_gather_bwd_rows": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_p, c_p]),
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
+    "bcm_scan_bwd_rows": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanRows), c_p]),
     "bcm_scan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(ScanArgs)]),
     "bcm_scan_chunking": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(c_i32), ctypes.POINTER(c_i32),
                                   ctypes.POINTER(c_i32)]),

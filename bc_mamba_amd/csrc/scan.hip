@@ -375,8 +375,18 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
   }
 }
 
-template <int G, int R, typename T, bool HAS_Z, bool TBL>
-__global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a) {
+// Dense gradient rows of the fused gather backward (bcm_scan_bwd_rows): the
+// extraction's event index of every channel row and the [NC, L] output.
+struct ScanRows {
+  const uint32_t* bitmask;  // channel ch reads mask row ch / mrd (words W)
+  int64_t mrd, W;
+  const int32_t* ts;        // [NC, nT + 1] absolute index of each tile's first event
+  int64_t nT, L;
+  void* dx;                 // [NC, L] of T
+};
+
+template <int G, int R, typename T, bool HAS_Z, bool TBL, bool DXR>
+__global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int RS = R + 1;
@@ -739,7 +749,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
 #pragma unroll
         for (int q = 0; q < R; ++q) {
           const int idx = q * G + jo;
-          buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, tp.at(tile, q));
+          const float v = tp.at(tile, q);
+          buf_store<T>(rdu, idx < cnt ? (eb + idx) * SZ : kBufOOB, v);
+          if constexpr (DXR) tilek[q * G + j] = v;  // du in event order for the dense row
         }
       }
       if (c > 0) {  // the previous chunk's loads, now that the tiles are free
@@ -756,6 +768,71 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       cacc[3 * N] += ddti_l;
       cacc[3 * N + 1] += ddta_l;
       cacc[3 * N + 2] += dD_l;
+    }
+    if constexpr (DXR) {
+      // dense gradient row of the channel (one pass: all of its du are in
+      // the group's k tile in event order). Lane j writes steps 4j..4j+3 of
+      // every 64-step tile (one tile per 16-lane store), taking its events
+      // from the tile's mask and the tile table; 0 between events
+      static_assert(4 * G == kTile, "one tile per group store");
+      wave_sync();
+      if (act) {
+        // row and lane constants formed here (opaque: not hoisted into
+        // registers that would stay live across the state loop)
+        const int64_t row = (int64_t)d + (int64_t)(b0 + opaque(slot)) * dim;
+        const uint32_t* mrow = rw.bitmask + (row / rw.mrd) * rw.W;
+        const int32_t* tsr = rw.ts + row * (rw.nT + 1);
+        T* dr = static_cast<T*>(rw.dx) + row * rw.L;
+        const int L = (int)rw.L;
+        const int off = 4 * opaque(j);  // the lane's first step in a tile
+        const uint32_t lo_keep = off >= 32 ? 0xFFFFFFFFu : (1u << off) - 1u;
+        const uint32_t hi_keep = off > 32 ? (1u << (off - 32)) - 1u : 0u;
+        const uint32_t sh = (uint32_t)off & 31u;
+        const int elo = -e0, ehi = C;  // local event index = table entry - e0, clamped to the tile region
+        // one tile: 4 steps, each value the next event's du masked by the
+        // step's bit (sign-extended 0 / -1), the LDS address advancing by
+        // one slot per set bit; the clamp keeps every read inside the
+        // group's region of C + G slots
+        auto seg = [&](uint64_t m, int32_t tv, int t0) {
+          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+          int e = tv + elo + (int)(__builtin_popcount(mlo & lo_keep) + __builtin_popcount(mhi & hi_keep));
+          e = min(max(e, 0), ehi);
+          const uint32_t w = off >= 32 ? mhi : mlo;
+          uint32_t o[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int32_t mk = __builtin_amdgcn_sbfe((int32_t)w, sh + (uint32_t)k, 1u);
+            o[k] = __float_as_uint(tilek[e]) & (uint32_t)mk;
+            e -= mk;
+          }
+          if constexpr (sizeof(T) == 4) {
+            st_stream(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(dr + t0));
+          } else {
+            T h[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) h[k] = from_f<T>(__uint_as_float(o[k]));
+            st_stream(*reinterpret_cast<u32x2*>(h), reinterpret_cast<u32x2*>(dr + t0));
+          }
+        };
+        constexpr int BAT = 8;
+        const int nfull = L / kTile;  // tiles whose 64 steps are all < L
+        int q0 = 0;
+        for (; q0 + BAT <= nfull; q0 += BAT) {
+          uint64_t m[BAT];
+          int32_t tv[BAT];
+#pragma unroll
+          for (int i = 0; i < BAT; ++i) {  // masks and table entries in flight together
+            m[i] = tile_mask(mrow, q0 + i);
+            tv[i] = tsr[q0 + i];
+          }
+#pragma unroll
+          for (int i = 0; i < BAT; ++i) seg(m[i], tv[i], (q0 + i) * kTile + off);
+        }
+        for (; q0 < nfull; ++q0) seg(tile_mask(mrow, q0), tsr[q0], q0 * kTile + off);
+        // a last partial tile (L % 64 != 0; L % 4 == 0, so a lane's 4 steps
+        // are all in range or all past the end)
+        if (nfull * kTile < L && nfull * kTile + off < L) seg(tile_mask(mrow, nfull), tsr[nfull], nfull * kTile + off);
+      }
     }
     if (b0 + b_step < n_per_d) {  // the next channel of this lane group
       channel(b + b_step, e0, n);
@@ -796,15 +873,15 @@ struct Plan {
   int S;       // workgroups per model channel
 };
 
-template <int G, int R, typename T, bool Z, bool BWD, bool TBL>
-static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* query) {
+template <int G, int R, typename T, bool Z, bool BWD, bool TBL, bool DXR>
+static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* query, const ScanRows* rw) {
   constexpr int CPW = kWave / G;
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
   int nw = (per_d + CPW - 1) / CPW;
   nw = nw < 1 ? 1 : (nw > kScanThreads / kWave ? kScanThreads / kWave : nw);
   // the per-workgroup limit covers static and dynamic LDS together
   hipFuncAttributes fa{};
-  const void* kfn = BWD ? reinterpret_cast<const void*>(&k_scan_bwd<G, R, T, Z, TBL>)
+  const void* kfn = BWD ? reinterpret_cast<const void*>(&k_scan_bwd<G, R, T, Z, TBL, DXR>)
                         : reinterpret_cast<const void*>(&k_scan_fwd<G, R, T, Z, TBL>);
   if (hipFuncGetAttributes(&fa, kfn) != hipSuccess) return set_error(BCM_EHIP, "%s: hipFuncGetAttributes failed", fn);
   const int64_t cap = max_lds_bytes() - (int64_t)fa.sharedSizeBytes;
@@ -830,7 +907,8 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
   if (BWD && (!a.split_ws || a.split_ws_bytes < 4 * (int64_t)S * a.dim * (3 * a.dstate + 3))) S = 1;
   const dim3 grid((unsigned)((int64_t)a.dim * S));
   if (BWD) {
-    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a);
+    hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL, DXR>), grid, dim3(nw * kWave), (size_t)lds, s, a,
+                       rw ? *rw : ScanRows{});
     int rc = check_launch(fn);
     if (rc || S == 1) return rc;
     const int64_t tot = (int64_t)a.dim * (3 * a.dstate + 3);
@@ -889,26 +967,50 @@ static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* ne
   *needs_chunk_g = (*n_pass > 1 && C < kXChunk) ? 1 : 0;
 }
 
+// The fused dense-row backward exists for the single-pass 16-lane shapes
+// without z (the model's event path); rows_fusable() says when it applies.
+template <int G, int R, typename T, bool Z, bool BWD, bool TBL>
+static int launch_any(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q, const ScanRows* rw) {
+  if constexpr (BWD && !Z && G == 16) {
+    if (rw) return launch<G, R, T, Z, BWD, TBL, true>(a, s, fn, q, rw);
+  }
+  if (rw) return set_error(BCM_EINVAL, "%s: no fused dense-row backward for this shape", fn);
+  return launch<G, R, T, Z, BWD, TBL, false>(a, s, fn, q, nullptr);
+}
+
 template <typename T, bool Z, bool BWD>
-static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q = nullptr) {
+static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q = nullptr,
+                          const ScanRows* rw = nullptr) {
   switch (pick_shape(a)) {
-    case S16x4: return launch<16, 4, T, Z, BWD, true>(a, s, fn, q);
-    case S16x8: return launch<16, 8, T, Z, BWD, true>(a, s, fn, q);
-    case S16x16: return launch<16, 16, T, Z, BWD, true>(a, s, fn, q);
-    case S16x24: return launch<16, 24, T, Z, BWD, true>(a, s, fn, q);
-    case S32x16: return launch<32, 16, T, Z, BWD, true>(a, s, fn, q);
-    case S64x4: return launch<64, 4, T, Z, BWD, false>(a, s, fn, q);
-    case S64x8: return launch<64, 8, T, Z, BWD, false>(a, s, fn, q);
+    case S16x4: return launch_any<16, 4, T, Z, BWD, true>(a, s, fn, q, rw);
+    case S16x8: return launch_any<16, 8, T, Z, BWD, true>(a, s, fn, q, rw);
+    case S16x16: return launch_any<16, 16, T, Z, BWD, true>(a, s, fn, q, rw);
+    case S16x24: return launch_any<16, 24, T, Z, BWD, true>(a, s, fn, q, rw);
+    case S32x16: return launch_any<32, 16, T, Z, BWD, true>(a, s, fn, q, rw);
+    case S64x4: return launch_any<64, 4, T, Z, BWD, false>(a, s, fn, q, rw);
+    case S64x8: return launch_any<64, 8, T, Z, BWD, false>(a, s, fn, q, rw);
     default: break;
   }
   const bool tbl = a.dstate <= kTabMaxN;
   if (pick_shape(a) == S64x16)
-    return tbl ? launch<64, 16, T, Z, BWD, true>(a, s, fn, q) : launch<64, 16, T, Z, BWD, false>(a, s, fn, q);
-  return tbl ? launch<64, 32, T, Z, BWD, true>(a, s, fn, q) : launch<64, 32, T, Z, BWD, false>(a, s, fn, q);
+    return tbl ? launch_any<64, 16, T, Z, BWD, true>(a, s, fn, q, rw)
+               : launch_any<64, 16, T, Z, BWD, false>(a, s, fn, q, rw);
+  return tbl ? launch_any<64, 32, T, Z, BWD, true>(a, s, fn, q, rw)
+             : launch_any<64, 32, T, Z, BWD, false>(a, s, fn, q, rw);
+}
+
+// True when bcm_scan_bwd_rows can write the dense rows from the scan kernel:
+// a 16-lane shape whose one pass holds every channel, no z, 4-step aligned
+// rows.
+static bool rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
+  const ShapeId id = pick_shape(a);
+  if (kShapeG[id] != 16 || a.max_seqlen > kShapeG[id] * kShapeR[id] || a.z) return false;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(r.dx);
+  return r.seqlen % 4 == 0 && p % (4 * dtype_size(a.dtype)) == 0;
 }
 
 template <bool BWD>
-static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* fn) {
+static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* fn, const ScanRows* rw = nullptr) {
   if (!ap) return set_error(BCM_EINVAL, "%s: null args", fn);
   const bcm_scan_args& a = *ap;
   if (!dtype_ok(a.dtype)) return set_error(BCM_EINVAL, "%s: u_flat must be fp16/bf16/fp32", fn);
@@ -953,7 +1055,7 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
   int rc = BCM_OK;
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
-    rc = z ? dispatch_shape<T, true, BWD>(a, s, fn) : dispatch_shape<T, false, BWD>(a, s, fn);
+    rc = z ? dispatch_shape<T, true, BWD>(a, s, fn, nullptr, rw) : dispatch_shape<T, false, BWD>(a, s, fn, nullptr, rw);
   });
   return rc;
 }
@@ -968,6 +1070,28 @@ int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream) {
 
 int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream) {
   return bcm::scan_entry<true>(args, stream, "bcm_scan_bwd");
+}
+
+int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_stream_t stream) {
+  const char* fn = "bcm_scan_bwd_rows";
+  if (!args || !rows) return bcm::set_error(BCM_EINVAL, "%s: null argument", fn);
+  const bcm_scan_rows& r = *rows;
+  if (r.seqlen < 0 || r.mask_row_div < 1) return bcm::set_error(BCM_EINVAL, "%s: invalid seqlen / mask_row_div", fn);
+  if (args->n_channels >= 1 && r.seqlen > 0) {
+    if (!r.bitmask || !r.tile_start || !r.dx) return bcm::set_error(BCM_EINVAL, "%s: null index / dx pointer", fn);
+    if ((reinterpret_cast<uintptr_t>(r.bitmask) & 7) != 0)
+      return bcm::set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  }
+  if (args->n_channels < 1 || r.seqlen == 0 || !bcm::dtype_ok(args->dtype) || !bcm::rows_fusable(*args, r)) {
+    // two steps: the scan backward, then the rows from du
+    int rc = bcm::scan_entry<true>(args, stream, fn);
+    if (rc) return rc;
+    return bcm_gather_bwd_rows(args->du, args->dtype, r.bitmask, r.mask_row_div, r.tile_start, args->n_channels,
+                               r.seqlen, r.dx, stream);
+  }
+  const bcm::ScanRows rw{r.bitmask, r.mask_row_div, bcm::bitmask_words(r.seqlen), r.tile_start,
+                         bcm::tile_count(r.seqlen), r.seqlen, r.dx};
+  return bcm::scan_entry<true>(args, stream, fn, &rw);
 }
 
 int64_t bcm_scan_bwd_workspace_bytes(const bcm_scan_args* args) {

@@ -8,9 +8,10 @@ depthwise causal conv + SiLU (PyTorch-ROCm), then the event path on the HIP
 kernels (extraction, gather, flat selective scan, zero-order-hold restore),
 then out_proj. With `fused_event_path=True` (default) the block calls the
 fused entry points: one extraction pass that also gathers x_conv at the
-events and builds the event index, the restore and the gather backward read
-that index instead of rebuilding it, and the per-block host syncs drop from
-two to one. Results are identical to the unfused composition.
+events and builds the event index, the restore reads that index instead of
+rebuilding it, the scan backward writes the dense x_conv gradient rows from
+the same index (no separate gather backward), and the per-block host syncs
+drop from two to one. Results are identical to the unfused composition.
 
 The decode `step` / inference cache of the reference are not part of the
 event path (the reference's own `step` reads an undefined `self.pw_B`).
@@ -26,6 +27,7 @@ try:
     from . import _native as _nat
     from . import extract_events_cuda as _ee_cuda
     from . import restore_dense_cuda_nodecay
+    from . import selective_scan_cuda
     from .causal_conv1d import causal_conv1d_fn
     from .runtime_breakdown import cuda_stage
     from .selective_scan_interface import selective_scan_flat_ch_fn
@@ -33,6 +35,7 @@ except ImportError:  # imported with this directory on sys.path
     import _native as _nat
     import extract_events_cuda as _ee_cuda
     import restore_dense_cuda_nodecay
+    import selective_scan_cuda
     from causal_conv1d import causal_conv1d_fn
     from runtime_breakdown import cuda_stage
     from selective_scan_interface import selective_scan_flat_ch_fn
@@ -114,6 +117,45 @@ class _IndexedGatherFn(torch.autograd.Function):
             _nat.call("bcm_gather_bwd_rows", _nat.ptr(g), _nat.dtype_code(g.dtype), _nat.ptr(bitmask), int(expand),
                       _nat.ptr(tile_start), B * D, L, _nat.ptr(dx), _nat.stream_of(g))
         return dx, None, None
+
+
+class _IndexedScanFn(torch.autograd.Function):
+    """The gather of x_conv at the events (already done by the fused
+    extraction) and the depthwise flat scan as one autograd node. Its
+    backward writes the dense x_conv gradient from the scan kernel
+    (bcm_scan_bwd_rows) instead of scattering du in a second pass. Same
+    results as _IndexedGatherFn followed by SelectiveScanFlatChFn."""
+
+    @staticmethod
+    def forward(ctx, x_conv, payload, event_index, k_flat, cu_seqlens, max_seqlen: int, dt_idle, dt_active, A, W_B,
+                W_C, D):
+        # payload = (x_events,): kept out of the autograd inputs on purpose
+        x_ev = payload[0]
+        dt_idle, dt_active = dt_idle.contiguous(), dt_active.contiguous()
+        A, W_B, W_C = A.contiguous(), W_B.contiguous(), W_C.contiguous()
+        chunk_g = selective_scan_cuda.chunk_states_buffer(x_ev, cu_seqlens, max_seqlen, A)
+        out, x = selective_scan_cuda.fwd_flat_ch(x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B,
+                                                 W_C, D, None, is_depthwise_bc=True, _chunk_g=chunk_g)
+        ctx.save_for_backward(x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, x,
+                              *([D] if D is not None else []))
+        ctx.chunk_g, ctx.event_index, ctx.max_seqlen = chunk_g, event_index, max_seqlen
+        ctx.shape, ctx.has_D = x_conv.shape, D is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, x = ctx.saved_tensors[:9]
+        D = ctx.saved_tensors[9] if ctx.has_D else None
+        B, Dm, L = ctx.shape
+        bitmask, tile_start, expand = ctx.event_index
+        dx = torch.empty((B * Dm, L), dtype=x_ev.dtype, device=x_ev.device)
+        with cuda_stage("sparse_scan_backward"):
+            res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A,
+                                                  W_B, W_C, dout.contiguous(), x, D, is_depthwise_bc=True,
+                                                  _chunk_g=ctx.chunk_g, _rows=(bitmask, expand, tile_start, dx))
+        _du, dA, dW_B, dW_C, ddt_idle, ddt_active = res[:6]
+        dD = res[6] if ctx.has_D else None
+        return dx.view(B, Dm, L), None, None, None, None, None, ddt_idle, ddt_active, dA, dW_B, dW_C, dD
 
 
 class _IndexedRestoreFn(torch.autograd.Function):
@@ -279,16 +321,17 @@ class Mamba(nn.Module):
                 _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_ev, event_index = \
                     _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach(),
                                                     positions=False)
-            with cuda_stage("active_gather_forward"):
-                x_conv_flat = _IndexedGatherFn.apply(x, (x_ev,), event_index)
+            with cuda_stage("sparse_scan_forward"):
+                y_flat = _IndexedScanFn.apply(x, (x_ev,), event_index, k_flat, cu_seqlens, int(max_seqlen), dt_idle,
+                                              dt_active, A, W_B, W_C, self.D)
         else:
             _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_conv_flat = self.extract_events_1d(
                 hidden_states, x, self.threshold)
-
-        with cuda_stage("sparse_scan_forward"):
-            y_flat, _ = selective_scan_flat_ch_fn(x_conv_flat, k_flat, cu_seqlens, int(max_seqlen), dt_idle,
-                                                  dt_active, A, W_B, W_C, self.D, None, tile_offsets=None,
-                                                  tile_chunk_size=0, is_depthwise_bc=True, pw_B=None, pw_C=None)
+            with cuda_stage("sparse_scan_forward"):
+                y_flat, _ = selective_scan_flat_ch_fn(x_conv_flat, k_flat, cu_seqlens, int(max_seqlen), dt_idle,
+                                                      dt_active, A, W_B, W_C, self.D, None, tile_offsets=None,
+                                                      tile_chunk_size=0, is_depthwise_bc=True, pw_B=None,
+                                                      pw_C=None)
         with cuda_stage("dense_restoration_forward"):
             if self.fused_event_path:
                 y_dense = _IndexedRestoreFn.apply(y_flat, event_index, n_ch, self.d_inner, seqlen)

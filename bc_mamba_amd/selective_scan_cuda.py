@@ -211,12 +211,16 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
-                pw_B=None, pw_C=None, _chunk_g=None):
+                pw_B=None, pw_C=None, _chunk_g=None, _rows=None):
     """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
     ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
     dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
     shape of B / C otherwise. Parameter gradients are reduced
-    deterministically inside the kernels."""
+    deterministically inside the kernels.
+    `_rows` (not in the reference signature; depthwise mode without pw_B):
+    (bitmask, mask_row_div, tile_start, dx) of the extraction's event index
+    and a contiguous [n_channels, L] tensor of u_flat's dtype, which also
+    receives the gather backward of du (du at the events, 0 elsewhere)."""
     fn = "selective_scan_bwd_flat_ch"
     _check(dout_flat.dtype == u_flat.dtype, f"{fn}: dout_flat must match u_flat dtype")
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous()
@@ -289,7 +293,17 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
             split_ws = torch.empty(split_bytes // 4, dtype=torch.float32, device=dev) if split_bytes else None
             a.split_ws = split_ws.data_ptr() if split_ws is not None else None
             a.split_ws_bytes = split_bytes
-            _nat.call("bcm_scan_bwd", a, s)
+            if _rows is None:
+                _nat.call("bcm_scan_bwd", a, s)
+            else:
+                bitmask, mrd, tile_start, dx = _rows
+                _check(pw_B is None, f"{fn}: dense rows need W_B / W_C without pw_B / pw_C")
+                _check(dx.is_contiguous() and dx.dtype == u_flat.dtype and dx.dim() == 2
+                       and dx.size(0) == n_ch, f"{fn}: dx must be a contiguous (n_channels, L) tensor of u's dtype")
+                r = _nat.ScanRows()
+                r.bitmask, r.mask_row_div, r.tile_start = bitmask.data_ptr(), int(mrd), tile_start.data_ptr()
+                r.seqlen, r.dx = int(dx.size(1)), dx.data_ptr()
+                _nat.call("bcm_scan_bwd_rows", a, r, s)
             if pw_B is not None:  # dB, dC hold dW_eff here
                 dpw_B, dpw_C = dB @ B.t(), dC @ C.t()
                 dB, dC = pw_B.t() @ dB, pw_C.t() @ dC

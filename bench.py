@@ -7,7 +7,8 @@ batch, inputs resident in HBM:
             events and the event index built in the same pass; the host
             reads E while fill runs) -> flat selective scan ->
             zero-order-hold restore
-  backward: restore backward -> selective scan backward -> gather backward
+  backward: restore backward -> selective scan backward with the gather
+            backward (du at the events, dense dx rows) in the same kernel
 All stages run in libbcm_event_scan.so on torch's current stream. Prints one
 JSON line (metric / value / roofline / cpu_baseline ...).
 
@@ -34,8 +35,8 @@ COLD_REPS = 11
 # device kernels behind each stage of Path.KERNELS (symbol substrings)
 STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
                  "scan_fwd": ["k_scan_fwd"], "restore_fwd": ["k_restore_fwd"],
-                 "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"], "scan_bwd": ["k_scan_bwd"],
-                 "gather_bwd": ["k_gather_bwd_rows"]}
+                 "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"],
+                 "scan_bwd": ["k_scan_bwd", "k_scan_param_reduce", "k_gather_bwd_rows"]}
 
 
 def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
@@ -67,7 +68,7 @@ class Path:
     the host polls it while fill runs, and the GPU never idles on the round
     trip."""
 
-    KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd", "gather_bwd"]
+    KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd"]
 
     def __init__(self, w, dev):
         import torch
@@ -97,6 +98,10 @@ class Path:
         f32 = dict(dtype=torch.float32, device=dev)
         self.grads = [torch.empty((w.D, w.N), **f32) for _ in range(3)] + [torch.empty(w.D, **f32) for _ in range(3)]
         self.args = self._scan_args()
+        self.rows = nat.ScanRows()
+        self.rows.bitmask, self.rows.mask_row_div, self.rows.tile_start = self.bitmask.data_ptr(), 1, \
+            self.tile_start.data_ptr()
+        self.rows.seqlen, self.rows.dx = L, self.dx.data_ptr()
         self.E = self.ms = -1
         self.events = {}
 
@@ -166,9 +171,9 @@ class Path:
                                              4 * self.ws.numel(), s))
         if self.dy is not self.dy32:
             self.dy[:E].copy_(self.dy32[:E])
-        mark("scan_bwd", lambda: nat.call("bcm_scan_bwd", self.args, s))
-        mark("gather_bwd", lambda: nat.call("bcm_gather_bwd_rows", P(self.du), nat.dtype_code(w.dtype),
-                                            P(self.bitmask), 1, P(self.tile_start), self.NC, L, P(self.dx), s))
+        # the scan backward writes du and the dense dx rows (the gather
+        # backward) in one kernel where the shape allows, else in two
+        mark("scan_bwd", lambda: nat.call("bcm_scan_bwd_rows", self.args, self.rows, s))
 
     def kernel_ms(self, name):
         self.t.cuda.synchronize()
@@ -342,7 +347,7 @@ def main():
     kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC,
                     "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
                     "restore_fwd": alg["fwd_restore"], "restore_bwd": alg["bwd_restore"],
-                    "scan_bwd": alg["bwd_scan"], "gather_bwd": alg["bwd_gather"]}
+                    "scan_bwd": alg["bwd_scan"] + alg["bwd_gather"]}
     dom_gbs = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
     result = {
         "metric": METRIC,

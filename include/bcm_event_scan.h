@@ -228,6 +228,24 @@ int bcm_scan_fwd(const bcm_scan_args* args, bcm_stream_t stream);
  * selective_scan_bwd_kernel.cuh:635-1169). */
 int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream);
 
+/* The model path's scan backward with the gather backward folded in
+ * (SelectiveScanFlatChFn.backward then GatherEventsFn.backward, e_model.py
+ * :188-193, extract_events_cuda.cu:717-754): everything bcm_scan_bwd
+ * writes (du included), plus dx [n_channels, seqlen] (args->dtype) = du at
+ * each channel's events and 0 elsewhere, the result of bcm_gather_bwd_rows
+ * on du. bitmask / tile_start are the extraction's event index
+ * (bcm_extract_indexed) and must describe the events of cu_seqlens. One
+ * kernel for single-pass 16-lane shapes without z and seqlen % 4 == 0
+ * (dx aligned to 4 elements); otherwise the two steps run in turn. */
+typedef struct bcm_scan_rows {
+  const uint32_t* bitmask;    /* [n_channels / mask_row_div, words], 8-byte aligned */
+  int64_t mask_row_div;       /* channel ch reads bitmask row ch / mask_row_div */
+  const int32_t* tile_start;  /* [n_channels, tiles + 1] */
+  int64_t seqlen;             /* L */
+  void* dx;                   /* [n_channels, L] */
+} bcm_scan_rows;
+int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_stream_t stream);
+
 /* B and C of the non-depthwise modes of fwd_flat_ch / bwd_flat_ch
  * (selective_scan.cpp:760-776, 840-848, 969-990, 1085-1090):
  *   BCM_BC_LEGACY  per event: B[s*b_row_stride + e]  ([dstate, E])

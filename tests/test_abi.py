@@ -57,6 +57,24 @@ def test_scan_bc_layout_matches_header():
     assert ctypes.sizeof(nat.ScanBC) == 4 * 4 + 3 * 8 + 5 * 8 + 2 * 8
 
 
+def test_scan_rows_layout_matches_header():
+    assert [f for f, _ in nat.ScanRows._fields_] == header_struct_fields("bcm_scan_rows")
+    assert ctypes.sizeof(nat.ScanRows) == 5 * 8
+
+
+def test_scan_rows_arguments_are_rejected_before_launch(lib):
+    a = nat.ScanArgs()
+    a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 4, 2, 16, 10, 1, 0
+    assert lib.bcm_scan_bwd_rows(a, None, None) == 1 and "null argument" in lib.bcm_last_error().decode()
+    r = nat.ScanRows()
+    r.seqlen, r.mask_row_div = 64, 0
+    assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "mask_row_div" in lib.bcm_last_error().decode()
+    r.mask_row_div = 1
+    assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "null index" in lib.bcm_last_error().decode()
+    r.bitmask, r.tile_start, r.dx = 20, 16, 16  # never dereferenced: rejected first
+    assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "8-byte aligned" in lib.bcm_last_error().decode()
+
+
 def test_host_helpers(lib):
     assert lib.bcm_abi_version() == 2
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64

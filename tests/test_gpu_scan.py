@@ -39,7 +39,7 @@ def _case(B, D, L, p, N, dtype, seed, with_z=False, with_D=True, empty_every=0, 
     WB = torch.randn(dim, N, generator=g) / math.sqrt(N)
     WC = torch.randn(dim, N, generator=g) / math.sqrt(N)
     Dv = torch.randn(dim, generator=g) if with_D else None
-    return dict(ch=ch, k=k, cu=cu, ms=ms, u=u, dout=dout, z=z, dt_i=dt_i, dt_a=dt_a, A=A, WB=WB, WC=WC, D=Dv)
+    return dict(ch=ch, t=t, k=k, cu=cu, ms=ms, u=u, dout=dout, z=z, dt_i=dt_i, dt_a=dt_a, A=A, WB=WB, WC=WC, D=Dv)
 
 
 def _run_and_check(c, dtype, dev):
