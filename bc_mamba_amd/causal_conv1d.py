@@ -17,7 +17,7 @@ try:
 except ImportError:  # imported with this directory on sys.path
     import _native as _nat
 
-__all__ = ["causal_conv1d_fn", "CausalConv1dFn"]
+__all__ = ["causal_conv1d_fn", "CausalConv1dFn", "conv1d_bwd_events"]
 
 
 def _check(cond, msg):
@@ -61,6 +61,32 @@ class CausalConv1dFn(torch.autograd.Function):
                       int(ctx.silu), dx.data_ptr(), dw.data_ptr(), db.data_ptr() if db is not None else None,
                       ws.data_ptr() if ws is not None else None, nbytes, _nat.stream_of(x))
         return dx, dw.to(ctx.wdtype), (db.to(ctx.wdtype) if db is not None else None), None
+
+
+def conv1d_bwd_events(x, weight, bias, silu, du, event_index):
+    """Backward of the conv evaluated at the events (extract_events_indexed
+    with conv=...) and the gather, from du [E] (the gradient of x_events):
+    (dx with x's strides, dweight [D, K] fp32, dbias [D] fp32 or None)
+    (bcm_causal_conv1d_bwd_events). No reference counterpart as one call:
+    it is GatherEventsFn.backward followed by the conv backward."""
+    B, D, L = x.shape
+    bitmask, tile_start, mrd = event_index
+    w = weight.detach().float().contiguous()
+    b = bias.detach().float().contiguous() if bias is not None else None
+    _check(du.dtype == x.dtype and du.is_contiguous(), "conv1d_bwd_events: du must be contiguous, x's dtype")
+    dx = torch.empty_strided(x.shape, x.stride(), dtype=x.dtype, device=x.device)
+    dw = torch.empty_like(w)
+    db = torch.empty(D, dtype=torch.float32, device=x.device) if bias is not None else None
+    K = int(w.size(1))
+    with torch.cuda.device(x.device):
+        nbytes = int(_nat.lib().bcm_causal_conv1d_bwd_events_workspace_bytes(B, D, K))
+        ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=x.device)
+        _nat.call("bcm_causal_conv1d_bwd_events", x.data_ptr(), _nat.dtype_code(x.dtype), x.stride(0), x.stride(1),
+                  B, D, L, w.data_ptr(), b.data_ptr() if b is not None else None, K, int(bool(silu)),
+                  du.data_ptr(), int(du.numel()), bitmask.data_ptr(), int(mrd), tile_start.data_ptr(),
+                  dx.data_ptr(), dw.data_ptr(), db.data_ptr() if db is not None else None, ws.data_ptr(), nbytes,
+                  _nat.stream_of(x))
+    return dx, dw, db
 
 
 def causal_conv1d_fn(x, weight, bias=None, seq_idx=None, initial_states=None, return_final_states=False,

@@ -205,6 +205,143 @@ __global__ __launch_bounds__(256) void k_conv_bwd_reduce(const float* __restrict
   else if (dbias) dbias[d] = v;
 }
 
+// ---------------------------------------------- backward from the events
+// The conv evaluated only at the events (x_events of the fused fill), so its
+// gradient arrives as du [E], one value per event. g = du * silu'(pre) lives
+// at the events only, and the kernel writes the dense dx row straight from
+// it: one wave per row, in windows of kCbWin steps taken from the row's end
+// backward. Pass 1 gives every step of the window its g (0 between events;
+// pre recomputed from x, the event found from the tile mask and the tile
+// table) in LDS and accumulates the lane's dw / dbias terms; pass 2 forms
+// dx[t] = sum_k w[k] g[t+(K-1)-k] from LDS, the K-1 slots past the window
+// holding the first g of the window after it. dx has x's row strides.
+constexpr int kCbWin = 1024;  // steps per window (4 per lane and 256-step segment)
+
+template <typename T, bool SILU, int KM>
+__global__ __launch_bounds__(256) void k_conv_bwd_events(
+    const T* __restrict__ x, int64_t sb, int64_t sd, int dim, int64_t L, const float* __restrict__ w,
+    const float* __restrict__ bias, int K_, const T* __restrict__ du, int64_t n_events,
+    const uint32_t* __restrict__ bitmask, int64_t W, int64_t mrd, const int32_t* __restrict__ ts, int64_t nT,
+    T* __restrict__ dx, float* __restrict__ part, int64_t rows) {
+  const int K = KM == 4 ? 4 : K_;
+  constexpr int PRE = (KM - 1 + 3) / 4 * 4;  // halo steps before t0, whole vectors
+  __shared__ float s_g[4][kCbWin + kConvMaxK];
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= rows) return;  // no workgroup barrier below
+  const int64_t b = row / dim;
+  const int d = (int)(row % dim);
+  const T* xr = x + b * sb + (int64_t)d * sd;
+  T* dr = dx + b * sb + (int64_t)d * sd;
+  const uint32_t* mrow = bitmask + (row / mrd) * W;
+  const int32_t* tsr = ts + row * (nT + 1);
+  float wk[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
+  const float b0 = bias ? bias[d] : 0.0f;
+  const __amdgpu_buffer_rsrc_t rdu = buf_rsrc(du, n_events * (int64_t)sizeof(T));
+  float* sg = s_g[wave];
+  float aw[KM], ab = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KM; ++k) aw[k] = 0.0f;
+  if (lane < KM) sg[kCbWin + lane] = 0.0f;  // g past the row's end
+  wave_sync();
+  constexpr int SEGS = kCbWin / (4 * kWave);
+  for (int64_t w0 = (L - 1) / kCbWin * kCbWin; w0 >= 0; w0 -= kCbWin) {
+#pragma unroll
+    for (int q = 0; q < SEGS; ++q) {  // pass 1: g at the lane's 4 steps
+      const int lt = 4 * kWave * q + 4 * lane;
+      const int64_t t0 = w0 + lt;
+      float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (t0 < L) {  // L % 4 == 0: all 4 steps in range
+        float xv[PRE + 4];  // xv[i] = x[t0-PRE+i]
+#pragma unroll
+        for (int v = 0; v < PRE / 4 + 1; ++v) load4<T, true>(xr, t0 - PRE + 4 * v, L, xv + 4 * v);
+        const int64_t tl = t0 / kTile;
+        const int off = (int)(t0 % kTile);
+        const uint64_t m = tile_mask(mrow, tl);
+        const uint32_t nib = (uint32_t)(m >> off) & 0xFu;
+        uint32_t e = (uint32_t)tsr[tl] + (uint32_t)__popcll(m & ((1ull << off) - 1ull));
+        float dv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // the events' du loads in flight together
+          const uint32_t bit = (nib >> k) & 1u;
+          dv[k] = buf_load<T>(rdu, bit ? e * (uint32_t)sizeof(T) : kBufOOB);
+          e += bit;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float pre = b0;
+#pragma unroll
+          for (int j = 0; j < KM; ++j)
+            if (j < K) pre = fmaf(wk[j], xv[PRE + k - (K - 1) + j], pre);
+          float gv = dv[k];
+          if (SILU) {
+            const float sgm = 1.0f / (1.0f + __expf(-pre));
+            gv = dv[k] * sgm * (1.0f + pre * (1.0f - sgm));
+          }
+          g[k] = ((nib >> k) & 1u) ? gv : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+          for (int j = 0; j < KM; ++j)
+            if (j < K) aw[j] = fmaf(g[k], xv[PRE + k - (K - 1) + j], aw[j]);
+          ab += g[k];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sg[lt + k] = g[k];
+    }
+    wave_sync();
+#pragma unroll
+    for (int q = 0; q < SEGS; ++q) {  // pass 2: dx at the lane's 4 steps
+      const int lt = 4 * kWave * q + 4 * lane;
+      const int64_t t0 = w0 + lt;
+      if (t0 < L) {
+        float gg[4 + KM - 1];  // g[t0 .. t0+3+KM-1]; slots past the window carry the next window's first g
+#pragma unroll
+        for (int i = 0; i < 4 + KM - 1; ++i) gg[i] = sg[lt + i];
+        float o[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int k = 0; k < KM; ++k)
+            if (k < K) acc = fmaf(wk[k], gg[s + (K - 1) - k], acc);
+          o[s] = acc;
+        }
+        store4<T, true>(dr, t0, L, o);
+      }
+    }
+    wave_sync();
+    const float carry = lane < KM ? sg[lane] : 0.0f;  // this window's first g, for the window before it
+    wave_sync();
+    if (lane < KM) sg[kCbWin + lane] = carry;
+    wave_sync();
+  }
+  // the row's dw / dbias terms: butterfly over the wave (fixed order)
+#pragma unroll
+  for (int k = 0; k <= KM; ++k) {
+    float v = k < KM ? aw[k] : ab;
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (lane == 0 && (k < K || k == KM)) part[row * (K + 1) + (k < KM ? k : K)] = v;
+  }
+}
+
+// dw / dbias from the rows' terms: channel d sums rows d, d + dim, ... in order.
+__global__ __launch_bounds__(256) void k_conv_bwd_events_reduce(const float* __restrict__ part, int64_t nb, int dim,
+                                                                int K, float* __restrict__ dw,
+                                                                float* __restrict__ dbias) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)dim * (K + 1)) return;
+  const int d = (int)(i / (K + 1)), k = (int)(i % (K + 1));
+  float v = 0.0f;
+  for (int64_t bb = 0; bb < nb; ++bb) v += part[(bb * dim + d) * (K + 1) + k];
+  if (k < K) dw[(int64_t)d * K + k] = v;
+  else if (dbias) dbias[d] = v;
+}
+
 // Batch groups of the backward: enough workgroups to fill the chip.
 inline int conv_split(int64_t B, int64_t D) {
   const int64_t want = (8 * (int64_t)device_cus() + D - 1) / D;
@@ -302,6 +439,71 @@ int bcm_causal_conv1d_bwd(const void* x, int dtype, const float* weight, const f
   const int64_t n = D * (K + 1);
   hipLaunchKernelGGL(bcm::k_conv_bwd_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, bcm::hs(stream), part,
                      P, (int)D, K, dweight, dbias);
+  return bcm::check_launch(fn);
+}
+
+int64_t bcm_causal_conv1d_bwd_events_workspace_bytes(int64_t B, int64_t D, int K) {
+  if (B < 1 || D < 1 || K < 1 || K > bcm::kConvMaxK) return 0;
+  return 4 * B * D * (K + 1);
+}
+
+int bcm_causal_conv1d_bwd_events(const void* x, int dtype, int64_t x_batch_stride, int64_t x_dim_stride, int64_t B,
+                                 int64_t D, int64_t L, const float* weight, const float* bias, int K, int silu,
+                                 const void* du, int64_t n_events, const uint32_t* bitmask, int64_t mask_row_div,
+                                 const int32_t* tile_start, void* dx, float* dweight, float* dbias, void* workspace,
+                                 int64_t workspace_bytes, bcm_stream_t stream) {
+  const char* fn = "bcm_causal_conv1d_bwd_events";
+  int rc = bcm::conv_checks(fn, dtype, B, D, L, K);
+  if (rc) return rc;
+  if (!weight || !dweight) return bcm::set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (B == 0 || L == 0) {  // no rows: the weight gradients are zero
+    rc = bcm_zero(dweight, 4 * D * K, stream);
+    if (!rc && dbias) rc = bcm_zero(dbias, 4 * D, stream);
+    return rc;
+  }
+  if (!x || !dx || !bitmask || !tile_start || (n_events > 0 && !du))
+    return bcm::set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_events < 0 || n_events * 4 > INT32_MAX) return bcm::set_error(BCM_EINVAL, "%s: n_events out of range", fn);
+  if (mask_row_div < 1) return bcm::set_error(BCM_EINVAL, "%s: mask_row_div must be >= 1", fn);
+  const size_t es = bcm::dtype_size(dtype);
+  const uintptr_t va = 4 * es;  // one 4-step vector
+  if (L % 4 || x_batch_stride % 4 || x_dim_stride % 4 || x_batch_stride < 0 || x_dim_stride < 0 ||
+      reinterpret_cast<uintptr_t>(x) % va || reinterpret_cast<uintptr_t>(dx) % va)
+    return bcm::set_error(BCM_EINVAL, "%s: needs L and the row strides multiples of 4 and x, dx aligned to 4 elements",
+                          fn);
+  if ((reinterpret_cast<uintptr_t>(bitmask) & 7) != 0)
+    return bcm::set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  const int64_t rows = B * D;
+  if (!workspace || workspace_bytes < 4 * rows * (K + 1))
+    return bcm::set_error(BCM_EINVAL, "%s: workspace needs %lld bytes", fn, (long long)(4 * rows * (K + 1)));
+  const int64_t W = bcm::bitmask_words(L), nT = bcm::tile_count(L);
+  float* part = static_cast<float*>(workspace);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  bcm::dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    auto go = [&](auto s_, auto km) {
+      constexpr bool S = decltype(s_)::value;
+      constexpr int KM = decltype(km)::value;
+      hipLaunchKernelGGL((bcm::k_conv_bwd_events<T, S, KM>), grid, dim3(256), 0, bcm::hs(stream),
+                         static_cast<const T*>(x), x_batch_stride, x_dim_stride, (int)D, L, weight, bias, K,
+                         static_cast<const T*>(du), n_events, bitmask, W, mask_row_div, tile_start, nT,
+                         static_cast<T*>(dx), part, rows);
+    };
+    using K4 = std::integral_constant<int, 4>;
+    using K8 = std::integral_constant<int, 8>;
+    if (silu) {
+      if (K == 4) go(std::true_type{}, K4{});
+      else go(std::true_type{}, K8{});
+    } else {
+      if (K == 4) go(std::false_type{}, K4{});
+      else go(std::false_type{}, K8{});
+    }
+  });
+  rc = bcm::check_launch(fn);
+  if (rc) return rc;
+  const int64_t n = D * (K + 1);
+  hipLaunchKernelGGL(bcm::k_conv_bwd_events_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     bcm::hs(stream), part, B, (int)D, K, dweight, dbias);
   return bcm::check_launch(fn);
 }
 

@@ -181,12 +181,41 @@ __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict_
 // ------------------------------------------------------------------- fill
 constexpr int kFillSeg = 64 * 32;  // steps per segment (one word per lane)
 
+// The depthwise causal conv + SiLU evaluated at the events (fill with
+// KM > 0): row lc of the conv input is x + (lc / dim) * sb + (lc % dim) * sd.
+struct ConvAt {
+  const float* w;     // [dim, K]
+  const float* bias;  // [dim] or NULL
+  int K, dim, silu;
+  int64_t sb, sd;     // element strides of the batch and channel index
+};
+
+// silu(bias + sum_k w[k] x[t-(K-1)+k]) at step t of row xr, x = 0 before
+// t = 0: the expression and order of bcm_causal_conv1d_fwd, so the value
+// (after rounding to T) is the one the dense conv writes at (row, t).
+template <typename T, int KM>
+__device__ __forceinline__ T conv_at(const T* __restrict__ xr, int t, const float* wk, float b0, int K, bool silu) {
+  float xv[KM];
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {  // the taps' loads in flight together
+    const int tt = t - (K - 1) + k;
+    xv[k] = (k < K && tt >= 0) ? to_f(ld_stream_elem(xr + tt)) : 0.0f;
+  }
+  float pre = b0;
+#pragma unroll
+  for (int k = 0; k < KM; ++k)
+    if (k < K) pre = fmaf(wk[k], xv[k], pre);
+  return from_f<T>(silu ? pre / (1.0f + __expf(-pre)) : pre);
+}
+
 // BLK: the row offsets come from the count pass's block sums (bsum/bmax,
 // one per 4 rows): the block adds up the sums of the blocks before it and
 // the counts of its rows before each row, and writes cu_seqlens itself.
 // Block 0 also writes meta = (E, max count) (one 64-bit store written
 // through to memory, so a host may poll it while the fill runs).
-template <typename T, bool GATHER, bool TILES, bool BLK>
+// KM = 0: x_ev gathers x at the events; KM = 4 (width exactly 4) or 8 (any
+// width <= 8): x_ev is the conv + SiLU of x (ConvAt) at the events.
+template <typename T, bool GATHER, bool TILES, bool BLK, int KM = 0>
 __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitmask, int64_t W,
                                               const int32_t* __restrict__ base_cu, int64_t n_rows, int64_t L,
                                               int expand, const T* __restrict__ x, int32_t* __restrict__ ch_ids,
@@ -194,7 +223,9 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
                                               T* __restrict__ x_ev, int32_t* __restrict__ tile_start, int64_t nT,
                                               int32_t* __restrict__ head_flags, const int32_t* __restrict__ counts,
                                               const int32_t* __restrict__ bsum, const int32_t* __restrict__ bmax,
-                                              int32_t* __restrict__ meta, int32_t* __restrict__ cu_out) {
+                                              int32_t* __restrict__ meta, int32_t* __restrict__ cu_out,
+                                              const ConvAt cv) {
+  static_assert(KM == 0 || GATHER, "the conv form writes x_ev");
   __shared__ int32_t s_t[4][kFillSeg];
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int64_t c = (int64_t)blockIdx.x * 4 + wave;
@@ -292,6 +323,18 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
     for (int r = 0; r < expand; ++r) {
       const int64_t lc = c * expand + r;
       const int64_t obase = (int64_t)cu0 * expand + (int64_t)r * n + off;
+      // conv form: the channel's taps and input row (wave-uniform)
+      constexpr int KW = KM > 0 ? KM : 1;
+      float wk[KW];
+      float b0 = 0.0f;
+      const T* xr = x + lc * L;
+      if constexpr (KM > 0) {
+        const int dch = (int)(lc % cv.dim);
+#pragma unroll
+        for (int k = 0; k < KM; ++k) wk[k] = k < cv.K ? cv.w[(int64_t)dch * cv.K + k] : 0.0f;
+        b0 = cv.bias ? cv.bias[dch] : 0.0f;
+        xr = x + (lc / cv.dim) * cv.sb + (int64_t)dch * cv.sd;
+      }
       for (int i0 = 0; i0 < seg_cnt; i0 += 4 * kWave) {
         int tv[4];
         T xv[4];
@@ -299,7 +342,8 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
         for (int q = 0; q < 4; ++q) {
           const int i = i0 + q * kWave + lane;
           tv[q] = i < seg_cnt ? st[i] : 0;
-          if (GATHER) xv[q] = ld_stream_elem(x + lc * L + tv[q]);
+          if constexpr (KM > 0) xv[q] = conv_at<T, KM>(xr, tv[q], wk, b0, KM == 4 ? 4 : cv.K, cv.silu != 0);
+          else if (GATHER) xv[q] = ld_stream_elem(xr + tv[q]);
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -548,7 +592,7 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_
     constexpr bool TT = decltype(tiles)::value;
     hipLaunchKernelGGL((k_fill<T, G, TT, false>), grid, block, 0, hs(stream), bitmask, W, base_cu, n_rows, L, ex,
                        static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
-                       head_flags, nullptr, nullptr, nullptr, nullptr, nullptr);
+                       head_flags, nullptr, nullptr, nullptr, nullptr, nullptr, ConvAt{});
   };
   using Y = std::true_type;
   using N = std::false_type;
@@ -615,7 +659,7 @@ int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts, cons
     constexpr bool TT = decltype(tiles)::value;
     hipLaunchKernelGGL((k_fill<T, G, TT, true>), grid, block, 0, hs(stream), bitmask, W, nullptr, n_rows, L, ex,
                        static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
-                       nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens);
+                       nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens, ConvAt{});
   };
   using Y = std::true_type;
   using N = std::false_type;
@@ -628,6 +672,50 @@ int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts, cons
     if (tile_start) launch(float{}, N{}, Y{});
     else launch(float{}, N{}, N{});
   }
+  return check_launch(fn);
+}
+
+int bcm_extract_fill_blocks_conv(const uint32_t* bitmask, const int32_t* counts, const int32_t* block_sums,
+                                 int32_t* meta, int64_t n_rows, int64_t L, int64_t expand, const void* x, int x_dtype,
+                                 int64_t x_batch_stride, int64_t x_dim_stride, int64_t dim, const float* weight,
+                                 const float* bias, int K, int silu, int32_t* cu_seqlens, int32_t* ch_ids,
+                                 int32_t* t_steps, int32_t* k_flat, void* x_events, int32_t* tile_start,
+                                 bcm_stream_t stream) {
+  const char* fn = "bcm_extract_fill_blocks_conv";
+  if (n_rows < 1 || L < 1 || expand < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (!bitmask || !counts || !block_sums || !meta || !cu_seqlens || !k_flat || !x || !x_events || !weight)
+    return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!aligned(meta, 8)) return set_error(BCM_EINVAL, "%s: meta must be 8-byte aligned", fn);
+  if (!dtype_ok(x_dtype)) return set_error(BCM_EINVAL, "%s: x must be fp32, fp16 or bf16", fn);
+  if (K < 1 || K > 8) return set_error(BCM_EINVAL, "%s: kernel width must be in [1, 8]", fn);
+  if (dim < 1 || (n_rows * expand) % dim != 0 || dim > INT32_MAX)
+    return set_error(BCM_EINVAL, "%s: n_rows * expand must be a multiple of dim", fn);
+  if (x_batch_stride < 0 || x_dim_stride < 0) return set_error(BCM_EINVAL, "%s: negative stride", fn);
+  if (n_rows * expand * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: rows * expand * L must fit in int32", fn);
+  if (tile_start && !aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  const int64_t W = bitmask_words(L), nT = tile_count(L), nblk = (n_rows + 3) / 4;
+  const dim3 grid((unsigned)nblk), block(256);
+  const int ex = (int)expand;
+  const ConvAt cv{weight, bias, K, (int)dim, silu, x_batch_stride, x_dim_stride};
+  dispatch_dtype(x_dtype, [&](auto tag) {
+    using T = decltype(tag);
+    auto go = [&](auto tiles, auto km) {
+      constexpr bool TT = decltype(tiles)::value;
+      constexpr int KM = decltype(km)::value;
+      hipLaunchKernelGGL((k_fill<T, true, TT, true, KM>), grid, block, 0, hs(stream), bitmask, W, nullptr, n_rows, L,
+                         ex, static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start,
+                         nT, nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens, cv);
+    };
+    using K4 = std::integral_constant<int, 4>;
+    using K8 = std::integral_constant<int, 8>;
+    if (tile_start) {
+      if (K == 4) go(std::true_type{}, K4{});
+      else go(std::true_type{}, K8{});
+    } else {
+      if (K == 4) go(std::false_type{}, K4{});
+      else go(std::false_type{}, K8{});
+    }
+  });
   return check_launch(fn);
 }
 

@@ -4,14 +4,19 @@
 `Mamba` block (:258-506) with `extract_events_1d` (:361-409).
 
 The block runs the same composition as the reference: dense in_proj GEMM,
-depthwise causal conv + SiLU (PyTorch-ROCm), then the event path on the HIP
+depthwise causal conv + SiLU, then the event path on the HIP
 kernels (extraction, gather, flat selective scan, zero-order-hold restore),
 then out_proj. With `fused_event_path=True` (default) the block calls the
 fused entry points: one extraction pass that also gathers x_conv at the
 events and builds the event index, the restore reads that index instead of
 rebuilding it, the scan backward writes the dense x_conv gradient rows from
 the same index (no separate gather backward), and the per-block host syncs
-drop from two to one. Results are identical to the unfused composition.
+drop from two to one. With `conv_at_events=True` (default) the depthwise
+conv + SiLU is evaluated only at the events, by the extraction itself, and
+its backward goes from du straight to the conv input's gradient: no dense
+x_conv exists in either direction. Results match the unfused composition
+(forward values identical; the conv weight gradients up to summation
+order).
 
 The decode `step` / inference cache of the reference are not part of the
 event path (the reference's own `step` reads an undefined `self.pw_B`).
@@ -28,7 +33,7 @@ try:
     from . import extract_events_cuda as _ee_cuda
     from . import restore_dense_cuda_nodecay
     from . import selective_scan_cuda
-    from .causal_conv1d import causal_conv1d_fn
+    from .causal_conv1d import causal_conv1d_fn, conv1d_bwd_events
     from .runtime_breakdown import cuda_stage
     from .selective_scan_interface import selective_scan_flat_ch_fn
 except ImportError:  # imported with this directory on sys.path
@@ -36,7 +41,7 @@ except ImportError:  # imported with this directory on sys.path
     import extract_events_cuda as _ee_cuda
     import restore_dense_cuda_nodecay
     import selective_scan_cuda
-    from causal_conv1d import causal_conv1d_fn
+    from causal_conv1d import causal_conv1d_fn, conv1d_bwd_events
     from runtime_breakdown import cuda_stage
     from selective_scan_interface import selective_scan_flat_ch_fn
 
@@ -119,6 +124,31 @@ class _IndexedGatherFn(torch.autograd.Function):
         return dx, None, None
 
 
+def _event_scan_fwd(ctx, x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D):
+    """Depthwise flat scan forward of the fused block; keeps what the
+    backward (_event_scan_bwd) reads in ctx."""
+    dt_idle, dt_active = dt_idle.contiguous(), dt_active.contiguous()
+    A, W_B, W_C = A.contiguous(), W_B.contiguous(), W_C.contiguous()
+    chunk_g = selective_scan_cuda.chunk_states_buffer(x_ev, cu_seqlens, max_seqlen, A)
+    out, xs = selective_scan_cuda.fwd_flat_ch(x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D,
+                                              None, is_depthwise_bc=True, _chunk_g=chunk_g)
+    ctx.scan = (x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs, D)
+    ctx.chunk_g, ctx.max_seqlen = chunk_g, max_seqlen
+    return out
+
+
+def _event_scan_bwd(ctx, dout, rows=None):
+    """(du, dt_idle, dt_active, dA, dW_B, dW_C, dD) of the fused block's scan;
+    with rows = (bitmask, expand, tile_start, dx) the scan kernel also
+    writes the dense gather backward into dx."""
+    x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs, D = ctx.scan
+    res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, W_B, W_C,
+                                          dout.contiguous(), xs, D, is_depthwise_bc=True, _chunk_g=ctx.chunk_g,
+                                          _rows=rows)
+    du, dA, dW_B, dW_C, ddt_idle, ddt_active = res[:6]
+    return du, ddt_idle, ddt_active, dA, dW_B, dW_C, (res[6] if D is not None else None)
+
+
 class _IndexedScanFn(torch.autograd.Function):
     """The gather of x_conv at the events (already done by the fused
     extraction) and the depthwise flat scan as one autograd node. Its
@@ -130,32 +160,46 @@ class _IndexedScanFn(torch.autograd.Function):
     def forward(ctx, x_conv, payload, event_index, k_flat, cu_seqlens, max_seqlen: int, dt_idle, dt_active, A, W_B,
                 W_C, D):
         # payload = (x_events,): kept out of the autograd inputs on purpose
-        x_ev = payload[0]
-        dt_idle, dt_active = dt_idle.contiguous(), dt_active.contiguous()
-        A, W_B, W_C = A.contiguous(), W_B.contiguous(), W_C.contiguous()
-        chunk_g = selective_scan_cuda.chunk_states_buffer(x_ev, cu_seqlens, max_seqlen, A)
-        out, x = selective_scan_cuda.fwd_flat_ch(x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B,
-                                                 W_C, D, None, is_depthwise_bc=True, _chunk_g=chunk_g)
-        ctx.save_for_backward(x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, x,
-                              *([D] if D is not None else []))
-        ctx.chunk_g, ctx.event_index, ctx.max_seqlen = chunk_g, event_index, max_seqlen
-        ctx.shape, ctx.has_D = x_conv.shape, D is not None
-        return out
+        ctx.event_index, ctx.shape = event_index, x_conv.shape
+        return _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D)
 
     @staticmethod
     def backward(ctx, dout):
-        x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, x = ctx.saved_tensors[:9]
-        D = ctx.saved_tensors[9] if ctx.has_D else None
         B, Dm, L = ctx.shape
         bitmask, tile_start, expand = ctx.event_index
+        x_ev = ctx.scan[0]
         dx = torch.empty((B * Dm, L), dtype=x_ev.dtype, device=x_ev.device)
         with cuda_stage("sparse_scan_backward"):
-            res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A,
-                                                  W_B, W_C, dout.contiguous(), x, D, is_depthwise_bc=True,
-                                                  _chunk_g=ctx.chunk_g, _rows=(bitmask, expand, tile_start, dx))
-        _du, dA, dW_B, dW_C, ddt_idle, ddt_active = res[:6]
-        dD = res[6] if ctx.has_D else None
-        return dx.view(B, Dm, L), None, None, None, None, None, ddt_idle, ddt_active, dA, dW_B, dW_C, dD
+            _du, *grads = _event_scan_bwd(ctx, dout, rows=(bitmask, expand, tile_start, dx))
+        ctx.scan = None
+        return (dx.view(B, Dm, L), None, None, None, None, None, *grads)
+
+
+class _IndexedConvScanFn(torch.autograd.Function):
+    """The block's depthwise causal conv + SiLU evaluated only at the events
+    (by the fused extraction, from the conv input x), the gather and the
+    depthwise flat scan as one autograd node: no dense x_conv is written or
+    read, forward or backward. The backward runs the scan backward to du and
+    then bcm_causal_conv1d_bwd_events, which writes dx (x's strides),
+    dweight and dbias from du. Same values as the dense conv followed by
+    _IndexedScanFn (dweight / dbias up to summation order)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, payload, event_index, k_flat, cu_seqlens, max_seqlen: int, dt_idle, dt_active,
+                A, W_B, W_C, D):
+        ctx.event_index, ctx.conv = event_index, (x, weight, bias)
+        return _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, weight, bias = ctx.conv
+        with cuda_stage("sparse_scan_backward"):
+            du, *grads = _event_scan_bwd(ctx, dout)
+        with cuda_stage("conv_backward"):
+            dx, dw, db = conv1d_bwd_events(x, weight, bias, True, du, ctx.event_index)
+        ctx.scan = ctx.conv = None
+        return (dx, dw.to(weight.dtype), db.to(bias.dtype) if db is not None else None, None, None, None, None, None,
+                *grads)
 
 
 class _IndexedRestoreFn(torch.autograd.Function):
@@ -229,7 +273,7 @@ class Mamba(nn.Module):
                  dt_init="random", dt_scale=1.0, dt_init_floor=1e-4, conv_bias=True, bias=False,
                  use_fast_path=False, spiking=True, spike_mode="ste", prob_activation="sigmoid",
                  sample_inference=False, threshold=0.5, layer_idx=None, device=None, dtype=None,
-                 fused_event_path=True):
+                 fused_event_path=True, conv_at_events=True):
         factory_kwargs = {"device": device, "dtype": dtype}
         super().__init__()
         self.d_model, self.d_state, self.d_conv, self.expand = d_model, d_state, d_conv, expand
@@ -244,6 +288,7 @@ class Mamba(nn.Module):
         self.sample_inference, self.threshold = sample_inference, threshold
         self.scan_impl = "flat_ch"
         self.fused_event_path = fused_event_path
+        self.conv_at_events = conv_at_events
 
         self.in_proj = nn.Linear(self.d_model, self.d_inner, bias=bias, **factory_kwargs)
         self.conv1d = nn.Conv1d(in_channels=self.d_inner, out_channels=self.d_inner, bias=conv_bias,
@@ -299,6 +344,14 @@ class Mamba(nn.Module):
             return causal_conv1d_fn(x, self.conv1d.weight[:, 0, :], self.conv1d.bias, activation="silu")
         return self.act(self.conv1d(x)[..., :seqlen])
 
+    def _conv_at_events_ok(self, x):
+        """The fused path evaluates the conv at the events when x's rows are
+        contiguous and 4-step aligned (bcm_causal_conv1d_bwd_events)."""
+        es = x.element_size()
+        return (self.fused_event_path and self.conv_at_events and x.stride(2) == 1 and x.size(2) % 4 == 0
+                and x.stride(0) % 4 == 0 and x.stride(1) % 4 == 0 and x.data_ptr() % (4 * es) == 0
+                and self.d_conv <= 8 and x.dtype in (torch.float32, torch.float16, torch.bfloat16))
+
     def forward(self, hidden_states, inference_params=None):
         if inference_params is not None:
             raise RuntimeError("Mamba: the decode / inference-cache path is not part of the event-path build")
@@ -307,7 +360,9 @@ class Mamba(nn.Module):
                       l=seqlen)
         if self.in_proj.bias is not None:
             x = x + rearrange(self.in_proj.bias.to(dtype=x.dtype), "d -> d 1")
-        x = self._conv(x, seqlen).contiguous()
+        conv_ev = self._conv_at_events_ok(x)
+        if not conv_ev:
+            x = self._conv(x, seqlen).contiguous()
 
         dt_idle, dt_active = self.delta_gen.levels()
         A = -torch.exp(self.A_log)
@@ -317,13 +372,18 @@ class Mamba(nn.Module):
 
         if self.fused_event_path:
             base_input = rearrange(hidden_states.detach(), "b l d -> b d l").contiguous()
+            w_conv, b_conv = self.conv1d.weight[:, 0, :], self.conv1d.bias
             with cuda_stage("routing_index_extraction"):
                 _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_ev, event_index = \
                     _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach(),
-                                                    positions=False)
+                                                    positions=False, conv=(w_conv, b_conv, True) if conv_ev else None)
             with cuda_stage("sparse_scan_forward"):
-                y_flat = _IndexedScanFn.apply(x, (x_ev,), event_index, k_flat, cu_seqlens, int(max_seqlen), dt_idle,
-                                              dt_active, A, W_B, W_C, self.D)
+                if conv_ev:  # x is the conv input: silu(conv(x)) exists only at the events
+                    y_flat = _IndexedConvScanFn.apply(x, w_conv, b_conv, (x_ev,), event_index, k_flat, cu_seqlens,
+                                                      int(max_seqlen), dt_idle, dt_active, A, W_B, W_C, self.D)
+                else:
+                    y_flat = _IndexedScanFn.apply(x, (x_ev,), event_index, k_flat, cu_seqlens, int(max_seqlen),
+                                                  dt_idle, dt_active, A, W_B, W_C, self.D)
         else:
             _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_conv_flat = self.extract_events_1d(
                 hidden_states, x, self.threshold)

@@ -193,7 +193,7 @@ def _extract_indexed_exact(base_input, threshold, expand, x, positions):
         return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)
 
 
-def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True, exact_alloc=False):
+def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True, exact_alloc=False, conv=None):
     """Fused extraction for the block forward (no reference counterpart; the
     reference composes extract_base_events + expand_base_events +
     gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
@@ -207,14 +207,27 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
     block sums (no offsets kernel) and is enqueued before E is known, so its
     event outputs are allocated for every possible event (B*d_model*expand*L)
     and returned as views of the first E. exact_alloc=True runs the separate
-    offsets pass, reads E first and allocates exactly E."""
+    offsets pass, reads E first and allocates exactly E.
+
+    conv = (weight [D, K], bias [D] or None, silu): x is then the input of
+    the block's depthwise causal conv (rows contiguous, any batch / channel
+    strides, e.g. the in_proj GEMM output viewed as [B, D, L]) and x_events
+    is silu(conv(x)) evaluated at the events only, the values the dense
+    conv followed by the gather would give (bcm_extract_fill_blocks_conv)."""
     _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
            "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
     B, Dm, L = base_input.shape
     expand = int(expand)
     dev = base_input.device
     NC = B * Dm
-    if x is not None:
+    if conv is not None:
+        _check(x is not None and x.is_cuda and x.dim() == 3 and tuple(x.shape) == (B, Dm * expand, L)
+               and x.stride(2) == 1, "x must be a CUDA tensor [B, d_model*expand, L] with contiguous rows")
+        _check(not exact_alloc, "conv needs the fused fill (exact_alloc=False)")
+        if NC == 0 or L == 0:
+            r = _extract_indexed_exact(base_input, threshold, expand, None, positions)
+            return r[:5] + (torch.empty(0, dtype=x.dtype, device=dev),) + r[6:]
+    elif x is not None:
         _check(x.is_cuda and x.is_contiguous() and tuple(x.shape) == (B, Dm * expand, L),
                "x must be a contiguous CUDA tensor [B, d_model*expand, L]")
     if exact_alloc or NC == 0 or L == 0:
@@ -235,9 +248,19 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
         meta.arm()
         _nat.call("bcm_extract_count_blocks", _nat.ptr(x2d), _nat.dtype_code(base_input.dtype), NC, L,
                   float(threshold), _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), s)
-        _nat.call("bcm_extract_fill_blocks", _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), meta.ptr(), NC,
-                  L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(cu),
-                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
+        if conv is None:
+            _nat.call("bcm_extract_fill_blocks", _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), meta.ptr(),
+                      NC, L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(cu),
+                      _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
+        else:
+            w, b, silu = conv
+            w = w.detach().float().contiguous()
+            b = b.detach().float().contiguous() if b is not None else None
+            _check(w.dim() == 2 and w.size(0) == Dm * expand and 1 <= w.size(1) <= 8, "conv weight must be [D, K<=8]")
+            _nat.call("bcm_extract_fill_blocks_conv", _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums),
+                      meta.ptr(), NC, L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype), x.stride(0), x.stride(1),
+                      Dm * expand, _nat.ptr(w), _nat.ptr(b), int(w.size(1)), int(bool(silu)), _nat.ptr(cu),
+                      _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
         E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
         E = E_base * expand
         k = k[:E]

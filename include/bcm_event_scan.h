@@ -121,6 +121,26 @@ int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts,
                             int32_t* k_flat, void* x_events,
                             int32_t* tile_start, bcm_stream_t stream);
 
+/* bcm_extract_fill_blocks with the depthwise causal conv + SiLU of the
+ * model block (e_model.py:442-451) evaluated at the events instead of
+ * gathered from a dense x_conv (the conv producer fused with the gather,
+ * e_model.py:403-406): for the event (ch, t), d = ch % dim,
+ *   x_events[e] = silu(bias[d] + sum_k weight[d,k] x[ch, t-(K-1)+k])
+ * with x = 0 before t = 0 (plain conv when silu == 0); the value, rounding
+ * included, that bcm_causal_conv1d_fwd writes at (ch, t). x is the conv
+ * input: row ch = b * dim + d starts at x + b * x_batch_stride +
+ * d * x_dim_stride (elements; rows contiguous), so the [D, B*L] output of the
+ * in_proj GEMM is read in place. weight [dim, K] (K <= 8), bias [dim] or
+ * NULL, fp32. The other arguments are those of bcm_extract_fill_blocks. */
+int bcm_extract_fill_blocks_conv(const uint32_t* bitmask, const int32_t* counts,
+                                 const int32_t* block_sums, int32_t* meta,
+                                 int64_t n_rows, int64_t L, int64_t expand,
+                                 const void* x, int x_dtype, int64_t x_batch_stride,
+                                 int64_t x_dim_stride, int64_t dim, const float* weight,
+                                 const float* bias, int K, int silu, int32_t* cu_seqlens,
+                                 int32_t* ch_ids, int32_t* t_steps, int32_t* k_flat,
+                                 void* x_events, int32_t* tile_start, bcm_stream_t stream);
+
 /* expand_base_events (extract_events_cuda.cu:529-603): logical cu_seqlens
  * [n_rows*expand+1] and expanded streams [E_base*expand]. */
 int bcm_expand_events(const int32_t* base_ch, const int32_t* base_t,
@@ -304,6 +324,26 @@ int64_t bcm_causal_conv1d_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, i
 int bcm_causal_conv1d_bwd(const void* x, int dtype, const float* weight, const float* bias, const void* dout,
                           int64_t B, int64_t D, int64_t L, int K, int silu, void* dx, float* dweight,
                           float* dbias, void* workspace, int64_t workspace_bytes, bcm_stream_t stream);
+
+/* Backward of the conv evaluated at the events (bcm_extract_fill_blocks_conv)
+ * and the gather (GatherEventsFn.backward, e_model.py:188-193, then the conv
+ * backward of e_model.py:442-451): from du [n_events], the gradient of
+ * x_events, with g = du * silu'(pre) at the events and 0 elsewhere,
+ *   dx[ch, t] = sum_k weight[d,k] g[ch, t+(K-1)-k]   (dtype; every step written)
+ *   dweight[d,k] = sum g x[ch, t-(K-1)+k],  dbias[d] = sum g   (fp32, fully
+ *   written; rows summed in row order, no atomics)
+ * x and dx have the row strides of bcm_extract_fill_blocks_conv (rows
+ * ch = b * D + d, B * D of them); bitmask / mask_row_div / tile_start are
+ * the extraction's event index. Needs L and both strides multiples of 4,
+ * x and dx aligned to 4 elements, and a workspace of
+ * bcm_causal_conv1d_bwd_events_workspace_bytes(B, D, K) bytes. */
+int64_t bcm_causal_conv1d_bwd_events_workspace_bytes(int64_t B, int64_t D, int K);
+int bcm_causal_conv1d_bwd_events(const void* x, int dtype, int64_t x_batch_stride, int64_t x_dim_stride,
+                                 int64_t B, int64_t D, int64_t L, const float* weight, const float* bias,
+                                 int K, int silu, const void* du, int64_t n_events,
+                                 const uint32_t* bitmask, int64_t mask_row_div,
+                                 const int32_t* tile_start, void* dx, float* dweight, float* dbias,
+                                 void* workspace, int64_t workspace_bytes, bcm_stream_t stream);
 
 /* ---- (3) zero-order-hold restore ---------------------------------------- */
 /* Event index of sorted per-channel time steps (the restore kernels' input

@@ -66,3 +66,67 @@ def test_conv1d_bf16_and_deterministic(cuda_device):
     assert_close(dxg.float().cpu(), dx, 2e-2, 2e-3, "dx")
     assert_close(dwg.cpu(), dw, 2e-2, 2e-3, "dw")
     assert_close(dbg.cpu(), db, 2e-2, 2e-3, "dbias")
+
+
+# ---- the conv evaluated at the events (fill) and its backward from du ----
+from bc_mamba_amd import extract_events_cuda as ee  # noqa: E402
+from bc_mamba_amd.causal_conv1d import conv1d_bwd_events  # noqa: E402
+
+
+def _in_proj_layout(x):
+    """x [B, D, L] laid out as the block's in_proj output: a [D, B*L] matrix
+    viewed as [B, D, L] (row (b, d) at d*B*L + b*L; rows contiguous)."""
+    B, D, L = x.shape
+    return x.permute(1, 0, 2).contiguous().view(D, B * L).view(D, B, L).permute(1, 0, 2)
+
+
+@pytest.mark.parametrize("B,Dm,expand,L,K,silu,bias,dtype,strided", [
+    (2, 8, 1, 256, 4, True, True, torch.float32, False),
+    (3, 4, 2, 300, 4, True, True, torch.float32, True),     # in_proj layout, expanded channels
+    (2, 4, 2, 1100, 3, True, False, torch.float32, True),   # width 3 (any-width form), two 1024-step windows
+    (2, 6, 1, 64, 8, False, True, torch.float32, False),    # plain conv, width 8
+    (2, 8, 2, 512, 4, True, True, torch.bfloat16, True),
+    (2, 8, 1, 200, 4, True, True, torch.float16, False),
+])
+def test_conv_at_events_matches_dense_conv_then_gather(cuda_device, B, Dm, expand, L, K, silu, bias, dtype, strided):
+    """x_events of the fill with conv (bcm_extract_fill_blocks_conv) equal
+    bit for bit the dense conv followed by the gather; the backward from du
+    (bcm_causal_conv1d_bwd_events) gives the dense path's dx bit for bit and
+    its dweight / dbias within 1e-5 (fp32 sums in another order)."""
+    print(f"conv-at-events case B={B} Dm={Dm} x{expand} L={L} K={K} silu={silu} {dtype} strided={strided}",
+          flush=True)
+    dev = cuda_device
+    D = Dm * expand
+    g = torch.Generator().manual_seed(L + K + B)
+    mem = (torch.rand(B, Dm, L, generator=g) < 0.2).float().to(dev)
+    x = torch.randn(B, D, L, generator=g).to(dtype).to(dev)
+    if strided:
+        x = _in_proj_layout(x)
+        assert not x.is_contiguous() and x.stride(2) == 1
+    w = (torch.randn(D, K, generator=g) / K).to(dev)
+    b = torch.randn(D, generator=g).to(dev) if bias else None
+    # dense reference: conv, then the fused extraction's gather
+    xc = causal_conv1d_fn(x.contiguous(), w, b, activation="silu" if silu else None)
+    _, _, k1, cu1, ms1, xe_ref, idx = ee.extract_events_indexed(mem, 0.5, expand, xc, positions=False)
+    _, _, k2, cu2, ms2, xe, idx2 = ee.extract_events_indexed(mem, 0.5, expand, x, positions=False,
+                                                            conv=(w, b, silu))
+    assert torch.equal(k1, k2) and torch.equal(cu1, cu2) and ms1 == ms2
+    nw = (L + 31) // 32  # bitmask rows are padded to 1024 steps; the padding words are not written
+    assert torch.equal(idx[0][:, :nw], idx2[0][:, :nw]) and torch.equal(idx[1], idx2[1])
+    assert xe.dtype == dtype and torch.equal(xe, xe_ref)
+    # backward: du at the events -> dense dx_conv -> dense conv backward
+    du = torch.randn(xe.numel(), generator=g).to(dtype).to(dev)
+    dxc = torch.empty(B * D, L, dtype=dtype, device=dev)
+    ee._nat.call("bcm_gather_bwd_rows", du.data_ptr(), ee._nat.dtype_code(dtype), idx[0].data_ptr(), expand,
+                 idx[1].data_ptr(), B * D, L, dxc.data_ptr(), ee._nat.stream_of(du))
+    xr = x.contiguous().requires_grad_(True)
+    wr = w.clone().requires_grad_(True)
+    br = b.clone().requires_grad_(True) if bias else None
+    causal_conv1d_fn(xr, wr, br, activation="silu" if silu else None).backward(dxc.view(B, D, L))
+    dx, dw, db = conv1d_bwd_events(x, w, b, silu, du, idx2)
+    torch.cuda.synchronize()
+    assert dx.stride() == x.stride()
+    assert torch.equal(dx, xr.grad)
+    assert_close(dw.cpu(), wr.grad.cpu().numpy(), 1e-5, 1e-6, "dweight")
+    if bias:
+        assert_close(db.cpu(), br.grad.cpu().numpy(), 1e-5, 1e-6, "dbias")

@@ -126,3 +126,32 @@ def test_config4_model_fused_matches_reference_composition(cuda_device):
     assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 10
     for n in grads[0]:
         assert_close(grads[0][n].cpu(), grads[1][n].cpu().numpy(), 1e-3, 1e-4, n)
+
+
+def test_mamba_block_conv_at_events_matches_dense_conv(cuda_device):
+    """The fused block with the conv evaluated at the events equals the
+    fused block with the dense HIP conv: output and the scan / projection
+    gradients bit for bit; the conv weight / bias gradients (summed in
+    another order) and those behind in_proj (its GEMM sees dx in another
+    layout) within the fp32 bar."""
+    torch.manual_seed(0)
+    blk = e_model.Mamba(d_model=32, d_state=16, expand=2, device=cuda_device)
+    torch.manual_seed(1)
+    hs = (torch.rand(3, 304, 32, device=cuda_device) > 0.7).float()
+    outs, grads = [], []
+    for at_events in (True, False):
+        blk.conv_at_events = at_events
+        blk.zero_grad()
+        h = hs.clone().requires_grad_(True)
+        o = blk(h)
+        (o * torch.linspace(-1, 1, o.numel(), device=cuda_device).view_as(o)).sum().backward()
+        outs.append(o.detach())
+        grads.append({n: p.grad.detach().clone() for n, p in blk.named_parameters() if p.grad is not None})
+        grads[-1]["input"] = h.grad.detach().clone()
+    assert torch.equal(outs[0], outs[1])
+    assert grads[0].keys() == grads[1].keys() and "conv1d.weight" in grads[0]
+    for n in grads[0]:
+        if n.startswith(("conv1d.", "in_proj.")) or n == "input":
+            assert_close(grads[0][n].cpu(), grads[1][n].cpu().numpy(), 1e-4, 1e-5, n)
+        else:
+            assert torch.equal(grads[0][n], grads[1][n]), n
