@@ -205,6 +205,24 @@ __global__ __launch_bounds__(256) void k_conv_bwd_reduce(const float* __restrict
   else if (dbias) dbias[d] = v;
 }
 
+// x[t .. t+3] of a row through a buffer resource over the row: vectors
+// before the row start or past its end read 0 (no branch, so the loads of a
+// window issue back to back). t is a multiple of 4 and L % 4 == 0.
+template <typename T>
+__device__ __forceinline__ void buf_load4(__amdgpu_buffer_rsrc_t r, int64_t t, int64_t L, float* v) {
+  const uint32_t off = (t >= 0 && t < L) ? (uint32_t)(t * (int64_t)sizeof(T)) : kBufOOB;
+  if constexpr (sizeof(T) == 4) {
+    const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(q[i]);
+  } else {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    const T* e = reinterpret_cast<const T*>(&q);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = to_f(e[i]);
+  }
+}
+
 // ---------------------------------------------- backward from the events
 // The conv evaluated only at the events (x_events of the fused fill), so its
 // gradient arrives as du [E], one value per event. g = du * silu'(pre) lives
@@ -240,6 +258,7 @@ __global__ __launch_bounds__(256) void k_conv_bwd_events(
   for (int k = 0; k < KM; ++k) wk[k] = k < K ? w[(int64_t)d * K + k] : 0.0f;
   const float b0 = bias ? bias[d] : 0.0f;
   const __amdgpu_buffer_rsrc_t rdu = buf_rsrc(du, n_events * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xr, L * (int64_t)sizeof(T));
   float* sg = s_g[wave];
   float aw[KM], ab = 0.0f;
 #pragma unroll
@@ -248,50 +267,61 @@ __global__ __launch_bounds__(256) void k_conv_bwd_events(
   wave_sync();
   constexpr int SEGS = kCbWin / (4 * kWave);
   for (int64_t w0 = (L - 1) / kCbWin * kCbWin; w0 >= 0; w0 -= kCbWin) {
+    // pass 1: g at the lane's 4 steps of each segment. Two rounds of loads
+    // per window: x, masks and table entries of all segments, then the
+    // events' du; lanes past L (L % 4 == 0: whole vectors) get g = 0
+    float xv[SEGS][PRE + 4];  // xv[q][i] = x[t0-PRE+i]
+    uint64_t m[SEGS];
+    int32_t tv[SEGS];
 #pragma unroll
-    for (int q = 0; q < SEGS; ++q) {  // pass 1: g at the lane's 4 steps
+    for (int q = 0; q < SEGS; ++q) {
+      const int64_t t0 = w0 + 4 * kWave * q + 4 * lane;
+#pragma unroll
+      for (int v = 0; v < PRE / 4 + 1; ++v) buf_load4<T>(rx, t0 - PRE + 4 * v, L, xv[q] + 4 * v);
+      const int64_t tl = (t0 < L ? t0 : 0) / kTile;
+      m[q] = tile_mask(mrow, tl);
+      tv[q] = tsr[tl];
+    }
+    float dv[SEGS][4];
+    uint32_t nib[SEGS];
+#pragma unroll
+    for (int q = 0; q < SEGS; ++q) {
+      const int64_t t0 = w0 + 4 * kWave * q + 4 * lane;
+      const int off = (int)(t0 % kTile);
+      nib[q] = t0 < L ? (uint32_t)(m[q] >> off) & 0xFu : 0u;
+      uint32_t e = (uint32_t)tv[q] + (uint32_t)__popcll(m[q] & ((1ull << off) - 1ull));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t bit = (nib[q] >> k) & 1u;
+        dv[q][k] = buf_load<T>(rdu, bit ? e * (uint32_t)sizeof(T) : kBufOOB);
+        e += bit;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < SEGS; ++q) {
       const int lt = 4 * kWave * q + 4 * lane;
-      const int64_t t0 = w0 + lt;
-      float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (t0 < L) {  // L % 4 == 0: all 4 steps in range
-        float xv[PRE + 4];  // xv[i] = x[t0-PRE+i]
+      float g[4];
 #pragma unroll
-        for (int v = 0; v < PRE / 4 + 1; ++v) load4<T, true>(xr, t0 - PRE + 4 * v, L, xv + 4 * v);
-        const int64_t tl = t0 / kTile;
-        const int off = (int)(t0 % kTile);
-        const uint64_t m = tile_mask(mrow, tl);
-        const uint32_t nib = (uint32_t)(m >> off) & 0xFu;
-        uint32_t e = (uint32_t)tsr[tl] + (uint32_t)__popcll(m & ((1ull << off) - 1ull));
-        float dv[4];
+      for (int k = 0; k < 4; ++k) {
+        float pre = b0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {  // the events' du loads in flight together
-          const uint32_t bit = (nib >> k) & 1u;
-          dv[k] = buf_load<T>(rdu, bit ? e * (uint32_t)sizeof(T) : kBufOOB);
-          e += bit;
+        for (int j = 0; j < KM; ++j)
+          if (j < K) pre = fmaf(wk[j], xv[q][PRE + k - (K - 1) + j], pre);
+        float gv = dv[q][k];
+        if (SILU) {
+          const float sgm = 1.0f / (1.0f + __expf(-pre));
+          gv = dv[q][k] * sgm * (1.0f + pre * (1.0f - sgm));
         }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          float pre = b0;
-#pragma unroll
-          for (int j = 0; j < KM; ++j)
-            if (j < K) pre = fmaf(wk[j], xv[PRE + k - (K - 1) + j], pre);
-          float gv = dv[k];
-          if (SILU) {
-            const float sgm = 1.0f / (1.0f + __expf(-pre));
-            gv = dv[k] * sgm * (1.0f + pre * (1.0f - sgm));
-          }
-          g[k] = ((nib >> k) & 1u) ? gv : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-#pragma unroll
-          for (int j = 0; j < KM; ++j)
-            if (j < K) aw[j] = fmaf(g[k], xv[PRE + k - (K - 1) + j], aw[j]);
-          ab += g[k];
-        }
+        g[k] = ((nib[q] >> k) & 1u) ? gv : 0.0f;
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sg[lt + k] = g[k];
+      for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+          if (j < K) aw[j] = fmaf(g[k], xv[q][PRE + k - (K - 1) + j], aw[j]);
+        ab += g[k];
+        sg[lt + k] = g[k];
+      }
     }
     wave_sync();
 #pragma unroll

@@ -199,7 +199,7 @@ __device__ __forceinline__ T conv_at(const T* __restrict__ xr, int t, const floa
 #pragma unroll
   for (int k = 0; k < KM; ++k) {  // the taps' loads in flight together
     const int tt = t - (K - 1) + k;
-    xv[k] = (k < K && tt >= 0) ? to_f(ld_stream_elem(xr + tt)) : 0.0f;
+    xv[k] = (k < K && tt >= 0) ? to_f(xr[tt]) : 0.0f;  // cached: an event's taps share lines
   }
   float pre = b0;
 #pragma unroll
