@@ -83,6 +83,8 @@ SIGNATURES = {
     "bcm_scan_var_fwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p]),
     "bcm_scan_var_workspace_bytes": (c_i64, [c_i64, c_i32]),
     "bcm_scan_var_bwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p, c_i64, c_p]),
+    "bcm_spike_bits": (c_i32, [c_p, c_i32, c_i64, c_i64, c_i64, ctypes.c_float, c_p, c_p, c_p]),
+    "bcm_extract_count_bits": (c_i32, [c_p, c_i64, c_i64, c_p, c_p, c_p]),
     "bcm_extract_fill_blocks_conv": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_i64, c_i64, c_i64,
                                              c_p, c_p, c_i32, c_i32, c_p, c_p, c_p, c_p, c_p, c_p, c_p]),
     "bcm_causal_conv1d_bwd_events_workspace_bytes": (c_i64, [c_i64, c_i64, c_i32]),

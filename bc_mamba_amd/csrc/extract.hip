@@ -114,6 +114,73 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   if constexpr (BLK) block_totals(cnt, bsum, bmax);  // every wave, one barrier
 }
 
+// ------------------------------------------------- spikes straight to bits
+// The straight-through spike head (SpikeSamplerSurrogate mode "ste",
+// e_model.py:233-254: s = (p >= thr) + p - p, evaluated left to right) on
+// p [B, L, Dm], writing the event bitmask of the rows (b, d) directly: no
+// transposed copy of s and no count pass over it. One wave per (b, 64
+// channels, 64-step tile): lane d reads p[b, l, d] for the tile's 64 steps
+// (each a coalesced 256-byte row of the wave), packs the 64 bits of its row
+// into one mask word pair and, when s is requested, writes s in p's layout.
+// Bits past L stay 0; the padding words of a row are not written.
+template <typename T>
+__global__ __launch_bounds__(256) void k_spike_bits(const T* __restrict__ p, int64_t B, int64_t L, int64_t Dm,
+                                                    float thr, uint32_t* __restrict__ bitmask, int64_t W,
+                                                    T* __restrict__ s_out) {
+  const int lane = lane_id();
+  const int64_t nT = (L + kTile - 1) / kTile, nG = (Dm + kWave - 1) / kWave;
+  const int64_t gw = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (gw >= B * nG * nT) return;
+  const int64_t j = gw % nT, g = (gw / nT) % nG, b = gw / (nT * nG);
+  const int64_t d = g * kWave + lane;
+  if (d >= Dm) return;
+  const int64_t t0 = j * kTile;
+  const int n = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const T* pr = p + (b * L + t0) * Dm + d;
+  thr = to_f(from_f<T>(thr));  // torch compares in p's dtype
+  float v[kTile];
+#pragma unroll
+  for (int l = 0; l < kTile; ++l) v[l] = l < n ? to_f(pr[(int64_t)l * Dm]) : 0.0f;  // all 64 loads in flight
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int l = 0; l < kTile; ++l) {
+    const bool hit = l < n && v[l] >= thr;
+    if (l < 32) lo |= (uint32_t)hit << l;
+    else hi |= (uint32_t)hit << (l - 32);
+  }
+  *reinterpret_cast<uint2*>(bitmask + (b * Dm + d) * W + 2 * j) = make_uint2(lo, hi);
+  if (s_out) {
+    T* sr = s_out + (b * L + t0) * Dm + d;
+#pragma unroll
+    for (int l = 0; l < kTile; ++l) {
+      if (l < n) {
+        // the STE value rounded as torch rounds it: the hard spike in p's
+        // dtype, plus p, minus p
+        const float h = to_f(from_f<T>(v[l] >= thr ? 1.0f : 0.0f));
+        const float a = to_f(from_f<T>(h + v[l]));
+        sr[(int64_t)l * Dm] = from_f<T>(a - v[l]);
+      }
+    }
+  }
+}
+
+// Counts and block totals (as k_count with BLK) from a finished bitmask:
+// one wave per row.
+__global__ __launch_bounds__(256) void k_count_bits(const uint32_t* __restrict__ bitmask, int64_t n_rows, int64_t L,
+                                                    int64_t W, int32_t* __restrict__ counts,
+                                                    int32_t* __restrict__ bsum, int32_t* __restrict__ bmax) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  int cnt = 0;
+  if (row < n_rows) {
+    const int64_t nw = (L + 31) / 32;
+    for (int64_t w = lane; w < nw; w += kWave) cnt += __popc(bitmask[row * W + w]);
+    cnt = wave_sum(cnt);
+    if (lane == 0) counts[row] = cnt;
+  }
+  block_totals(cnt, bsum, bmax);
+}
+
 // ------------------------------------------------------------------- scan
 // One block: exclusive offsets of the per-row counts, total and maximum.
 // cu[0] = 0, cu[i+1] = counts[0] + ... + counts[i]; meta = (total, max).
@@ -716,6 +783,37 @@ int bcm_extract_fill_blocks_conv(const uint32_t* bitmask, const int32_t* counts,
       else go(std::false_type{}, K8{});
     }
   });
+  return check_launch(fn);
+}
+
+int bcm_spike_bits(const void* p, int dtype, int64_t B, int64_t L, int64_t Dm, float threshold, uint32_t* bitmask,
+                   void* s_out, bcm_stream_t stream) {
+  const char* fn = "bcm_spike_bits";
+  if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: p must be fp32, fp16 or bf16", fn);
+  if (B < 0 || L < 0 || Dm < 0) return set_error(BCM_EINVAL, "%s: negative size", fn);
+  if (B == 0 || L == 0 || Dm == 0) return BCM_OK;
+  if (!p || !bitmask) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (!aligned(bitmask, 8)) return set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  if (B * L * Dm > INT32_MAX) return set_error(BCM_EINVAL, "%s: B * L * Dm must fit in int32", fn);
+  const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (Dm + kWave - 1) / kWave;
+  const dim3 grid(blocks_for(B * nG * nT, 4)), block(256);
+  dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    hipLaunchKernelGGL((k_spike_bits<T>), grid, block, 0, hs(stream), static_cast<const T*>(p), B, L, Dm, threshold,
+                       bitmask, W, static_cast<T*>(s_out));
+  });
+  return check_launch(fn);
+}
+
+int bcm_extract_count_bits(const uint32_t* bitmask, int64_t n_rows, int64_t L, int32_t* counts, int32_t* block_sums,
+                           bcm_stream_t stream) {
+  const char* fn = "bcm_extract_count_bits";
+  if (n_rows < 1 || L < 1) return set_error(BCM_EINVAL, "%s: n_rows and L must be positive", fn);
+  if (!bitmask || !counts || !block_sums) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_rows * L > INT32_MAX) return set_error(BCM_EINVAL, "%s: n_rows * L must fit in int32", fn);
+  const int64_t nblk = (n_rows + 3) / 4;
+  hipLaunchKernelGGL(k_count_bits, dim3((unsigned)nblk), dim3(256), 0, hs(stream), bitmask, n_rows, L,
+                     bitmask_words(L), counts, block_sums, block_sums + nblk);
   return check_launch(fn);
 }
 

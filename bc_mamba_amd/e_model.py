@@ -244,16 +244,52 @@ class TwoLevelDelta(nn.Module):
         return F.softplus(self.a0) + self.eps, F.softplus(self.a1) + self.eps
 
 
+class _SpikeBitsFn(torch.autograd.Function):
+    """The "ste" spike s = (p >= thr) + p - p with its identity gradient, as
+    one kernel that also emits the event bitmask of the transposed spikes
+    (bcm_spike_bits). The bitmask rides on s as `_bcm_event_bits` =
+    (bitmask, threshold, s._version) for the next block's extraction."""
+
+    @staticmethod
+    def forward(ctx, p, threshold: float):
+        s, bitmask = _ee_cuda.spike_bits(p, threshold)
+        s._bcm_event_bits = (bitmask, threshold, s._version)
+        return s
+
+    @staticmethod
+    def backward(ctx, grad_s):
+        return grad_s, None
+
+
+def _event_bits_of(s, extract_threshold):
+    """The bitmask a spike tensor carries, if it still describes s and the
+    extraction's strict s > extract_threshold selects exactly the spikes:
+    s is exactly 0 without a spike and within 2^-6 of 1 with one (any
+    dtype), so any threshold in [0, 0.9) does."""
+    bits = getattr(s, "_bcm_event_bits", None)
+    if bits is None or bits[2] != s._version or not (0.0 <= extract_threshold < 0.9):
+        return None
+    return bits[0]
+
+
 class SpikeSamplerSurrogate(nn.Module):
     """Bernoulli / threshold spike sampler with a straight-through gradient
-    (e_model.py:233-254)."""
+    (e_model.py:233-254). With fused_bits (default) the "ste" mode on a
+    contiguous [B, L, D] CUDA tensor runs as one kernel that also emits the
+    event bitmask the next block's extraction reads (bcm_spike_bits): same
+    values and gradient."""
 
-    def __init__(self, mode: str = "ste", sample_inference: bool = False, threshold: float = 0.5):
+    def __init__(self, mode: str = "ste", sample_inference: bool = False, threshold: float = 0.5,
+                 fused_bits: bool = True):
         super().__init__()
         assert mode in ("prob", "ste")
         self.mode, self.sample_inference, self.threshold = mode, sample_inference, threshold
+        self.fused_bits = fused_bits
 
     def forward(self, p):
+        if (self.mode == "ste" and self.fused_bits and p.is_cuda and p.dim() == 3 and p.is_contiguous()
+                and p.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            return _SpikeBitsFn.apply(p, float(self.threshold))
         if self.mode == "prob":
             if self.training:
                 s = torch.bernoulli(p)
@@ -371,12 +407,17 @@ class Mamba(nn.Module):
         n_ch = batch * self.d_inner
 
         if self.fused_event_path:
-            base_input = rearrange(hidden_states.detach(), "b l d -> b d l").contiguous()
+            # spikes from a fused STE head carry their event bitmask: no
+            # transposed copy of the membrane and no count pass over it
+            bits = _event_bits_of(hidden_states, self.threshold)
+            base_input = None if bits is not None else \
+                rearrange(hidden_states.detach(), "b l d -> b d l").contiguous()
             w_conv, b_conv = self.conv1d.weight[:, 0, :], self.conv1d.bias
             with cuda_stage("routing_index_extraction"):
                 _ch, time_steps, k_flat, cu_seqlens, max_seqlen, x_ev, event_index = \
                     _ee_cuda.extract_events_indexed(base_input, self.threshold, self.expand, x.detach(),
-                                                    positions=False, conv=(w_conv, b_conv, True) if conv_ev else None)
+                                                    positions=False, conv=(w_conv, b_conv, True) if conv_ev else None,
+                                                    bits=(bits, (batch, dim, seqlen)) if bits is not None else None)
             with cuda_stage("sparse_scan_forward"):
                 if conv_ev:  # x is the conv input: silu(conv(x)) exists only at the events
                     y_flat = _IndexedConvScanFn.apply(x, w_conv, b_conv, (x_ev,), event_index, k_flat, cu_seqlens,

@@ -193,7 +193,25 @@ def _extract_indexed_exact(base_input, threshold, expand, x, positions):
         return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)
 
 
-def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True, exact_alloc=False, conv=None):
+def spike_bits(p, threshold, want_s=True):
+    """The straight-through spike head (SpikeSamplerSurrogate mode "ste",
+    e_model.py:233-254) on p [B, L, Dm] as one kernel (bcm_spike_bits):
+    returns (s, bitmask) with s = (p >= threshold) + p - p (None unless
+    want_s) and the event bitmask [B*Dm, words] of the transposed spikes,
+    ready for extract_events_indexed(bits=...)."""
+    _check(p.is_cuda and p.is_contiguous() and p.dim() == 3, "p must be a contiguous 3-D CUDA tensor [B, L, Dm]")
+    _check(p.dtype in (torch.float32, torch.float16, torch.bfloat16), "p must be fp32, fp16 or bf16")
+    B, L, Dm = p.shape
+    bitmask = torch.empty((B * Dm, _nat.bitmask_words(L)), dtype=_I32, device=p.device)
+    s = torch.empty_like(p) if want_s else None
+    with torch.cuda.device(p.device):
+        _nat.call("bcm_spike_bits", _nat.ptr(p), _nat.dtype_code(p.dtype), B, L, Dm, float(threshold),
+                  _nat.ptr(bitmask), _nat.ptr(s), _nat.stream_of(p))
+    return s, bitmask
+
+
+def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=True, exact_alloc=False, conv=None,
+                           bits=None):
     """Fused extraction for the block forward (no reference counterpart; the
     reference composes extract_base_events + expand_base_events +
     gather_events_fwd). Returns (channel_ids, time_steps, k_flat, cu_seqlens,
@@ -213,12 +231,23 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
     the block's depthwise causal conv (rows contiguous, any batch / channel
     strides, e.g. the in_proj GEMM output viewed as [B, D, L]) and x_events
     is silu(conv(x)) evaluated at the events only, the values the dense
-    conv followed by the gather would give (bcm_extract_fill_blocks_conv)."""
-    _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
-           "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
-    B, Dm, L = base_input.shape
+    conv followed by the gather would give (bcm_extract_fill_blocks_conv).
+
+    bits = (bitmask, (B, d_model, L)): the rows' event bitmask is already
+    built (spike_bits, the bits of base_input > threshold); base_input is
+    then not read and may be None, and the count pass only counts bits."""
+    if bits is not None:
+        bits_mask, (B, Dm, L) = bits
+        _check(bits_mask.is_cuda and bits_mask.dtype == _I32 and bits_mask.is_contiguous()
+               and tuple(bits_mask.shape) == (B * Dm, _nat.bitmask_words(L)), "bits must be [B*d_model, words] int32")
+        _check(not exact_alloc and B * Dm > 0 and L > 0, "bits need the fused fill and a non-empty batch")
+        dev = bits_mask.device
+    else:
+        _check(base_input.is_cuda and base_input.is_contiguous() and base_input.dim() == 3,
+               "base_input must be a contiguous 3-D CUDA tensor [B, d_model, L]")
+        B, Dm, L = base_input.shape
+        dev = base_input.device
     expand = int(expand)
-    dev = base_input.device
     NC = B * Dm
     if conv is not None:
         _check(x is not None and x.is_cuda and x.dim() == 3 and tuple(x.shape) == (B, Dm * expand, L)
@@ -233,10 +262,9 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
     if exact_alloc or NC == 0 or L == 0:
         return _extract_indexed_exact(base_input, threshold, expand, x, positions)
     with torch.cuda.device(dev):
-        x2d = base_input.view(NC, L)
-        s = _nat.stream_of(x2d)
+        s = _nat.stream_of(bits[0] if bits is not None else base_input)
         NCi, cap = NC * expand, NC * expand * L
-        bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
+        bitmask = bits[0] if bits is not None else torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
         counts = _empty_i32(NC, dev)
         bsums = _empty_i32(_nat.lib().bcm_extract_block_sums_bytes(NC) // 4, dev)
         cu = _empty_i32(NCi + 1, dev)
@@ -246,8 +274,11 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
         xe = torch.empty(cap, dtype=x.dtype, device=dev) if x is not None else None
         meta = _nat.HostMeta()
         meta.arm()
-        _nat.call("bcm_extract_count_blocks", _nat.ptr(x2d), _nat.dtype_code(base_input.dtype), NC, L,
-                  float(threshold), _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), s)
+        if bits is not None:
+            _nat.call("bcm_extract_count_bits", _nat.ptr(bitmask), NC, L, _nat.ptr(counts), _nat.ptr(bsums), s)
+        else:
+            _nat.call("bcm_extract_count_blocks", _nat.ptr(base_input), _nat.dtype_code(base_input.dtype), NC, L,
+                      float(threshold), _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), s)
         if conv is None:
             _nat.call("bcm_extract_fill_blocks", _nat.ptr(bitmask), _nat.ptr(counts), _nat.ptr(bsums), meta.ptr(),
                       NC, L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype) if x is not None else 0, _nat.ptr(cu),

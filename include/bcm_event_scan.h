@@ -121,6 +121,22 @@ int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts,
                             int32_t* k_flat, void* x_events,
                             int32_t* tile_start, bcm_stream_t stream);
 
+/* The straight-through spike head that produces the next block's membrane
+ * (SpikeSamplerSurrogate mode "ste", e_model.py:233-254, lra_impl.py:1398;
+ * p = sigmoid(prob_head(...)) [B, L, Dm]) emitting the event bitmask
+ * directly: bitmask row b * Dm + d gets bit t set where p[b, t, d] >= threshold
+ * (the rows of bcm_extract_count over the transposed spikes, whose strict
+ * "> thr_extract" with 0 <= thr_extract < 1 selects exactly these steps).
+ * With s_out != NULL also writes the spike value s = (p >= threshold) + p - p
+ * in p's dtype and layout, rounded as torch evaluates it. The padding words
+ * of each bitmask row are not written. */
+int bcm_spike_bits(const void* p, int dtype, int64_t B, int64_t L, int64_t Dm, float threshold,
+                   uint32_t* bitmask, void* s_out, bcm_stream_t stream);
+/* counts and block_sums of bcm_extract_count_blocks from a finished bitmask
+ * (bcm_spike_bits), for bcm_extract_fill_blocks(_conv). */
+int bcm_extract_count_bits(const uint32_t* bitmask, int64_t n_rows, int64_t L, int32_t* counts,
+                           int32_t* block_sums, bcm_stream_t stream);
+
 /* bcm_extract_fill_blocks with the depthwise causal conv + SiLU of the
  * model block (e_model.py:442-451) evaluated at the events instead of
  * gathered from a dense x_conv (the conv producer fused with the gather,
