@@ -125,23 +125,24 @@ class _IndexedGatherFn(torch.autograd.Function):
 
 
 def _event_scan_fwd(ctx, x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D):
-    """Depthwise flat scan forward of the fused block; keeps what the
-    backward (_event_scan_bwd) reads in ctx."""
+    """Depthwise flat scan forward of the fused block. Returns (out, the
+    tensors the backward reads), for ctx.save_for_backward."""
     dt_idle, dt_active = dt_idle.contiguous(), dt_active.contiguous()
     A, W_B, W_C = A.contiguous(), W_B.contiguous(), W_C.contiguous()
     chunk_g = selective_scan_cuda.chunk_states_buffer(x_ev, cu_seqlens, max_seqlen, A)
     out, xs = selective_scan_cuda.fwd_flat_ch(x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D,
                                               None, is_depthwise_bc=True, _chunk_g=chunk_g)
-    ctx.scan = (x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs, D)
-    ctx.chunk_g, ctx.max_seqlen = chunk_g, max_seqlen
-    return out
+    ctx.chunk_g, ctx.max_seqlen, ctx.has_D = chunk_g, max_seqlen, D is not None
+    return out, [x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs] + ([D] if D is not None else [])
 
 
-def _event_scan_bwd(ctx, dout, rows=None):
-    """(du, dt_idle, dt_active, dA, dW_B, dW_C, dD) of the fused block's scan;
-    with rows = (bitmask, expand, tile_start, dx) the scan kernel also
-    writes the dense gather backward into dx."""
-    x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs, D = ctx.scan
+def _event_scan_bwd(ctx, saved, dout, rows=None):
+    """(du, dt_idle, dt_active, dA, dW_B, dW_C, dD) of the fused block's scan
+    from the tensors _event_scan_fwd saved; with rows = (bitmask, expand,
+    tile_start, dx) the scan kernel also writes the dense gather backward
+    into dx."""
+    x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs = saved[:9]
+    D = saved[9] if ctx.has_D else None
     res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, W_B, W_C,
                                           dout.contiguous(), xs, D, is_depthwise_bc=True, _chunk_g=ctx.chunk_g,
                                           _rows=rows)
@@ -161,17 +162,20 @@ class _IndexedScanFn(torch.autograd.Function):
                 W_C, D):
         # payload = (x_events,): kept out of the autograd inputs on purpose
         ctx.event_index, ctx.shape = event_index, x_conv.shape
-        return _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D)
+        out, saved = _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B,
+                                     W_C, D)
+        ctx.save_for_backward(*saved)
+        return out
 
     @staticmethod
     def backward(ctx, dout):
         B, Dm, L = ctx.shape
         bitmask, tile_start, expand = ctx.event_index
-        x_ev = ctx.scan[0]
+        saved = ctx.saved_tensors
+        x_ev = saved[0]
         dx = torch.empty((B * Dm, L), dtype=x_ev.dtype, device=x_ev.device)
         with cuda_stage("sparse_scan_backward"):
-            _du, *grads = _event_scan_bwd(ctx, dout, rows=(bitmask, expand, tile_start, dx))
-        ctx.scan = None
+            _du, *grads = _event_scan_bwd(ctx, saved, dout, rows=(bitmask, expand, tile_start, dx))
         return (dx.view(B, Dm, L), None, None, None, None, None, *grads)
 
 
@@ -187,17 +191,22 @@ class _IndexedConvScanFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias, payload, event_index, k_flat, cu_seqlens, max_seqlen: int, dt_idle, dt_active,
                 A, W_B, W_C, D):
-        ctx.event_index, ctx.conv = event_index, (x, weight, bias)
-        return _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D)
+        ctx.event_index, ctx.has_bias = event_index, bias is not None
+        out, saved = _event_scan_fwd(ctx, payload[0], k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B,
+                                     W_C, D)
+        ctx.n_scan = len(saved)
+        ctx.save_for_backward(*saved, x, weight, *([bias] if bias is not None else []))
+        return out
 
     @staticmethod
     def backward(ctx, dout):
-        x, weight, bias = ctx.conv
+        saved = ctx.saved_tensors
+        x, weight = saved[ctx.n_scan], saved[ctx.n_scan + 1]
+        bias = saved[ctx.n_scan + 2] if ctx.has_bias else None
         with cuda_stage("sparse_scan_backward"):
-            du, *grads = _event_scan_bwd(ctx, dout)
+            du, *grads = _event_scan_bwd(ctx, saved[:ctx.n_scan], dout)
         with cuda_stage("conv_backward"):
             dx, dw, db = conv1d_bwd_events(x, weight, bias, True, du, ctx.event_index)
-        ctx.scan = ctx.conv = None
         return (dx, dw.to(weight.dtype), db.to(bias.dtype) if db is not None else None, None, None, None, None, None,
                 *grads)
 

@@ -108,3 +108,38 @@ def test_interface_exports_reference_names():
     assert issubclass(ssi.SelectiveScanFlatChFn, torch.autograd.Function)
     with pytest.raises(RuntimeError, match="not part of"):
         ssi.selective_scan_depthwise_bc_fn()
+
+
+def test_spike_bits_and_bits_extraction_checks(fake_cuda):
+    with pytest.raises(RuntimeError, match="p must be a contiguous 3-D CUDA tensor"):
+        ee.spike_bits(torch.rand(4, 8), 0.5)
+    with pytest.raises(RuntimeError, match="p must be fp32, fp16 or bf16"):
+        ee.spike_bits(torch.rand(2, 4, 8, dtype=torch.float64), 0.5)
+    bad = torch.zeros((3, 32), dtype=i32)  # rows of 2 x 2 channels need 4
+    with pytest.raises(RuntimeError, match="bits must be"):
+        ee.extract_events_indexed(None, 0.5, 1, None, bits=(bad, (2, 2, 64)))
+    ok = torch.zeros((4, 32), dtype=i32)
+    with pytest.raises(RuntimeError, match="bits need the fused fill"):
+        ee.extract_events_indexed(None, 0.5, 1, None, exact_alloc=True, bits=(ok, (2, 2, 64)))
+
+
+def test_conv_at_events_checks(fake_cuda):
+    mem = torch.zeros(2, 2, 64)
+    x = torch.zeros(2, 4, 64)[:, :, :63]  # 63 steps where the membrane has 64
+    w = torch.zeros(4, 4)
+    with pytest.raises(RuntimeError, match="x must be a CUDA tensor"):
+        ee.extract_events_indexed(mem, 0.5, 2, x, conv=(w, None, True))
+    x = torch.zeros(2, 4, 64)
+    with pytest.raises(RuntimeError, match="conv needs the fused fill"):
+        ee.extract_events_indexed(mem, 0.5, 2, x, exact_alloc=True, conv=(w, None, True))
+
+
+def test_spike_sampler_uses_torch_off_the_gpu():
+    """The fused STE head runs only on CUDA tensors; elsewhere the sampler
+    computes the reference expression (same values, same gradient)."""
+    from bc_mamba_amd.e_model import SpikeSamplerSurrogate
+    p = torch.rand(2, 5, 3, requires_grad=True)
+    s = SpikeSamplerSurrogate(mode="ste", threshold=0.4)(p)
+    assert torch.equal(s, (p >= 0.4).float() + p - p) and not hasattr(s, "_bcm_event_bits")
+    s.sum().backward()
+    assert torch.equal(p.grad, torch.ones_like(p))
