@@ -11,7 +11,9 @@ fused entry points: one extraction pass that also gathers x_conv at the
 events and builds the event index, the restore reads that index instead of
 rebuilding it, the scan backward writes the dense x_conv gradient rows from
 the same index (no separate gather backward), and the per-block host syncs
-drop from two to one. With `conv_at_events=True` (default) the depthwise
+drop from two to one. The fused path's token projections (in_proj, out_proj,
+prob_head) take their weight gradients as split-K products
+(`projections`). With `conv_at_events=True` (default) the depthwise
 conv + SiLU is evaluated only at the events, by the extraction itself, and
 its backward goes from du straight to the conv input's gradient: no dense
 x_conv exists in either direction. Results match the unfused composition
@@ -32,6 +34,7 @@ try:
     from . import _native as _nat
     from . import extract_events_cuda as _ee_cuda
     from . import restore_dense_cuda_nodecay
+    from . import projections
     from . import selective_scan_cuda
     from .causal_conv1d import causal_conv1d_fn, conv1d_bwd_events
     from .runtime_breakdown import cuda_stage
@@ -40,6 +43,7 @@ except ImportError:  # imported with this directory on sys.path
     import _native as _nat
     import extract_events_cuda as _ee_cuda
     import restore_dense_cuda_nodecay
+    import projections
     import selective_scan_cuda
     from causal_conv1d import causal_conv1d_fn, conv1d_bwd_events
     from runtime_breakdown import cuda_stage
@@ -357,7 +361,8 @@ class Mamba(nn.Module):
                                        device=device)
 
     def to_spike(self, out):
-        logits = self.prob_head(out)
+        logits = projections.linear(out, self.prob_head.weight, self.prob_head.bias) if self.fused_event_path \
+            else self.prob_head(out)
         p = torch.sigmoid(logits) if self.prob_activation == "sigmoid" else torch.clamp(logits, 0.0, 1.0)
         return self.spike_sampler(p)
 
@@ -401,8 +406,11 @@ class Mamba(nn.Module):
         if inference_params is not None:
             raise RuntimeError("Mamba: the decode / inference-cache path is not part of the event-path build")
         batch, seqlen, dim = hidden_states.shape
-        x = rearrange(self.in_proj.weight @ rearrange(hidden_states, "b l d -> d (b l)"), "d (b l) -> b d l",
-                      l=seqlen)
+        if self.fused_event_path:  # the same product, with the split-K weight gradient
+            xw = projections.proj_tokens_last(self.in_proj.weight, hidden_states.reshape(batch * seqlen, dim))
+        else:
+            xw = self.in_proj.weight @ rearrange(hidden_states, "b l d -> d (b l)")
+        x = rearrange(xw, "d (b l) -> b d l", l=seqlen)
         if self.in_proj.bias is not None:
             x = x + rearrange(self.in_proj.bias.to(dtype=x.dtype), "d -> d 1")
         conv_ev = self._conv_at_events_ok(x)
@@ -447,4 +455,6 @@ class Mamba(nn.Module):
                 y_dense = _IndexedRestoreFn.apply(y_flat, event_index, n_ch, self.d_inner, seqlen)
             else:
                 y_dense = restore_dense_fn(y_flat, time_steps.to(torch.int32), cu_seqlens, self.d_inner, seqlen)
+        if self.fused_event_path:
+            return projections.linear(y_dense, self.out_proj.weight, self.out_proj.bias)
         return self.out_proj(y_dense)

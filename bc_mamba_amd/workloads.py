@@ -150,8 +150,9 @@ class SpikeMambaNet(torch.nn.Module):
         self.head = torch.nn.Linear(d_model, num_classes)
 
     def forward(self, tokens):
+        from . import projections
         v = self.inp(tokens.long())
-        s = self.in_spike(torch.sigmoid(self.in_prob(v)))
+        s = self.in_spike(torch.sigmoid(projections.linear(v, self.in_prob.weight, self.in_prob.bias)))
         for blk in self.blocks:
             s, v = blk(s, v)
         return self.head(self.norm(s).mean(dim=1))
