@@ -503,6 +503,13 @@ int bcm_causal_conv1d_bwd_events(const void* x, int dtype, int64_t x_batch_strid
                           fn);
   if ((reinterpret_cast<uintptr_t>(bitmask) & 7) != 0)
     return bcm::set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
+  {  // dx is written through the same strides: rows must not overlap
+    const bool dim_inner = x_dim_stride <= x_batch_stride;
+    const int64_t s_in = dim_inner ? x_dim_stride : x_batch_stride, n_in = dim_inner ? D : B;
+    const int64_t s_out = dim_inner ? x_batch_stride : x_dim_stride, n_out = dim_inner ? B : D;
+    if ((n_in > 1 && s_in < L) || (n_out > 1 && s_out < s_in * n_in))
+      return bcm::set_error(BCM_EINVAL, "%s: the row strides make rows overlap", fn);
+  }
   const int64_t rows = B * D;
   if (!workspace || workspace_bytes < 4 * rows * (K + 1))
     return bcm::set_error(BCM_EINVAL, "%s: workspace needs %lld bytes", fn, (long long)(4 * rows * (K + 1)));

@@ -398,8 +398,10 @@ class Mamba(nn.Module):
         """The fused path evaluates the conv at the events when x's rows are
         contiguous and 4-step aligned (bcm_causal_conv1d_bwd_events)."""
         es = x.element_size()
+        (s_in, n_in), (s_out, _) = sorted(((x.stride(1), x.size(1)), (x.stride(0), x.size(0))))
+        rows_apart = s_in >= x.size(2) and s_out >= s_in * n_in  # dx reuses x's strides
         return (self.fused_event_path and self.conv_at_events and x.stride(2) == 1 and x.size(2) % 4 == 0
-                and x.stride(0) % 4 == 0 and x.stride(1) % 4 == 0 and x.data_ptr() % (4 * es) == 0
+                and x.stride(0) % 4 == 0 and x.stride(1) % 4 == 0 and x.data_ptr() % (4 * es) == 0 and rows_apart
                 and self.d_conv <= 8 and x.dtype in (torch.float32, torch.float16, torch.bfloat16))
 
     def forward(self, hidden_states, inference_params=None):

@@ -127,3 +127,16 @@ def test_scan_chunk_states_size_is_checked(lib):
     assert needs and n_pass > 1
     a.chunk_g, a.chunk_g_bytes = 16, 4 * 8 * n_pass * 16 - 4
     assert lib.bcm_scan_fwd(a, None) == 1 and "chunk_g needs" in lib.bcm_last_error().decode()
+
+
+def test_conv_events_backward_rejects_overlapping_rows(lib):
+    """dx is written with x's row strides: strides whose rows overlap (a
+    broadcast batch, rows closer than L) are refused before any launch."""
+    ws = 4 * 2 * 4 * 5  # B=2, D=4, L=64, K=4: pointers are never dereferenced
+
+    def call(sb, sd):
+        return lib.bcm_causal_conv1d_bwd_events(16, 0, sb, sd, 2, 4, 64, 16, None, 4, 1, 16, 10, 16, 1, 16, 16, 16,
+                                                None, 16, ws, None)
+    assert call(0, 64) == 1 and "overlap" in lib.bcm_last_error().decode()     # broadcast batch
+    assert call(256, 32) == 1 and "overlap" in lib.bcm_last_error().decode()   # rows 32 apart, L = 64
+    assert call(64, 64) == 1 and "overlap" in lib.bcm_last_error().decode()
