@@ -25,6 +25,7 @@ CASES = [  # B, D, L, density, N, dtype, with_z, p_short  (one kernel unless not
     (2, 8, 230, 0.5, 16, torch.float32, False, None),    # L % 4 != 0: two steps
     (2, 8, 448, 0.5, 16, torch.float32, True, None),     # z: two steps
     (2, 8, 1200, 0.6, 16, torch.float32, False, 0.02),   # multi-pass channels: two steps
+    (96, 2, 300, 0.5, 16, torch.float32, False, None),   # 96 channels per model channel: split workgroups
 ]
 
 
