@@ -29,6 +29,10 @@ How each function is pinned (tests/test_oracle.py):
   pw_grads             and in W
   conv1d_fwd / _bwd    torch.nn.functional.conv1d (groups = D, padding K-1,
                        the reference's own fallback) and float64 autograd
+  conv_at_events /     equal to the dense conv1d_fwd read at the events, and
+  conv_bwd_events      to float64 autograd through a gather of the dense conv
+  spike_ste            torch's (p >= thr).float() + p - p bit for bit, bits
+                       equal to the dense s > 0.5 of the transposed spikes
 """
 import math
 
@@ -449,6 +453,48 @@ def conv1d_bwd(x, w, bias, dout, silu=True):
         dx += w[None, :, k, None] * gp[:, :, K - 1 - k:K - 1 - k + L]
         dw[:, k] = (g * xp[:, :, k:k + L]).sum(axis=(0, 2))
     return dx, dw, g.sum(axis=(0, 2))
+
+
+def conv_at_events(x, w, bias, ch, t, silu=True):
+    """The conv + SiLU evaluated only at the events (ch, t) of the flat
+    channels x [NC, L] (channel ch uses w[ch % D]): x_events[e] =
+    act(bias + Σ_k w[k] x[ch, t-(K-1)+k]), e_model.py:442-451 followed by
+    the gather of :403-406."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    D, K = w.shape
+    ch = np.asarray(ch, np.int64)
+    t = np.asarray(t, np.int64)
+    d = ch % D
+    pre = np.asarray(bias, np.float64)[d] if bias is not None else np.zeros(len(ch))
+    for k in range(K):
+        tt = t - (K - 1) + k
+        pre = pre + w[d, k] * np.where(tt >= 0, x[ch, np.maximum(tt, 0)], 0.0)
+    return pre / (1.0 + np.exp(-pre)) if silu else pre
+
+
+def conv_bwd_events(x, w, bias, du, ch, t, silu=True):
+    """Backward of conv_at_events from du [E]: the gather backward (du at
+    the events, 0 elsewhere) followed by conv1d_bwd over the rows of x
+    [B, D, L]. Returns (dx [B, D, L], dw [D, K], dbias [D])."""
+    x = np.asarray(x, np.float64)
+    B, D, L = x.shape
+    dense = gather_bwd(np.asarray(du, np.float64), ch, t, B * D, L).reshape(B, D, L)
+    return conv1d_bwd(x, w, bias, dense, silu)
+
+
+# -------------------------------------------------------------- spike head
+def spike_ste(p, threshold):
+    """SpikeSamplerSurrogate mode "ste" (e_model.py:233-254) on p [B, L, Dm]:
+    (s, bits) with s = (p >= thr) + p - p evaluated left to right in
+    float32 (the reference's dtype), and bits [B*Dm, L] bool the spikes of
+    the transposed rows (b, d), the membrane the next block extracts."""
+    p = np.asarray(p, np.float32)
+    thr = np.float32(threshold)
+    hard = (p >= thr).astype(np.float32)
+    s = (hard + p) - p
+    B, L, Dm = p.shape
+    return s, (p >= thr).transpose(0, 2, 1).reshape(B * Dm, L)
 
 
 # ------------------------------------------------------------------ restore

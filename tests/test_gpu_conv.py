@@ -114,6 +114,13 @@ def test_conv_at_events_matches_dense_conv_then_gather(cuda_device, B, Dm, expan
     nw = (L + 31) // 32  # bitmask rows are padded to 1024 steps; the padding words are not written
     assert torch.equal(idx[0][:, :nw], idx2[0][:, :nw]) and torch.equal(idx[1], idx2[1])
     assert xe.dtype == dtype and torch.equal(xe, xe_ref)
+    # and against the CPU oracle: conv + SiLU evaluated at the oracle's events
+    rtol, atol = (1e-4, 1e-5) if dtype == torch.float32 else (2e-2, 2e-3)
+    och, ot, ok_, ocu, _, _ = orc.extract_base_events(mem.cpu().numpy(), 0.5)
+    och, ot = orc.expand_base_events(och, ot, ok_, ocu, B, Dm, expand)[:2]
+    xf = x.float().contiguous().cpu().numpy().reshape(B * D, L)
+    assert_close(xe.float().cpu(), orc.conv_at_events(xf, w.cpu().numpy(), b.cpu().numpy() if bias else None,
+                                                      och, ot, silu), rtol, atol, "x_events vs oracle")
     # backward: du at the events -> dense dx_conv -> dense conv backward
     du = torch.randn(xe.numel(), generator=g).to(dtype).to(dev)
     dxc = torch.empty(B * D, L, dtype=dtype, device=dev)
@@ -130,3 +137,9 @@ def test_conv_at_events_matches_dense_conv_then_gather(cuda_device, B, Dm, expan
     assert_close(dw.cpu(), wr.grad.cpu().numpy(), 1e-5, 1e-6, "dweight")
     if bias:
         assert_close(db.cpu(), br.grad.cpu().numpy(), 1e-5, 1e-6, "dbias")
+    odx, odw, odb = orc.conv_bwd_events(xf.reshape(B, D, L), w.cpu().numpy(), b.cpu().numpy() if bias else None,
+                                        du.float().cpu().numpy(), och, ot, silu)
+    assert_close(dx.float().contiguous().cpu(), odx, rtol, atol, "dx vs oracle")
+    assert_close(dw.cpu(), odw, rtol, atol, "dweight vs oracle")
+    if bias:
+        assert_close(db.cpu(), odb, rtol, atol, "dbias vs oracle")

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from bc_mamba_amd import extract_events_cuda as ee
+from oracle import event_path as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -32,6 +33,9 @@ def test_spike_bits_match_ste_and_mask(cuda_device, B, L, Dm, thr, dtype):
     words = bitmask[:, :nw].cpu().numpy().view(np.uint32)
     bits = np.unpackbits(words.view(np.uint8), bitorder="little").reshape(B * Dm, nw * 32)[:, :L]
     assert np.array_equal(bits.astype(bool), hard)
+    if dtype == torch.float32:  # the CPU oracle of the spike head
+        os_, obits = orc.spike_ste(p.cpu().numpy(), thr)
+        assert np.array_equal(s.cpu().numpy(), os_) and np.array_equal(bits.astype(bool), obits)
 
 
 @pytest.mark.parametrize("expand", [1, 2])

@@ -401,3 +401,50 @@ def test_torch_path_extract_matches_oracle():
     tch, tt, tk, tcu, _ = tp.extract(torch.from_numpy(mem), 0.5)
     for a, b in ((ch, tch), (t, tt), (k, tk), (cu, tcu)):
         assert np.array_equal(a, b.numpy())
+
+
+# ------------------------------------------- conv at the events, spike head
+def test_conv_at_events_is_the_dense_conv_read_at_the_events():
+    rng = np.random.default_rng(4)
+    B, D, L, K = 2, 3, 40, 4
+    x = rng.standard_normal((B, D, L))
+    w = rng.standard_normal((D, K))
+    b = rng.standard_normal(D)
+    mask = rng.random((B * D, L)) < 0.3
+    ch, t = np.nonzero(mask)
+    for silu in (True, False):
+        dense = orc.conv1d_fwd(x, w, b, silu).reshape(B * D, L)
+        got = orc.conv_at_events(x.reshape(B * D, L), w, b, ch, t, silu)
+        assert_close(got, dense[ch, t], rtol=1e-13, atol_rel=1e-14, name="x_events")
+
+
+def test_conv_bwd_events_matches_autograd_through_the_gather():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    B, D, L, K = 2, 3, 30, 3
+    x = rng.standard_normal((B, D, L))
+    w = rng.standard_normal((D, K))
+    b = rng.standard_normal(D)
+    mask = rng.random((B * D, L)) < 0.3
+    ch, t = np.nonzero(mask)
+    du = rng.standard_normal(len(ch))
+    xt = torch.tensor(x, requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    y = torch.nn.functional.silu(torch.nn.functional.conv1d(xt, wt[:, None, :], bt, padding=K - 1, groups=D)[..., :L])
+    y.reshape(B * D, L)[torch.tensor(ch), torch.tensor(t)].mul(torch.tensor(du)).sum().backward()
+    dx, dw, db = orc.conv_bwd_events(x, w, b, du, ch, t)
+    assert_close(dx, xt.grad.numpy(), rtol=1e-12, atol_rel=1e-13, name="dx")
+    assert_close(dw, wt.grad.numpy(), rtol=1e-12, atol_rel=1e-13, name="dw")
+    assert_close(db, bt.grad.numpy(), rtol=1e-12, atol_rel=1e-13, name="db")
+
+
+def test_spike_ste_matches_torch_and_the_dense_extraction():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(6)
+    p = rng.random((2, 50, 7)).astype(np.float32)
+    s, bits = orc.spike_ste(p, 0.3)
+    pt = torch.tensor(p)
+    assert np.array_equal(s, ((pt >= 0.3).float() + pt - pt).numpy())
+    mem = s.transpose(0, 2, 1).reshape(14, 50)
+    assert np.array_equal(bits, mem > 0.5)
