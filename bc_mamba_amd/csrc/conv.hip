@@ -199,7 +199,14 @@ __global__ __launch_bounds__(256) void k_conv_bwd_reduce(const float* __restrict
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)D * (K + 1)) return;
   float v = 0.0f;
-  for (int p = 0; p < P; ++p) v += part[(int64_t)p * D * (K + 1) + i];
+  for (int p0 = 0; p0 < P; p0 += 8) {  // 8 loads in flight, summed in group order
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = p0 + j < P ? part[(int64_t)(p0 + j) * D * (K + 1) + i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (p0 + j < P) v += q[j];
+  }
   const int d = (int)(i / (K + 1)), k = (int)(i % (K + 1));
   if (k < K) dw[(int64_t)d * K + k] = v;
   else if (dbias) dbias[d] = v;
@@ -367,7 +374,16 @@ __global__ __launch_bounds__(256) void k_conv_bwd_events_reduce(const float* __r
   if (i >= (int64_t)dim * (K + 1)) return;
   const int d = (int)(i / (K + 1)), k = (int)(i % (K + 1));
   float v = 0.0f;
-  for (int64_t bb = 0; bb < nb; ++bb) v += part[(bb * dim + d) * (K + 1) + k];
+  const int64_t stride = (int64_t)dim * (K + 1);
+  const float* pr = part + (int64_t)d * (K + 1) + k;
+  for (int64_t b0 = 0; b0 < nb; b0 += 8) {  // 8 loads in flight, summed in row order
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = b0 + j < nb ? pr[(b0 + j) * stride] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (b0 + j < nb) v += q[j];
+  }
   if (k < K) dw[(int64_t)d * K + k] = v;
   else if (dbias) dbias[d] = v;
 }

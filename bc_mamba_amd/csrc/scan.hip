@@ -862,7 +862,14 @@ __global__ __launch_bounds__(256) void k_scan_param_reduce(const bcm_scan_args a
   if (t >= (int64_t)a.dim * NA) return;
   const int d = (int)(t / NA), i = (int)(t % NA);
   float v = 0.0f;
-  for (int sp = 0; sp < S; ++sp) v += a.split_ws[((int64_t)sp * a.dim + d) * NA + i];
+  for (int s0 = 0; s0 < S; s0 += 8) {  // 8 loads in flight, summed in split order
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = s0 + j < S ? a.split_ws[((int64_t)(s0 + j) * a.dim + d) * NA + i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (s0 + j < S) v += q[j];
+  }
   store_param_grad(a, d, N, i, v);
 }
 
