@@ -385,9 +385,12 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
       st[pos++] = (int)(32 * w + b);
     }
     wave_sync();
-    // write-out in batches of 8 events per lane (a row's ~300 events in one
-    // batch at 15 % density): the gathers of a batch are in flight together
-    // and the index stores never wait on them
+    // write-out in batches of FB events per lane: the gathers of a batch are
+    // in flight together and the index stores never wait on them. 8 for the
+    // plain gather (a row's ~300 events in one batch at 15 % density: 22.9 ->
+    // 21.0 us at config 1); 4 for the conv form, whose 4 taps per event
+    // already fill the queue (8 there: 39 -> 48 us at config 4)
+    constexpr int FB = KM > 0 ? 4 : 8;
     for (int r = 0; r < expand; ++r) {
       const int64_t lc = c * expand + r;
       const int64_t obase = (int64_t)cu0 * expand + (int64_t)r * n + off;
@@ -403,18 +406,18 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
         b0 = cv.bias ? cv.bias[dch] : 0.0f;
         xr = x + (lc / cv.dim) * cv.sb + (int64_t)dch * cv.sd;
       }
-      for (int i0 = 0; i0 < seg_cnt; i0 += 8 * kWave) {
-        int tv[8];
-        T xv[8];
+      for (int i0 = 0; i0 < seg_cnt; i0 += FB * kWave) {
+        int tv[FB];
+        T xv[FB];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < FB; ++q) {
           const int i = i0 + q * kWave + lane;
           tv[q] = i < seg_cnt ? st[i] : 0;
           if constexpr (KM > 0) xv[q] = conv_at<T, KM>(xr, tv[q], wk, b0, KM == 4 ? 4 : cv.K, cv.silu != 0);
           else if (GATHER) xv[q] = ld_stream_elem(xr + tv[q]);
         }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < FB; ++q) {
           const int i = i0 + q * kWave + lane;
           if (i < seg_cnt) {
             const int tp = i > 0 ? st[i - 1] : prev_t;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
         }
         if (GATHER) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
+          for (int q = 0; q < FB; ++q) {
             const int i = i0 + q * kWave + lane;
             if (i < seg_cnt) x_ev[obase + i] = xv[q];
           }
