@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("BCM_LIB_PATH", os.path.join(_HERE, "lib", "libbcm_event_scan.so"))
 
 F32, F16, BF16, U8 = 0, 1, 2, 3
+ABI_VERSION = 3  # BCM_ABI_VERSION of include/bcm_event_scan.h
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: U8, torch.uint8: U8}
 
 c_i32, c_i64, c_f32, c_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -32,8 +33,11 @@ class ScanArgs(ctypes.Structure):
         ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
         ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("chunk_g_bytes", c_i64),
-        ("split_ws", c_p), ("split_ws_bytes", c_i64),
+        ("split_ws", c_p), ("split_ws_bytes", c_i64), ("status", c_p),
     ]
+
+
+SCAN_SEQLEN_EXCEEDED = 1  # bcm_scan_args.status: a channel holds more than max_seqlen events
 
 
 class ScanRows(ctypes.Structure):
@@ -116,7 +120,7 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.bcm_abi_version() != 2:
+        if handle.bcm_abi_version() != ABI_VERSION:
             raise RuntimeError("bc_mamba_amd: ABI version mismatch")
         _lib = handle
     return _lib

@@ -186,9 +186,12 @@ __global__ __launch_bounds__(256) void k_count_bits(const uint32_t* __restrict__
 // cu[0] = 0, cu[i+1] = counts[0] + ... + counts[i]; meta = (total, max).
 // One workgroup: 8 counts per thread (two 16-byte loads), DPP wave scans,
 // one barrier per 8192 counts.
+// maxsrc != NULL: meta's maximum is taken over maxsrc[0..n) instead of the
+// counts (the block maxima when the counts are block sums).
 template <bool VEC>
 __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict__ counts, int64_t n,
-                                                      int32_t* __restrict__ cu, int32_t* __restrict__ meta) {
+                                                      int32_t* __restrict__ cu, int32_t* __restrict__ meta,
+                                                      const int32_t* __restrict__ maxsrc) {
   constexpr int ITEMS = 8;
   __shared__ int s_wsum[2][16];
   __shared__ int s_wmax[16];
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(1024) void k_scan_counts(const int32_t* __restrict_
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       sum += v[i];
-      mx = max(mx, v[i]);
+      mx = max(mx, maxsrc ? (i0 + i < n ? maxsrc[i0 + i] : 0) : v[i]);
     }
     const int incl = wave_incl_sum_dpp(sum);
     if (lane == kWave - 1) s_wsum[par][wave] = incl;  // double-buffered: one barrier per pass
@@ -276,10 +279,14 @@ __device__ __forceinline__ T conv_at(const T* __restrict__ xr, int t, const floa
 }
 
 // BLK: the row offsets come from the count pass's block sums (bsum/bmax,
-// one per 4 rows): the block adds up the sums of the blocks before it and
-// the counts of its rows before each row, and writes cu_seqlens itself.
-// Block 0 also writes meta = (E, max count) (one 64-bit store written
-// through to memory, so a host may poll it while the fill runs).
+// one per 4 rows) and the counts of the block's rows before each row; the
+// fill writes cu_seqlens itself. With bpre == NULL (few blocks) each block
+// adds up the sums of the blocks before it, and block 0 also writes meta =
+// (E, max count) (one 64-bit store written through to memory, so a host may
+// poll it while the fill runs); that is quadratic in the block count, so
+// for many blocks a one-workgroup scan of the block sums runs first
+// (k_scan_counts over bsum: bpre[i] = sum of the blocks before block i, and
+// meta) and each block reads its offset from bpre.
 // KM = 0: x_ev gathers x at the events; KM = 4 (width exactly 4) or 8 (any
 // width <= 8): x_ev is the conv + SiLU of x (ConvAt) at the events.
 template <typename T, bool GATHER, bool TILES, bool BLK, int KM = 0>
@@ -290,8 +297,8 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
                                               T* __restrict__ x_ev, int32_t* __restrict__ tile_start, int64_t nT,
                                               int32_t* __restrict__ head_flags, const int32_t* __restrict__ counts,
                                               const int32_t* __restrict__ bsum, const int32_t* __restrict__ bmax,
-                                              int32_t* __restrict__ meta, int32_t* __restrict__ cu_out,
-                                              const ConvAt cv) {
+                                              const int32_t* __restrict__ bpre, int32_t* __restrict__ meta,
+                                              int32_t* __restrict__ cu_out, const ConvAt cv) {
   static_assert(KM == 0 || GATHER, "the conv form writes x_ev");
   __shared__ int32_t s_t[4][kFillSeg];
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -310,9 +317,9 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
 #pragma unroll
     for (int q = 0; q < 4; ++q) cb[q] = r0 + q < n_rows ? counts[r0 + q] : 0;
     const int64_t nblk = (n_rows + 3) / 4;
-    const bool first = blockIdx.x == 0;
+    const bool first = blockIdx.x == 0 && bpre == nullptr;
     int sm = 0, mx = 0;  // blocks before this one (all blocks for block 0's totals)
-    const int64_t lim = first ? nblk : (int64_t)blockIdx.x;
+    const int64_t lim = bpre ? 0 : (first ? nblk : (int64_t)blockIdx.x);
     for (int64_t i0 = 0; i0 < lim; i0 += 8 * (int64_t)blockDim.x) {  // 8 independent loads per thread in flight
       int vs[8], vm[8];
 #pragma unroll
@@ -339,6 +346,7 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
       before += s_part[w][0];
       total_max = max(total_max, s_part[w][1]);
     }
+    if (bpre) before = bpre[blockIdx.x];
     if (first && threadIdx.x == 0) {
       const uint64_t packed = (uint64_t)(uint32_t)before | ((uint64_t)(uint32_t)total_max << 32);
       __hip_atomic_store(reinterpret_cast<uint64_t*>(meta), packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -594,6 +602,21 @@ __global__ __launch_bounds__(256) void k_gather_bwd_rows(const T* __restrict__ g
 
 static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Above this many 4-row blocks the fill reads its row offsets from a scan of
+// the block sums instead of summing them per block (block i reads i values:
+// ~2 M L2 reads at 2048 blocks, ~8 M at 4096, quadratic beyond).
+constexpr int64_t kFillSelfScanBlocks = 4096;
+
+// The prefix of the block sums (bpre = block_sums + 2 * nblk) and meta, when
+// the fill does not derive them itself; returns bpre or NULL.
+static const int32_t* block_prefix(const int32_t* block_sums, int64_t nblk, int32_t* meta, hipStream_t s) {
+  if (nblk <= kFillSelfScanBlocks) return nullptr;
+  int32_t* bpre = const_cast<int32_t*>(block_sums) + 2 * nblk;
+  hipLaunchKernelGGL(k_scan_counts<false>, dim3(1), dim3(1024), 0, s, block_sums, nblk, bpre, meta,
+                     block_sums + nblk);
+  return bpre;
+}
+
 static unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace bcm
@@ -636,9 +659,11 @@ int bcm_extract_scan(const int32_t* counts, int64_t n_rows, int32_t* cu_seqlens,
   if (!cu_seqlens || !meta || (n_rows > 0 && !counts)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
   if (!aligned(meta, 8)) return set_error(BCM_EINVAL, "%s: meta must be 8-byte aligned", fn);
   if (aligned(counts, 16))
-    hipLaunchKernelGGL(k_scan_counts<true>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
+    hipLaunchKernelGGL(k_scan_counts<true>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta,
+                       nullptr);
   else
-    hipLaunchKernelGGL(k_scan_counts<false>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta);
+    hipLaunchKernelGGL(k_scan_counts<false>, dim3(1), dim3(1024), 0, hs(stream), counts, n_rows, cu_seqlens, meta,
+                       nullptr);
   return check_launch(fn);
 }
 
@@ -663,7 +688,7 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_
     constexpr bool TT = decltype(tiles)::value;
     hipLaunchKernelGGL((k_fill<T, G, TT, false>), grid, block, 0, hs(stream), bitmask, W, base_cu, n_rows, L, ex,
                        static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
-                       head_flags, nullptr, nullptr, nullptr, nullptr, nullptr, ConvAt{});
+                       head_flags, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ConvAt{});
   };
   using Y = std::true_type;
   using N = std::false_type;
@@ -680,7 +705,9 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu, int64_t n_
   return check_launch(fn);
 }
 
-int64_t bcm_extract_block_sums_bytes(int64_t n_rows) { return n_rows < 0 ? 0 : 8 * ((n_rows + 3) / 4); }
+// block_sums layout: [nblk] sums, [nblk] maxima, [nblk + 1] exclusive
+// prefix of the sums (written only when the fill scans them first).
+int64_t bcm_extract_block_sums_bytes(int64_t n_rows) { return n_rows < 0 ? 0 : 4 * (3 * ((n_rows + 3) / 4) + 1); }
 
 int bcm_extract_count_blocks(const void* membrane, int dtype, int64_t n_rows, int64_t L, float threshold,
                              uint32_t* bitmask, int32_t* counts, int32_t* block_sums, bcm_stream_t stream) {
@@ -724,13 +751,14 @@ int bcm_extract_fill_blocks(const uint32_t* bitmask, const int32_t* counts, cons
   const int64_t W = bitmask_words(L), nT = tile_count(L), nblk = (n_rows + 3) / 4;
   const dim3 grid((unsigned)nblk), block(256);
   const int ex = (int)expand;
+  const int32_t* bpre = block_prefix(block_sums, nblk, meta, hs(stream));
   auto launch = [&](auto tag, auto gather, auto tiles) {
     using T = decltype(tag);
     constexpr bool G = decltype(gather)::value;
     constexpr bool TT = decltype(tiles)::value;
     hipLaunchKernelGGL((k_fill<T, G, TT, true>), grid, block, 0, hs(stream), bitmask, W, nullptr, n_rows, L, ex,
                        static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start, nT,
-                       nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens, ConvAt{});
+                       nullptr, counts, block_sums, block_sums + nblk, bpre, meta, cu_seqlens, ConvAt{});
   };
   using Y = std::true_type;
   using N = std::false_type;
@@ -768,6 +796,7 @@ int bcm_extract_fill_blocks_conv(const uint32_t* bitmask, const int32_t* counts,
   const dim3 grid((unsigned)nblk), block(256);
   const int ex = (int)expand;
   const ConvAt cv{weight, bias, K, (int)dim, silu, x_batch_stride, x_dim_stride};
+  const int32_t* bpre = block_prefix(block_sums, nblk, meta, hs(stream));
   dispatch_dtype(x_dtype, [&](auto tag) {
     using T = decltype(tag);
     auto go = [&](auto tiles, auto km) {
@@ -775,7 +804,7 @@ int bcm_extract_fill_blocks_conv(const uint32_t* bitmask, const int32_t* counts,
       constexpr int KM = decltype(km)::value;
       hipLaunchKernelGGL((k_fill<T, true, TT, true, KM>), grid, block, 0, hs(stream), bitmask, W, nullptr, n_rows, L,
                          ex, static_cast<const T*>(x), ch_ids, t_steps, k_flat, static_cast<T*>(x_events), tile_start,
-                         nT, nullptr, counts, block_sums, block_sums + nblk, meta, cu_seqlens, cv);
+                         nT, nullptr, counts, block_sums, block_sums + nblk, bpre, meta, cu_seqlens, cv);
     };
     using K4 = std::integral_constant<int, 4>;
     using K8 = std::integral_constant<int, 8>;

@@ -138,6 +138,13 @@ __device__ __forceinline__ void store_param_grad(const bcm_scan_args& a, int d, 
   else if (a.dD) a.dD[d] = v;
 }
 
+// A channel of n events longer than the caller's max_seqlen: its saved
+// states (x, chunk_g) have fewer rows than its passes need. Flagged in the
+// caller's status word (a plain vector store; several lanes may write it).
+__device__ __forceinline__ void report_seqlen(const bcm_scan_args& a, int n) {
+  if (n > a.max_seqlen && a.status) a.status[0] = BCM_SCAN_SEQLEN_EXCEEDED;
+}
+
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a) {
   using Ops = Grp<G>;
@@ -213,6 +220,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
     e0 = act ? a.cu_seqlens[ch] : 0;
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
+    report_seqlen(a, n);
   };
   int e0, n;
   const int b_first = sp * nslots, b_step = nslots * S;
@@ -324,7 +332,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
           carry[s] = Pn;
           carry[N + s] = gend;
           if (xsave) reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, gend * sWB[s]);
-          if (a.chunk_g && c + 1 < nch) a.chunk_g[(ch * ((a.max_seqlen + C - 1) / C) + c + 1) * N + s] = gend * sWB[s];
+          // chunk_g has one row per pass of a max_seqlen-long channel: a
+          // longer channel (reported through a.status) has no row for its
+          // later passes
+          const int g_rows = (a.max_seqlen + C - 1) / C;
+          if (a.chunk_g && c + 1 < nch && c + 1 < g_rows) a.chunk_g[(ch * g_rows + c + 1) * N + s] = gend * sWB[s];
         }
       };
       auto states = [&](auto exact_tag) {
@@ -471,6 +483,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
     e0 = act ? a.cu_seqlens[ch] : 0;
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
+    report_seqlen(a, n);
   };
   int e0, n;
   const int b_first = sp * nslots, b_step = nslots * S;

@@ -223,9 +223,13 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
 
     By default the fill derives the row offsets itself from the count pass's
     block sums (no offsets kernel) and is enqueued before E is known, so its
-    event outputs are allocated for every possible event (B*d_model*expand*L)
-    and returned as views of the first E. exact_alloc=True runs the separate
-    offsets pass, reads E first and allocates exactly E.
+    event outputs are written into buffers sized for every possible event
+    (B*d_model*expand*L); once E is read, the first E entries are copied into
+    exact-size tensors and the worst-case buffers are released, so the
+    returned streams (which autograd keeps until the backward) hold E
+    entries. exact_alloc=True runs the separate offsets pass, reads E first
+    and fills exact-size tensors directly (no copies, one more kernel and
+    the GPU idle during the host read).
 
     conv = (weight [D, K], bias [D] or None, silu): x is then the input of
     the block's depthwise causal conv (rows contiguous, any batch / channel
@@ -294,9 +298,13 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
                       _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
         E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
         E = E_base * expand
-        k = k[:E]
+        # exact-size copies of the event streams, so that callers that keep
+        # them (autograd saves k and x_events for the backward) hold E
+        # entries, not the worst case; the worst-case buffers are released
+        # here (two small copy kernels, ~4E bytes each)
+        k = k[:E].clone()
         if positions:
-            ch, t = ch[:E], t[:E]
+            ch, t = ch[:E].clone(), t[:E].clone()
         if xe is not None:
-            xe = xe[:E]
+            xe = xe[:E].clone()
         return ch, t, k, cu, max_seqlen, xe, (bitmask, tile_start, expand)

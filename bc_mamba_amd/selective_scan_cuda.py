@@ -112,6 +112,25 @@ def _common_checks(fn, u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_activ
     return dim, dstate, mode
 
 
+class _SeqlenStatus:
+    """The scan kernels' status word (bcm_scan_args.status) for a call whose
+    max_seqlen comes from the caller: zeroed before the launch, read after
+    it (one host sync), RuntimeError when some channel held more than
+    max_seqlen events (its saved states would be incomplete)."""
+
+    def __init__(self, fn, max_seqlen, dev, enabled):
+        self.fn, self.max_seqlen = fn, int(max_seqlen)
+        self.t = torch.zeros(1, dtype=torch.int32, device=dev) if enabled else None
+
+    def attach(self, a):
+        a.status = self.t.data_ptr() if self.t is not None else None
+
+    def check(self):
+        if self.t is not None and int(self.t.item()) == _nat.SCAN_SEQLEN_EXCEEDED:
+            raise RuntimeError(f"{self.fn}: a channel holds more than max_seqlen = {self.max_seqlen} events "
+                               "(cu_seqlens and max_seqlen disagree)")
+
+
 def _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB=None, dC=None):
     """bcm_scan_bc of the legacy / tiled modes. Legacy B/C are per event when
     their second dimension is E, else per model channel, as
@@ -171,13 +190,18 @@ def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D
 
 
 def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D=None, z=None,
-                tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False, pw_B=None, pw_C=None, _chunk_g=None):
+                tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False, pw_B=None, pw_C=None, _chunk_g=None,
+                _trusted_seqlen=False):
     """Flat per-channel scan forward -> [out, x] or [out, x, out_z]
     (selective_scan.cpp:674-884). x is [n_channels, n_chunks, 2*dstate]
     float32 holding, per 2048-event chunk and state, (prod of decays, h).
     `_chunk_g` (not in the reference signature): a float32 tensor from
     chunk_states_buffer() that receives the pass-start states, so that
-    bwd_flat_ch need not recompute them (depthwise mode)."""
+    bwd_flat_ch need not recompute them (depthwise mode).
+    In depthwise mode the kernels report a channel longer than max_seqlen
+    and this call raises RuntimeError (one host sync to read the report);
+    `_trusted_seqlen=True` skips the report for callers whose max_seqlen
+    comes from the extraction itself."""
     fn = "selective_scan_fwd_flat_ch"
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous(),
            f"{fn}: u_flat/k_flat/cu_seqlens must be contiguous")
@@ -202,7 +226,10 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         if mode == "depthwise":
             if _chunk_g is not None:
                 a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
+            status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
+            status.attach(a)
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
+            status.check()
         else:
             bc = _bc(mode, B, C, int(u_flat.size(0)), tile_offsets, tile_chunk_size)
             _nat.call("bcm_scan_var_fwd", a, bc, _nat.stream_of(u_flat))
@@ -211,7 +238,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
-                pw_B=None, pw_C=None, _chunk_g=None, _rows=None):
+                pw_B=None, pw_C=None, _chunk_g=None, _rows=None, _trusted_seqlen=False):
     """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
     ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
     dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
@@ -220,7 +247,9 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     `_rows` (not in the reference signature; depthwise mode without pw_B):
     (bitmask, mask_row_div, tile_start, dx) of the extraction's event index
     and a contiguous [n_channels, L] tensor of u_flat's dtype, which also
-    receives the gather backward of du (du at the events, 0 elsewhere)."""
+    receives the gather backward of du (du at the events, 0 elsewhere).
+    As fwd_flat_ch, raises RuntimeError when a channel holds more than
+    max_seqlen events (unless `_trusted_seqlen`)."""
     fn = "selective_scan_bwd_flat_ch"
     _check(dout_flat.dtype == u_flat.dtype, f"{fn}: dout_flat must match u_flat dtype")
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous()
@@ -274,6 +303,8 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.dD = dD.data_ptr() if dD is not None else None
         a.dz = dz.data_ptr() if dz is not None else None
         if mode == "depthwise":
+            status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
+            status.attach(a)
             a.dW_B, a.dW_C = dB.data_ptr(), dC.data_ptr()
             _, _, needs_g = _nat.scan_chunking(a)
             if needs_g and _chunk_g is None:
@@ -286,6 +317,7 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 f.out, f.x = scratch_out.data_ptr(), torch.empty_like(x).data_ptr()
                 f.out_z = torch.empty_like(u_flat).data_ptr() if has_z else None
                 f.chunk_g, f.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
+                status.attach(f)
                 _nat.call("bcm_scan_fwd", f, s)
             if _chunk_g is not None:
                 a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
@@ -304,6 +336,7 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 r.bitmask, r.mask_row_div, r.tile_start = bitmask.data_ptr(), int(mrd), tile_start.data_ptr()
                 r.seqlen, r.dx = int(dx.size(1)), dx.data_ptr()
                 _nat.call("bcm_scan_bwd_rows", a, r, s)
+            status.check()
             if pw_B is not None:  # dB, dC hold dW_eff here
                 dpw_B, dpw_C = dB @ B.t(), dC @ C.t()
                 dB, dC = pw_B.t() @ dB, pw_C.t() @ dC

@@ -96,7 +96,7 @@ class SelectiveScanFlatChFn(torch.autograd.Function):
             result = selective_scan_cuda.bwd_flat_ch(
                 u_flat, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, B, C, dout.contiguous(), x,
                 D, z, out_flat, tile_offsets, ctx.tile_chunk_size, ctx.is_depthwise_bc, pw_B, pw_C,
-                _chunk_g=ctx.chunk_g)
+                _chunk_g=ctx.chunk_g, _trusted_seqlen=True)  # the forward checked max_seqlen
         du, dA, dW_B, dW_C, ddt_idle, ddt_active = result[:6]
         ridx = 6
         dD = dz = dpw_B = dpw_C = None

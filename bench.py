@@ -32,7 +32,7 @@ CAL_BYTES = 256 << 20  # device-to-device copy that calibrates the PMC byte coun
 FLUSH_BYTES = 512 << 20  # written before each cold step: more than L2 plus the 256 MB MALL
 COLD_REPS = 11
 
-# device kernels behind each stage of Path.KERNELS (symbol substrings)
+# device kernels behind each stage of FusedStep.KERNELS (symbol substrings)
 STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
                  "scan_fwd": ["k_scan_fwd"], "restore_fwd": ["k_restore_fwd"],
                  "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"],
@@ -59,126 +59,28 @@ def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
     }
 
 
-class Path:
-    """The fwd+bwd path driven through the C ABI with reusable buffers.
-
-    Event buffers are sized for the largest possible event count (every
-    step of every channel), so the fill kernel can be enqueued before the
-    host has read E: the fill writes E and max_seqlen to pinned memory early,
-    the host polls it while fill runs, and the GPU never idles on the round
-    trip."""
-
-    KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd"]
-
-    def __init__(self, w, dev):
-        import torch
-        from bc_mamba_amd import _native as nat
-        self.t, self.nat, self.w, self.dev = torch, nat, w, dev
-        B, D, L = w.B, w.D, w.L
-        self.NC = B * D
-        i32 = dict(dtype=torch.int32, device=dev)
-        self.bitmask = torch.empty((self.NC, nat.bitmask_words(L)), **i32)
-        self.counts = torch.empty(self.NC, **i32)
-        self.cu = torch.empty(self.NC + 1, **i32)
-        self.meta_h = nat.HostMeta()
-        self.bsums = torch.empty(nat.lib().bcm_extract_block_sums_bytes(self.NC) // 4, **i32)
-        self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
-        self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
-        self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
-        self.ws = torch.empty(nat.lib().bcm_restore_bwd_workspace_bytes(self.NC, L) // 4, dtype=torch.float32,
-                              device=dev)
-        cap = self.NC * L  # upper bound of E
-        self.k = torch.empty(cap, **i32)
-        self.u = torch.empty(cap, dtype=w.dtype, device=dev)
-        self.y = torch.empty(cap, dtype=w.dtype, device=dev)
-        self.dy32 = torch.empty(cap, dtype=torch.float32, device=dev)
-        self.dy = self.dy32 if w.dtype == torch.float32 else torch.empty(cap, dtype=w.dtype, device=dev)
-        self.du = torch.empty(cap, dtype=w.dtype, device=dev)
-        self.x = torch.empty((self.NC, max(1, -(-L // 2048)), 2 * w.N), dtype=torch.float32, device=dev)
-        f32 = dict(dtype=torch.float32, device=dev)
-        self.grads = [torch.empty((w.D, w.N), **f32) for _ in range(3)] + [torch.empty(w.D, **f32) for _ in range(3)]
-        self.args = self._scan_args()
-        self.rows = nat.ScanRows()
-        self.rows.bitmask, self.rows.mask_row_div, self.rows.tile_start = self.bitmask.data_ptr(), 1, \
-            self.tile_start.data_ptr()
-        self.rows.seqlen, self.rows.dx = L, self.dx.data_ptr()
-        self.E = self.ms = -1
-        self.events = {}
-
-    def _scan_args(self):
-        nat, w = self.nat, self.w
-        a = nat.ScanArgs()
-        a.n_channels, a.dim, a.dstate, a.dtype = self.NC, w.D, w.N, nat.dtype_code(w.dtype)
-        a.u, a.k, a.cu_seqlens = self.u.data_ptr(), self.k.data_ptr(), self.cu.data_ptr()
-        a.dt_idle, a.dt_active = w.dt_idle.data_ptr(), w.dt_active.data_ptr()
-        a.A, a.W_B, a.W_C, a.D = w.A.data_ptr(), w.W_B.data_ptr(), w.W_C.data_ptr(), w.D_skip.data_ptr()
-        a.out, a.x = self.y.data_ptr(), self.x.data_ptr()
-        a.dout, a.x_saved, a.du = self.dy.data_ptr(), self.x.data_ptr(), self.du.data_ptr()
-        a.dA, a.dW_B, a.dW_C, a.ddt_idle, a.ddt_active, a.dD = (g.data_ptr() for g in self.grads)
-        return a
-
-    def step(self, timed=()):
-        """One fwd+bwd. Kernels named in `timed` get HIP events around them."""
-        t, nat, w = self.t, self.nat, self.w
-        s = nat.stream_of(self.counts)
-        P = nat.ptr
-        ev = self.events
-
-        def mark(name, fn):
-            if name in timed:
-                a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-                a.record()
-                fn()
-                b.record()
-                ev.setdefault(name, []).append((a, b))
-            else:
-                fn()
-
-        B, D, L = w.B, w.D, w.L
-        # count also writes per-block sums; fill derives the row offsets from
-        # them, writes cu and sends (E, max_seqlen) straight to pinned host
-        # memory (no offsets kernel, no copy kernel, no event: the host polls
-        # while fill runs)
-        self.meta_h.arm()
-        mark("count", lambda: nat.call("bcm_extract_count_blocks", P(w.membrane), nat.dtype_code(w.membrane.dtype),
-                                       self.NC, L, float(w.threshold), P(self.bitmask), P(self.counts), P(self.bsums),
-                                       s))
-        mark("fill", lambda: nat.call("bcm_extract_fill_blocks", P(self.bitmask), P(self.counts), P(self.bsums),
-                                      self.meta_h.ptr(), self.NC, L, 1, P(w.x_conv), nat.dtype_code(w.dtype),
-                                      P(self.cu), None, None, P(self.k), P(self.u), P(self.tile_start), s))
-        E, ms = self.meta_h.wait(t.cuda.current_stream())  # fill keeps the GPU busy meanwhile
-        if E != self.E or ms != self.ms:
-            self.E, self.ms = E, ms
-            a = self.args
-            a.n_events, a.max_seqlen, a.n_chunks = E, ms, max(1, -(-ms // 2048))
-            # pass-start states of channels longer than one pass (written by
-            # the forward, read by the backward)
-            _, n_pass, needs = nat.scan_chunking(a)
-            self.chunk_g = t.empty((self.NC, n_pass, w.N), dtype=t.float32, device=self.u.device) if needs else None
-            a.chunk_g = self.chunk_g.data_ptr() if needs else None
-            a.chunk_g_bytes = self.chunk_g.numel() * 4 if needs else 0
-            # parameter-gradient partials when model channels are split over workgroups
-            nb = int(nat.lib().bcm_scan_bwd_workspace_bytes(a))
-            self.split_ws = t.empty(max(nb, 4) // 4, dtype=t.float32, device=self.u.device) if nb else None
-            a.split_ws = self.split_ws.data_ptr() if nb else None
-            a.split_ws_bytes = nb
-        mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
-        mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y), nat.dtype_code(w.dtype), E, P(self.bitmask), 1,
-                                             P(self.tile_start), self.NC, D, L, P(self.dense),
-                                             nat.dtype_code(w.dtype), s))
-        mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), nat.dtype_code(w.dtype), P(self.bitmask),
-                                             1, P(self.tile_start), self.NC, D, L, P(self.dy32), E, P(self.ws),
-                                             4 * self.ws.numel(), s))
-        if self.dy is not self.dy32:
-            self.dy[:E].copy_(self.dy32[:E])
-        # the scan backward writes du and the dense dx rows (the gather
-        # backward) in one kernel where the shape allows, else in two
-        mark("scan_bwd", lambda: nat.call("bcm_scan_bwd_rows", self.args, self.rows, s))
-
-    def kernel_ms(self, name):
-        self.t.cuda.synchronize()
-        v = [a.elapsed_time(b) for a, b in self.events.get(name, [])]
-        return sum(v) / len(v) if v else float("nan")
+def own_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o):
+    """Compulsory traffic of this build's own kernel interfaces for the same
+    step (each tensor once): the fill writes k and u but no ch / t streams;
+    restore and the gather backward read the event index (a bitmask of one
+    bit per step and a tile table of one int32 per 64 steps) instead of t
+    and ch; dy is fp32 and, for 16-bit u, copied once to u's dtype for the
+    scan backward. The reference interface's figure (algorithmic_bytes) is
+    the metric's numerator; this one says how close the kernels run to
+    their own floor."""
+    M, NC = B * D * L, B * D
+    n_ch = max(1, -(-max_seqlen // 2048))
+    st = NC * n_ch * N * 8
+    index = M // 8 + NC * (-(-L // 64) + 1) * 4  # bitmask + tile table
+    dy_copy = 0 if s_u == 4 else E * 4 + E * s_u
+    return {
+        "count": M * s_m + M // 8 + NC * 4,
+        "fill": M // 8 + NC * 4 + M * s_u + E * 4 + E * s_u + index - M // 8 + 4 * (NC + 1),
+        "scan_fwd": E * s_u + E * 4 + E * s_u + st,
+        "restore_fwd": E * s_u + index + M * s_o,
+        "restore_bwd": M * s_o + index + E * 4,
+        "scan_bwd": E * s_u + E * 4 + E * s_u + st + E * s_u + index + M * s_u + dy_copy,
+    }
 
 
 def calibration_copy(dev):
@@ -252,7 +154,8 @@ def cpu_baseline(cfg, batches, reps=3):
     import torch
     from bc_mamba_amd.workloads import CONFIGS, make_workload
     from oracle import torch_path as tp
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    # the box's CPU share (OMP_NUM_THREADS there), at most the cores the OS shows
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1)
     torch.set_num_threads(threads)
     w = make_workload(cfg, B=batches)
     args = (w.membrane, w.x_conv.float(), w.dout.float(), w.threshold, w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C,
@@ -273,7 +176,8 @@ def cpu_baseline(cfg, batches, reps=3):
                 break
     except OSError:
         pass
-    return {"value": E / med, "unit": "events/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": E / med, "unit": "events/s", "cores": torch.get_num_threads(), "os_cpu_count": os.cpu_count(),
+            "torch_threads": torch.get_num_threads(), "kind": "port",
             "sample": f"config {cfg} with B={batches} of its {CONFIGS[cfg]['B']} batches "
                       f"(E={E} events), torch fp32 restatement (oracle/torch_path.py), median of {reps} "
                       f"fwd+bwd reps, {cpu}", "seconds_per_rep": med}
@@ -299,6 +203,7 @@ def main():
 
     import torch
     from bc_mamba_amd import _native
+    from bc_mamba_amd.fused_step import FusedStep
     from bc_mamba_amd.workloads import make_workload
     _native.lib()
     dev = torch.device("cuda:0")
@@ -306,7 +211,7 @@ def main():
         print(json.dumps(model_step_bench(args, dev)), flush=True)
         return
     w = make_workload(args.cfg).to(dev)
-    path = Path(w, dev)
+    path = FusedStep(w, dev)
 
     if args.pmc_child:  # a few steps and the calibration copy, run under rocprofv3 --pmc by the parent
         for _ in range(3):
@@ -320,8 +225,8 @@ def main():
     for _ in range(max(args.warmup, 1)):
         path.step()
     for _ in range(PROBE_STEPS):
-        path.step(timed=Path.KERNELS)
-    per_kernel = {n: path.kernel_ms(n) for n in Path.KERNELS}
+        path.step(timed=FusedStep.KERNELS)
+    per_kernel = {n: path.kernel_ms(n) for n in FusedStep.KERNELS}
     dominant = max(per_kernel, key=per_kernel.get)
     path.events.clear()
 
@@ -345,6 +250,7 @@ def main():
     su = torch.tensor([], dtype=w.dtype).element_size()
     alg = algorithmic_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su)
     total_bytes = sum(alg.values())
+    own_total = sum(own_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su).values())
     # algorithmic bytes of one launch of each kernel (its share of the API-contract traffic)
     kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC,
                     "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
@@ -369,6 +275,10 @@ def main():
                    "max_seqlen": ms},
         "achieved_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
         "algorithmic_bytes": total_bytes,
+        # the same time against this build's own compulsory traffic (no ch /
+        # t streams, the event index instead): a stricter fraction
+        "own_bytes": own_total,
+        "path_frac_own_bytes": own_total / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "path_frac_of_hbm_peak": total_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": per_kernel,
         # one step after a 512 MiB write has flushed L2 and the 256 MB MALL
@@ -421,6 +331,7 @@ def model_step_bench(args, dev):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    peak = peak_memory(model, step)
     return {
         "metric": METRIC, "value": E / (ms * 1e-3), "unit": "events/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -429,8 +340,37 @@ def model_step_bench(args, dev):
                                "d_inner 512, N 16, L 1024, B 50, byte tokens, random init",
                    "events_per_step": E, "events_per_layer": per_layer,
                    "density_per_layer": [e / (50 * 1024 * 512) for e in per_layer]},
+        "peak_memory_bytes": peak,
         "roofline": None,
     }
+
+
+def peak_memory(model, step):
+    """torch.cuda.max_memory_allocated over one training step: the fused
+    event path (default) and the reference composition (every block with
+    fused_event_path=False and the plain STE sampler), same model, inputs
+    and parameters. Model state (parameters, and gradients, which step()
+    frees) is included in both."""
+    import torch
+    from bc_mamba_amd.e_model import SpikeSamplerSurrogate
+    samplers = [m for m in model.modules() if isinstance(m, SpikeSamplerSurrogate)]
+    res = {}
+    for name, fused in (("fused", True), ("reference_composition", False)):
+        for blk in model.blocks:
+            blk.core.fused_event_path = fused
+        for sm in samplers:
+            sm.fused_bits = fused
+        step()  # warm the allocator for this path
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        step()
+        torch.cuda.synchronize()
+        res[name] = int(torch.cuda.max_memory_allocated())
+    for blk in model.blocks:
+        blk.core.fused_event_path = True
+    for sm in samplers:
+        sm.fused_bits = True
+    return res
 
 
 def cold_step_ms(path, dev, reps):

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define BCM_ABI_VERSION 2
+#define BCM_ABI_VERSION 3
 
 typedef struct ihipStream_t* bcm_stream_t; /* == hipStream_t */
 
@@ -98,10 +98,13 @@ int bcm_extract_fill(const uint32_t* bitmask, const int32_t* base_cu,
  * replaces the DeviceScan of extract_events_cuda.cu:361-372 in the fused
  * model path, one kernel fewer).
  * bcm_extract_count_blocks: as bcm_extract_count; each block of 4 rows also
- * writes its rows' event sum and maximum count to block_sums
- * [2][ceil(n_rows/4)] int32 (bcm_extract_block_sums_bytes).
+ * writes its rows' event sum and maximum count to block_sums (int32, of
+ * bcm_extract_block_sums_bytes: nblk sums, nblk maxima, nblk + 1 words of
+ * scratch, nblk = ceil(n_rows/4)).
  * bcm_extract_fill_blocks: as bcm_extract_fill, each block deriving its
- * rows' offsets from block_sums and counts; it writes cu_seqlens
+ * rows' offsets from block_sums and counts (for more than 4096 blocks a
+ * one-workgroup scan of the block sums into the scratch words runs first,
+ * so the offset work stays linear in n_rows); it writes cu_seqlens
  * [n_rows*expand+1] (logical channels) and meta = (E_base, max count) as
  * bcm_extract_scan does (one 64-bit store written through to memory: a host
  * that set meta[0] = -1 may poll pinned meta while the fill runs). Since E
@@ -246,7 +249,17 @@ typedef struct bcm_scan_args {
    * fixed order (same results either way up to that order). */
   float* split_ws;
   int64_t split_ws_bytes;      /* size of split_ws (too small: no split) */
+  /* Optional (NULL: not reported) int32 status word, device memory or
+   * device-mapped pinned host memory, that the caller zeroes beforehand.
+   * The kernels set it to BCM_SCAN_SEQLEN_EXCEEDED when some channel holds
+   * more than max_seqlen events: x and chunk_g are sized from max_seqlen,
+   * so such a channel's saved states (and with them the backward of its
+   * later passes, and bcm_scan_bwd_rows' dense row) are incomplete. Every
+   * write stays inside the buffers either way. */
+  int32_t* status;
 } bcm_scan_args;
+
+#define BCM_SCAN_SEQLEN_EXCEEDED 1
 
 /* Events per pass of a channel (pass_len) and passes of the longest channel
  * (n_pass) for these arguments (max_seqlen, n_events, n_channels, dstate):

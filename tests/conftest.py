@@ -13,7 +13,7 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and the built native library")
 
 
-def assert_close(actual, expected, rtol, atol_rel=1e-5, name=""):
+def assert_close(actual, expected, rtol, atol_rel=1e-6, name=""):
     """|a - e| <= rtol*|e| + atol_rel*max|e| elementwise (the absolute floor
     covers exact zeros and cancellation in long fp32 sums)."""
     a = np.asarray(actual, dtype=np.float64)

@@ -47,8 +47,8 @@ def test_library_exports_every_header_symbol(lib):
 
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
-    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 26 pointers + 2 int64 sizes
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 26 * 8 + 2 * 8
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 27 pointers + 2 int64 sizes
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 27 * 8 + 2 * 8
 
 
 def test_scan_bc_layout_matches_header():
@@ -75,8 +75,15 @@ def test_scan_rows_arguments_are_rejected_before_launch(lib):
     assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "8-byte aligned" in lib.bcm_last_error().decode()
 
 
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    for name, value in (("BCM_ABI_VERSION", nat.ABI_VERSION), ("BCM_SCAN_SEQLEN_EXCEEDED", nat.SCAN_SEQLEN_EXCEEDED)):
+        m = re.search(r"#define\s+%s\s+(\d+)" % name, text)
+        assert m and int(m.group(1)) == value, name
+
+
 def test_host_helpers(lib):
-    assert lib.bcm_abi_version() == 2
+    assert lib.bcm_abi_version() == nat.ABI_VERSION == 3
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64
     assert lib.bcm_bitmask_words(1) == 32 and lib.bcm_bitmask_words(1025) == 64
     assert lib.bcm_tile_count(2048) == nat.tile_count(2048) == 32
@@ -127,6 +134,22 @@ def test_scan_chunk_states_size_is_checked(lib):
     assert needs and n_pass > 1
     a.chunk_g, a.chunk_g_bytes = 16, 4 * 8 * n_pass * 16 - 4
     assert lib.bcm_scan_fwd(a, None) == 1 and "chunk_g needs" in lib.bcm_last_error().decode()
+
+
+def test_scan_backward_requires_chunk_states(lib):
+    """A multi-pass backward whose passes are shorter than 2048 events needs
+    the forward's pass-start states: without chunk_g it is refused before
+    any launch instead of reading states it was not given (host validation
+    only; the pointers are never dereferenced)."""
+    a = nat.ScanArgs()
+    # 16 channels, mean 150 events, one of 744: the cost model picks passes
+    # much shorter than the longest channel
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 2400, 16, 8, 16, 744, 1, 0
+    pass_len, n_pass, needs = nat.scan_chunking(a)
+    assert needs and n_pass > 1 and pass_len < 2048  # the refusal below is exercised
+    a.cu_seqlens = a.dt_idle = a.dt_active = a.A = a.W_B = a.W_C = a.u = a.k = 16
+    a.dA = a.dW_B = a.dW_C = a.ddt_idle = a.ddt_active = a.dout = a.du = 16
+    assert lib.bcm_scan_bwd(a, None) == 1 and "chunk_g required" in lib.bcm_last_error().decode()
 
 
 def test_conv_events_backward_rejects_overlapping_rows(lib):

@@ -189,3 +189,57 @@ def test_block_offsets_match_scan(cuda_device, NC, L, p, expand):
     assert E2 * expand == E and ms2 == ms
     assert torch.equal(cu2, cu) and torch.equal(k2[:E], k) and torch.equal(xe2[:E], xe)
     assert torch.equal(ts2, tile_start)
+
+
+def _tile_table(ch, t, NC, L):
+    """Oracle tile table: each channel's first event index at or after step
+    64j (the channel's end for j = ntiles)."""
+    nT = (L + 63) // 64
+    key = ch.astype(np.int64) * L + t
+    j = np.minimum(np.arange(nT + 1) * 64, L)
+    q = np.arange(NC, dtype=np.int64)[:, None] * L + j[None, :]
+    return np.searchsorted(key, q.ravel(), side="left").reshape(NC, nT + 1).astype(np.int32)
+
+
+FUSED_CASES = [  # B, Dm, L, density, expand, positions
+    (32, 256, 2048, 0.15, 1, False),  # config 1: the bench's form (2048 blocks, self-derived offsets)
+    (32, 256, 2048, 0.15, 1, True),
+    (2, 64, 1024, "gauss", 2, False),  # the model block's expand 2
+    (3, 5, 1000, 0.3, 3, True),
+    (16, 1024, 128, 0.2, 1, True),     # 16384 rows: 4096 blocks, the last self-derived size
+    (64, 1024, 64, 0.25, 1, False),    # 65536 rows: 16384 blocks, offsets from the block-sum scan
+    (64, 1025, 96, 0.1, 2, True),      # a partial last block, L % 64 != 0, with the block-sum scan
+]
+
+
+@pytest.mark.parametrize("B,Dm,L,p,expand,positions", FUSED_CASES)
+def test_extract_indexed_fused_matches_oracle(cuda_device, B, Dm, L, p, expand, positions):
+    """The production extraction (bcm_extract_count_blocks +
+    bcm_extract_fill_blocks, one host read of E, the fill deriving row
+    offsets from block sums, x gathered at the events, the tile table)
+    against the oracle's extract_base_events + expand_base_events +
+    gather_fwd: every index output bit-exact."""
+    print(f"fused extract case B={B} Dm={Dm} L={L} p={p} expand={expand} positions={positions}", flush=True)
+    mem = _membrane(B, Dm, L, p, torch.float32, seed=B + Dm + L)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, Dm * expand, L, generator=g)
+    ch, t, k, cu, ms, xe, (bitmask, tile_start, mrd) = ee.extract_events_indexed(
+        mem.to(cuda_device), 0.5, expand, x.to(cuda_device), positions=positions)
+    bch, bt, bk, bcu, _, bms = orc.extract_base_events(mem.numpy(), 0.5)
+    och, ot, ok, ocu, oms = orc.expand_base_events(bch, bt, bk, bcu, B, Dm, expand)
+    assert ms == oms == bms and mrd == expand
+    assert k.numel() == len(ok) and k.untyped_storage().nbytes() == 4 * len(ok)  # exact size, not worst-case views
+    assert np.array_equal(_np(k), ok), "k"
+    assert np.array_equal(_np(cu), ocu), "cu_seqlens"
+    if positions:
+        assert np.array_equal(_np(ch), och) and np.array_equal(_np(t), ot), "ch / t"
+    else:
+        assert ch is None and t is None
+    assert np.array_equal(_np(tile_start), _tile_table(och, ot, B * Dm * expand, L)), "tile table"
+    assert torch.equal(xe.cpu(), x.reshape(-1, L)[torch.from_numpy(och).long(), torch.from_numpy(ot).long()])
+    # the bitmask rows are those of the base membrane (bit t of row c)
+    nw = (L + 31) // 32  # words past the last step are padding
+    bits = _np(bitmask).view(np.uint32)[:, :nw]
+    want = np.zeros_like(bits)
+    np.bitwise_or.at(want, (bch, bt // 32), (np.uint32(1) << (bt % 32).astype(np.uint32)))
+    assert np.array_equal(bits, want), "bitmask"

@@ -1,6 +1,6 @@
 """The HIP path, called through the drop-in API, reproduces the committed
 golden fixtures (tests/golden/*.npz): indices bit-exact, outputs and every
-gradient within rtol 1e-4 (fp32) plus an absolute floor of 1e-5 * max|ref|."""
+gradient within rtol 1e-4 (fp32) plus an absolute floor of 1e-6 * max|ref|."""
 import os
 
 import numpy as np
@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 PATH_CASES = ["cfg0_slice", "edges", "multi_chunk", "clamped", "z_gate"]
-RTOL, ATOL_REL = 1e-4, 1e-5
+RTOL, ATOL_REL = 1e-4, 1e-6
 
 
 def load(name):

@@ -35,10 +35,10 @@ def test_path_config0_matches_torch_formulation(cuda_device):
     ref_out, ref_g, rE = tp.path_fwd_bwd(w.membrane, d(w.x_conv), d(w.dout), w.threshold, d(w.dt_idle),
                                           d(w.dt_active), d(w.A), d(w.W_B), d(w.W_C), d(w.D_skip))
     assert E == rE
-    assert_close(out.cpu(), ref_out, 1e-4, 1e-5, "out")
+    assert_close(out.cpu(), ref_out, 1e-4, 1e-6, "out")
     for name, g, r in zip(("x_conv", "dt_idle", "dt_active", "A", "W_B", "W_C", "D"), grads,
                           [ref_g[n] for n in ("x_conv", "dt_idle", "dt_active", "A", "W_B", "W_C", "D")]):
-        assert_close(g.cpu(), r, 1e-4, 1e-5, name)
+        assert_close(g.cpu(), r, 1e-4, 1e-6, name)
 
 
 @pytest.mark.parametrize("expand", [1, 2])
@@ -93,11 +93,11 @@ def test_config1_full_size_properties(cuda_device):
     P = lambda v: n(v)[:64]
     ref_out, ref_x = orc.scan_fwd(n(u)[s:e], n(k.float()).astype(np.int32)[s:e], cu_s, ms_s, P(w.dt_idle),
                                   P(w.dt_active), P(w.A), P(w.W_B), P(w.W_C), P(w.D_skip))
-    assert_close(n(out)[s:e], ref_out, 1e-4, 1e-5, "out sample")
-    assert_close(n(x)[sel], ref_x, 1e-4, 1e-5, "x sample")
+    assert_close(n(out)[s:e], ref_out, 1e-4, 1e-6, "out sample")
+    assert_close(n(x)[sel], ref_x, 1e-4, 1e-6, "x sample")
     ref_g = orc.scan_bwd(n(u)[s:e], n(k.float()).astype(np.int32)[s:e], cu_s, ms_s, P(w.dt_idle), P(w.dt_active),
                          P(w.A), P(w.W_B), P(w.W_C), n(dout)[s:e], P(w.D_skip))
-    assert_close(n(gb[0])[s:e], ref_g[0], 1e-4, 1e-5, "du sample")
+    assert_close(n(gb[0])[s:e], ref_g[0], 1e-4, 1e-6, "du sample")
     # parameter gradients are sums over the 32 batches: compare with the sum of per-batch oracle runs would be
     # costly; the ddt_active of dim d equals the sum over its channels of dΔ, checked through linearity:
     g2 = ssc.bwd_flat_ch(u, k, cu, int(ms), w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, 2.0 * dout, x, D=w.D_skip,
