@@ -17,6 +17,8 @@
 // (deterministic, no zero-fill of dy).
 #include "bcm_common.hpp"
 
+#include <mutex>
+
 namespace bcm {
 
 template <bool USE_LDS>
@@ -248,6 +250,36 @@ __global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_r
 
 static unsigned nblk(int64_t waves) { return (unsigned)((waves + 3) / 4); }
 
+// Scratch of the allocation-free restore backward (bcm_restore_bwd_noalloc):
+// the per-tile head / tail partials and tile end indices, 3 words per
+// (channel, tile), for up to BCM_RESTORE_BWD_NOALLOC_MAX_TILES of them
+// (8 MiB per device, held until the process ends). Each device holds its own
+// copy; host code uses the address that hipGetSymbolAddress gives for the
+// current device, never the array's name.
+constexpr int64_t kScratchWords = 3ll * BCM_RESTORE_BWD_NOALLOC_MAX_TILES;
+static __device__ __align__(256) float scratch[kScratchWords];
+
+// Device address of `scratch` on the current device, resolved once per
+// device (first call on it) and cached.
+static int scratch_ptr(float** out, const char* fn) {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+    return set_error(BCM_EHIP, "%s: no current HIP device", fn);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(BCM_EHIP, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+    ptrs[dev] = p;
+  }
+  *out = static_cast<float*>(ptrs[dev]);
+  return BCM_OK;
+}
+
 static int check_restore(const char* fn, const uint32_t* bitmask, int64_t mrd, const int32_t* tile_start,
                          int64_t n_rows, int64_t dim, int64_t L) {
   if (n_rows < 0 || dim < 1 || L < 1 || mrd < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
@@ -317,36 +349,80 @@ int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L) {
   return (n_rows < 0 || L < 1) ? 0 : 3 * 4 * n_rows * tile_count(L);
 }
 
-int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
-                    const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy, int64_t n_events,
-                    void* workspace, int64_t workspace_bytes, bcm_stream_t stream) {
-  const char* fn = "bcm_restore_bwd";
-  if (!dtype_ok(dtype)) return set_error(BCM_EINVAL, "%s: dout must be fp32/fp16/bf16", fn);
-  int rc = check_restore(fn, bitmask, mask_row_div, tile_start, n_rows, dim, L);
-  if (rc) return rc;
-  if (n_rows == 0) return BCM_OK;
-  if (!dout || (n_events > 0 && !dy) || n_events < 0) return set_error(BCM_EINVAL, "%s: null pointer", fn);
-  if (n_events * 4 > INT32_MAX) return set_error(BCM_EINVAL, "%s: dy must be below 2 GiB", fn);
+}  // extern "C"
+
+namespace bcm {
+
+// Checks shared by both restore backward entry points (0: go on; 1: done,
+// nothing to launch; negative: error code negated).
+static int restore_bwd_checks(const char* fn, const void* dout, int dtype, const uint32_t* bitmask,
+                              int64_t mask_row_div, const int32_t* tile_start, int64_t n_rows, int64_t dim,
+                              int64_t L, const float* dy, int64_t n_events) {
+  if (!dtype_ok(dtype)) return -set_error(BCM_EINVAL, "%s: dout must be fp32/fp16/bf16", fn);
+  const int rc = check_restore(fn, bitmask, mask_row_div, tile_start, n_rows, dim, L);
+  if (rc) return -rc;
+  if (n_rows == 0) return 1;
+  if (!dout || (n_events > 0 && !dy) || n_events < 0) return -set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_events * 4 > INT32_MAX) return -set_error(BCM_EINVAL, "%s: dy must be below 2 GiB", fn);
+  return 0;
+}
+
+// Tile pass and fix-up pass with the side arrays in `workspace` (3 words
+// per (channel, tile), fully written by the tile pass before the fix-up
+// reads them).
+static int restore_bwd_run(const char* fn, const void* dout, int dtype, const uint32_t* bitmask,
+                           int64_t mask_row_div, const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L,
+                           float* dy, int64_t n_events, float* workspace, hipStream_t stream) {
   const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
-  if (!workspace || workspace_bytes < bcm_restore_bwd_workspace_bytes(n_rows, L))
-    return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn,
-                     (long long)bcm_restore_bwd_workspace_bytes(n_rows, L));
-  float* head = static_cast<float*>(workspace);
+  float* head = workspace;
   float* tail = head + nT * n_rows;
   int32_t* tend = reinterpret_cast<int32_t*>(tail + nT * n_rows);
   const int64_t waves = (n_rows / dim) * nT * nG;
   if (waves > INT32_MAX / 2 || dim > (1 << 22)) return set_error(BCM_EINVAL, "%s: problem too large", fn);
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    hipLaunchKernelGGL(k_restore_bwd_tiles<T>, dim3(nblk(waves)), dim3(256), 0, hs(stream),
+    hipLaunchKernelGGL(k_restore_bwd_tiles<T>, dim3(nblk(waves)), dim3(256), 0, stream,
                        static_cast<const T*>(dout), n_events, bitmask, W, mask_row_div, tile_start, (int)nT,
                        (int)nG, (int)waves, (int)dim, L, n_rows, dy, head, tail, tend);
   });
-  rc = check_launch(fn);
+  const int rc = check_launch(fn);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, hs(stream),
+  hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, stream,
                      nT, n_rows, head, tail, tend, dy, n_events);
   return check_launch(fn);
+}
+
+}  // namespace bcm
+
+extern "C" {
+
+int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
+                    const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy, int64_t n_events,
+                    void* workspace, int64_t workspace_bytes, bcm_stream_t stream) {
+  const char* fn = "bcm_restore_bwd";
+  const int c = restore_bwd_checks(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events);
+  if (c) return c > 0 ? BCM_OK : -c;
+  if (!workspace || workspace_bytes < bcm_restore_bwd_workspace_bytes(n_rows, L))
+    return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn,
+                     (long long)bcm_restore_bwd_workspace_bytes(n_rows, L));
+  return restore_bwd_run(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events,
+                         static_cast<float*>(workspace), hs(stream));
+}
+
+int bcm_restore_bwd_noalloc(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
+                            const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy,
+                            int64_t n_events, bcm_stream_t stream) {
+  const char* fn = "bcm_restore_bwd_noalloc";
+  const int c = restore_bwd_checks(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events);
+  if (c) return c > 0 ? BCM_OK : -c;
+  if (n_rows * tile_count(L) > BCM_RESTORE_BWD_NOALLOC_MAX_TILES)
+    return set_error(BCM_EINVAL, "%s: n_rows * ceil(L / 64) = %lld exceeds the scratch limit of %lld", fn,
+                     (long long)(n_rows * tile_count(L)), (long long)BCM_RESTORE_BWD_NOALLOC_MAX_TILES);
+  float* ws = nullptr;
+  const int rc = scratch_ptr(&ws, fn);
+  if (rc) return rc;
+  return restore_bwd_run(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events, ws,
+                         hs(stream));
 }
 
 }  // extern "C"

@@ -409,6 +409,25 @@ int bcm_restore_bwd(const void* dout, int dtype, const uint32_t* bitmask,
                     int64_t n_events, void* workspace,
                     int64_t workspace_bytes, bcm_stream_t stream);
 
+/* Allocation-free variant of bcm_restore_bwd. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, checks and result as bcm_restore_bwd, without
+ * the workspace: the per-tile partials live in the library's own scratch,
+ * a static device array of 8 MiB per device, so n_rows * ceil(L / 64) must
+ * not exceed BCM_RESTORE_BWD_NOALLOC_MAX_TILES (checked; larger problems
+ * are refused with BCM_EINVAL). It calls no hipMalloc / hipFree. All calls
+ * on one device share that device's scratch: calls that overlap in time on
+ * one device (different streams, no ordering between them) race and must
+ * not be issued; calls in one stream are ordered and safe. Nothing in the
+ * scratch needs clearing between calls (the tile pass writes every entry
+ * the fix-up pass reads). */
+#define BCM_RESTORE_BWD_NOALLOC_MAX_TILES 699040
+int bcm_restore_bwd_noalloc(const void* dout, int dtype, const uint32_t* bitmask,
+                            int64_t mask_row_div, const int32_t* tile_start,
+                            int64_t n_rows, int64_t dim, int64_t L, float* dy,
+                            int64_t n_events, bcm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

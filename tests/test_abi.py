@@ -77,9 +77,22 @@ def test_scan_rows_arguments_are_rejected_before_launch(lib):
 
 def test_header_constants_match_binding():
     text = open(HEADER).read()
-    for name, value in (("BCM_ABI_VERSION", nat.ABI_VERSION), ("BCM_SCAN_SEQLEN_EXCEEDED", nat.SCAN_SEQLEN_EXCEEDED)):
+    for name, value in (("BCM_ABI_VERSION", nat.ABI_VERSION), ("BCM_SCAN_SEQLEN_EXCEEDED", nat.SCAN_SEQLEN_EXCEEDED),
+                        ("BCM_RESTORE_BWD_NOALLOC_MAX_TILES", nat.RESTORE_BWD_NOALLOC_MAX_TILES)):
         m = re.search(r"#define\s+%s\s+(\d+)" % name, text)
         assert m and int(m.group(1)) == value, name
+
+
+def test_restore_bwd_noalloc_rejects_before_launch(lib):
+    """The allocation-free restore backward refuses a problem larger than
+    its scratch (and invalid arguments) before touching the device."""
+    L = 2048
+    rows = nat.RESTORE_BWD_NOALLOC_MAX_TILES // nat.tile_count(L) + 1
+    rows += (-rows) % 64  # divisible by dim
+    assert lib.bcm_restore_bwd_noalloc(16, 0, 16, 1, 16, rows, 64, L, 16, 10, None) == 1
+    assert "scratch limit" in lib.bcm_last_error().decode()
+    assert lib.bcm_restore_bwd_noalloc(16, 9, 16, 1, 16, 64, 64, L, 16, 10, None) == 1
+    assert lib.bcm_last_error().decode().startswith("bcm_restore_bwd_noalloc")
 
 
 def test_host_helpers(lib):
