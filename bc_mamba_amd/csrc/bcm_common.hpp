@@ -118,6 +118,12 @@ __device__ __forceinline__ int wave_sum(int v) {
   return v;
 }
 
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) v |= __shfl_xor(v, m, kWave);
+  return v;
+}
+
 __device__ __forceinline__ int wave_max(int v) {
 #pragma unroll
   for (int m = kWave / 2; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, kWave));

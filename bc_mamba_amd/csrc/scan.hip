@@ -22,8 +22,9 @@
 //     registers, so no per-event cross-lane reduction is needed.
 //   * Decays come from a per-workgroup LDS table T[s][k] = exp2(clamp(Δ(k)·A
 //     ·log2e)) for gaps k <= 64 (built with the same expression as the
-//     per-event path, so the values are identical); a wave whose chunk holds
-//     a longer gap computes every decay directly for that chunk.
+//     per-event path, so the values are identical). In the backward, items
+//     with a longer gap compute their own decay, state by state, with the
+//     same expression; a forward chunk with one runs the exact path.
 //   * Scaled recurrences: the forward runs g = h / W_B (g = a·g + Δu²) and the
 //     backward e = dx / W_C (e = a'·e' + dout·u), so the per-item multiplies
 //     by W_B / W_C leave the inner loops; they reappear once per state in the
@@ -55,6 +56,7 @@ constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding 
 constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
 constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
 constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
+constexpr int kFixSlots = 4;        // backward: item slots with a long gap that the table path fixes up
 
 struct FwdLds {
   int N, nw, G, R, nslots;
@@ -352,6 +354,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
           if (s + 1 < N) state(s + 1, av1, av0, exact_tag);
         }
       };
+      // a chunk with a gap longer than the table (rare: 0.85^64 per event
+      // at 15 % density) runs the exact path
       if constexpr (TBL) {
         if (exact_blk || __any(big)) states(std::true_type{});
         else states(std::false_type{});
@@ -553,10 +557,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
         for (int r = 0; r < R; ++r) {
           const bool valid = r < nv;
           const int kk = __float_as_int(gkm[r]);
-          tb[r] = valid ? (uint32_t)kk * 4u : 0u;
+          // gaps past the table read its last entry; the state loop replaces it
+          tb[r] = valid ? (uint32_t)min(kk, kTabK) * 4u : 0u;
           dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
           gkm[r] = valid ? (float)(kk - 1) : 0.0f;
-          big |= (valid && kk > kTabK) ? 1 : 0;
+          big |= (valid && kk > kTabK) ? (1 << r) : 0;
           if (r < HR) Sa += dlv[r];
           else Sb += dlv[r];
           uvv[r] = gg[r];
@@ -596,10 +601,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
       // the state loop reads gkm through an index the compiler cannot see
       // through, so it re-reads LDS instead of keeping the stored values live
       const float* km = gkm + opaque(0);
+      // items with a gap longer than the table (k > kTabK) compute their
+      // decays directly, state by state, on the table path; bigm is the
+      // wave-uniform set of item slots that hold one in some lane
+      const uint32_t bigm = (uint32_t)__builtin_amdgcn_readfirstlane(wave_or(big));
       wave_sync();  // cg0 written by the group's lanes
       // ---- state loop; EXACT: decays computed per item, products multiplied out
-      auto states = [&](auto exact_tag) {
-        constexpr bool EXACT = decltype(exact_tag)::value;
+      // mode: 0 table, 1 table with the long-gap fix-up, 2 exact
+      auto states = [&](auto mode_tag) {
+        constexpr int MODE = decltype(mode_tag)::value;
+        constexpr bool EXACT = MODE == 2;
 #pragma unroll 1
         for (int s = 0; s < N; ++s) {
           const float Al = sAl[s], wbc = sWBC[s], wbca = sWBCA[s];
@@ -612,15 +623,21 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           // parallelism and joined with the scan operator.
           // forward: local folds, group scan, exact states (in registers)
           float Pa = 1.0f, Ha = 0.0f, Pb = 1.0f, Hb = 0.0f;
+          if (!EXACT) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) av[r] = tab(sT, row, tb[r]);
+            if constexpr (MODE == 1) {
+#pragma unroll
+              for (int r = 0; r < R; ++r)
+                if ((bigm & (1u << r)) && tb[r] && km[r] >= (float)kTabK) av[r] = decay(fmaf(dti, km[r], dta) * Al);
+            }
+          }
 #pragma unroll
           for (int i = 0; i < HR; ++i) {
             const int ra = i, rb = i + HR;
             if (EXACT) {
               av[ra] = decay((tb[ra] ? fmaf(dti, km[ra], dta) : 0.0f) * Al);
               av[rb] = decay((tb[rb] ? fmaf(dti, km[rb], dta) : 0.0f) * Al);
-            } else {
-              av[ra] = tab(sT, row, tb[ra]);
-              av[rb] = tab(sT, row, tb[rb]);
             }
             Ha = fmaf(av[ra], Ha, du2[ra]);
             Hb = fmaf(av[rb], Hb, du2[rb]);
@@ -716,11 +733,17 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
           }
         }
       };
+      using Table = std::integral_constant<int, 0>;
+      using TableFix = std::integral_constant<int, 1>;
+      using Exact = std::integral_constant<int, 2>;
+      // the fix-up pays per marked slot and state: with many marked slots
+      // (bursty events with long gaps) the exact path is cheaper
       if constexpr (TBL) {
-        if (exact_blk || __any(big)) states(std::true_type{});
-        else states(std::false_type{});
+        if (exact_blk || __builtin_popcount(bigm) > kFixSlots) states(Exact{});
+        else if (bigm) states(TableFix{});
+        else states(Table{});
       } else {
-        states(std::true_type{});
+        states(Exact{});
       }
       // ---- per item: du, dΔ -> ddt, dD (u and the gated dout staged again)
       wave_sync();
