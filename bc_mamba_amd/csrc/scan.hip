@@ -51,6 +51,7 @@ namespace bcm {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kScanThreads = 512;   // workgroup size bound (8 waves)
+template <int G, bool BWD> constexpr int kScanThreadsG = kScanThreads;
 constexpr int kTabK = 64;           // gaps k = 1..kTabK come from the decay table
 constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
 constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
@@ -148,7 +149,7 @@ __device__ __forceinline__ void report_seqlen(const bcm_scan_args& a, int n) {
 }
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
-__global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a) {
+__global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int C = G * R;
@@ -262,9 +263,6 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
         to_tiles();
       }
       wave_sync();
-      float uu[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) uu[r] = mine[r];
       float dl[R], du2[R], acc[R];
       uint32_t tb[R];  // byte offset of the item's gap in a table row (0: padding)
       int big = 0;
@@ -276,7 +274,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
         // padding items are identities of the scan: Δ = 0 -> a = 1, Δu² = 0
         const int km1 = valid ? kk - 1 : -1;
         dl[r] = valid ? fmaf(dti, (float)km1, dta) : 0.0f;
-        du2[r] = dl[r] * uu[r] * uu[r];
+        const float uv = mine[r];  // u stays in the tile (read again for the outputs)
+        du2[r] = dl[r] * uv * uv;
         tb[r] = (uint32_t)(km1 + 1) * 4u;
         big |= km1 >= kTabK ? 1 : 0;
         if (r < HR) Sa += dl[r];
@@ -365,7 +364,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd(const bcm_scan_args a
       // ---- outputs: y = D·u + u·Σ_s g·W_B·W_C (and y·silu(z)), stored row by row
       wave_sync();
 #pragma unroll
-      for (int r = 0; r < R; ++r) mine[r] = fmaf(Dv, uu[r], uu[r] * acc[r]);
+      for (int r = 0; r < R; ++r) {
+        const float uv = mine[r];
+        mine[r] = fmaf(Dv, uv, uv * acc[r]);
+      }
       wave_sync();
       {
         const int jo = opaque(j);
@@ -402,7 +404,7 @@ struct ScanRows {
 };
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL, bool DXR>
-__global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw) {
+__global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int RS = R + 1;
@@ -807,10 +809,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
     }
     if constexpr (DXR) {
       // dense gradient row of the channel (one pass: all of its du are in
-      // the group's k tile in event order). Lane j writes steps 4j..4j+3 of
-      // every 64-step tile (one tile per 16-lane store), taking its events
-      // from the tile's mask and the tile table; 0 between events
-      static_assert(4 * G == kTile, "one tile per group store");
+      // the group's k tile in event order). Each 16 lanes of the group take
+      // one 64-step tile per store, lane j writing steps 4(j%16)..+3 of it
+      // (TPS tiles per group store), taking its events from the tile's mask
+      // and the tile table; 0 between events
+      constexpr int TPS = G / 16;
+      static_assert(G == 16 || G == 32, "one or two tiles per group store");
       wave_sync();
       if (act) {
         // row and lane constants formed here (opaque: not hoisted into
@@ -820,7 +824,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
         const int32_t* tsr = rw.ts + row * (rw.nT + 1);
         T* dr = static_cast<T*>(rw.dx) + row * rw.L;
         const int L = (int)rw.L;
-        const int off = 4 * opaque(j);  // the lane's first step in a tile
+        const int jo = opaque(j);
+        const int jt = jo / 16;        // the lane's tile within a group store
+        const int off = 4 * (jo % 16);  // the lane's first step in a tile
         const uint32_t lo_keep = off >= 32 ? 0xFFFFFFFFu : (1u << off) - 1u;
         const uint32_t hi_keep = off > 32 ? (1u << (off - 32)) - 1u : 0u;
         const uint32_t sh = (uint32_t)off & 31u;
@@ -850,24 +856,51 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd(const bcm_scan_args a
             st_stream(*reinterpret_cast<u32x2*>(h), reinterpret_cast<u32x2*>(dr + t0));
           }
         };
-        constexpr int BAT = 8;
         const int nfull = L / kTile;  // tiles whose 64 steps are all < L
-        int q0 = 0;
-        for (; q0 + BAT <= nfull; q0 += BAT) {
+        if constexpr (TPS == 1) {
+          constexpr int BAT = 8;
+          int q0 = 0;
+          for (; q0 + BAT <= nfull; q0 += BAT) {
+            uint64_t m[BAT];
+            int32_t tv[BAT];
+#pragma unroll
+            for (int i = 0; i < BAT; ++i) {  // masks and table entries in flight together
+              m[i] = tile_mask(mrow, q0 + i);
+              tv[i] = tsr[q0 + i];
+            }
+#pragma unroll
+            for (int i = 0; i < BAT; ++i) seg(m[i], tv[i], (q0 + i) * kTile + off);
+          }
+          for (; q0 < nfull; ++q0) seg(tile_mask(mrow, q0), tsr[q0], q0 * kTile + off);
+        } else {
+        constexpr int BAT = 8 / TPS;  // group stores per batch
+        const int ngs = (nfull + TPS - 1) / TPS;  // group stores over the full tiles
+        // tile of group store g for this lane; past the full tiles it reads
+        // the last full tile and stores nothing
+        auto tile_of = [&](int g) { return g * TPS + jt; };
+        int g0 = 0;
+        for (; g0 + BAT <= ngs; g0 += BAT) {
           uint64_t m[BAT];
           int32_t tv[BAT];
 #pragma unroll
           for (int i = 0; i < BAT; ++i) {  // masks and table entries in flight together
-            m[i] = tile_mask(mrow, q0 + i);
-            tv[i] = tsr[q0 + i];
+            const int qt = min(tile_of(g0 + i), nfull - 1);
+            m[i] = tile_mask(mrow, qt);
+            tv[i] = tsr[qt];
           }
 #pragma unroll
-          for (int i = 0; i < BAT; ++i) seg(m[i], tv[i], (q0 + i) * kTile + off);
+          for (int i = 0; i < BAT; ++i)
+            if (tile_of(g0 + i) < nfull) seg(m[i], tv[i], tile_of(g0 + i) * kTile + off);
         }
-        for (; q0 < nfull; ++q0) seg(tile_mask(mrow, q0), tsr[q0], q0 * kTile + off);
+        for (; g0 < ngs; ++g0) {
+          const int qt = tile_of(g0);
+          if (qt < nfull) seg(tile_mask(mrow, qt), tsr[qt], qt * kTile + off);
+        }
+        }
         // a last partial tile (L % 64 != 0; L % 4 == 0, so a lane's 4 steps
-        // are all in range or all past the end)
-        if (nfull * kTile < L && nfull * kTile + off < L) seg(tile_mask(mrow, nfull), tsr[nfull], nfull * kTile + off);
+        // are all in range or all past the end), by the group's first 16 lanes
+        if (jt == 0 && nfull * kTile < L && nfull * kTile + off < L)
+          seg(tile_mask(mrow, nfull), tsr[nfull], nfull * kTile + off);
       }
     }
     if (b0 + b_step < n_per_d) {  // the next channel of this lane group
@@ -921,7 +954,8 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
   constexpr int CPW = kWave / G;
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
   int nw = (per_d + CPW - 1) / CPW;
-  nw = nw < 1 ? 1 : (nw > kScanThreads / kWave ? kScanThreads / kWave : nw);
+  constexpr int kMaxW = kScanThreadsG<G, BWD> / kWave;
+  nw = nw < 1 ? 1 : (nw > kMaxW ? kMaxW : nw);
   // the per-workgroup limit covers static and dynamic LDS together
   hipFuncAttributes fa{};
   const void* kfn = BWD ? reinterpret_cast<const void*>(&k_scan_bwd<G, R, T, Z, TBL, DXR>)
@@ -1014,7 +1048,7 @@ static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* ne
 // without z (the model's event path); rows_fusable() says when it applies.
 template <int G, int R, typename T, bool Z, bool BWD, bool TBL>
 static int launch_any(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q, const ScanRows* rw) {
-  if constexpr (BWD && !Z && G == 16) {
+  if constexpr (BWD && !Z && (G == 16 || G == 32)) {
     if (rw) return launch<G, R, T, Z, BWD, TBL, true>(a, s, fn, q, rw);
   }
   if (rw) return set_error(BCM_EINVAL, "%s: no fused dense-row backward for this shape", fn);
@@ -1024,7 +1058,8 @@ static int launch_any(const bcm_scan_args& a, hipStream_t s, const char* fn, Pla
 template <typename T, bool Z, bool BWD>
 static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q = nullptr,
                           const ScanRows* rw = nullptr) {
-  switch (pick_shape(a)) {
+  const ShapeId id = pick_shape(a);
+  switch (id) {
     case S16x4: return launch_any<16, 4, T, Z, BWD, true>(a, s, fn, q, rw);
     case S16x8: return launch_any<16, 8, T, Z, BWD, true>(a, s, fn, q, rw);
     case S16x16: return launch_any<16, 16, T, Z, BWD, true>(a, s, fn, q, rw);
@@ -1035,7 +1070,7 @@ static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn,
     default: break;
   }
   const bool tbl = a.dstate <= kTabMaxN;
-  if (pick_shape(a) == S64x16)
+  if (id == S64x16)
     return tbl ? launch_any<64, 16, T, Z, BWD, true>(a, s, fn, q, rw)
                : launch_any<64, 16, T, Z, BWD, false>(a, s, fn, q, rw);
   return tbl ? launch_any<64, 32, T, Z, BWD, true>(a, s, fn, q, rw)
@@ -1047,7 +1082,7 @@ static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn,
 // rows.
 static bool rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
   const ShapeId id = pick_shape(a);
-  if (kShapeG[id] != 16 || a.max_seqlen > kShapeG[id] * kShapeR[id] || a.z) return false;
+  if ((kShapeG[id] != 16 && kShapeG[id] != 32) || a.max_seqlen > kShapeG[id] * kShapeR[id] || a.z) return false;
   const uintptr_t p = reinterpret_cast<uintptr_t>(r.dx);
   return r.seqlen % 4 == 0 && p % (4 * dtype_size(a.dtype)) == 0;
 }

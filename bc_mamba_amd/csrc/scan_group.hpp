@@ -99,4 +99,49 @@ template <> struct Grp<16> {  // one DPP row per group: all cross-lane steps are
   }
 };
 
+// Two DPP rows per group (lanes 0-31 and 32-63 of the wave): the row steps
+// of Grp<16>, then one step across the row pair. Forward direction: the odd
+// row combines with the last lane of the even row (DPP row_bcast:15, rows 1
+// and 3 written). Backward direction: the even row combines with the first
+// lane of the odd row, read as a scalar (lanes 16 and 48).
+template <> struct Grp<32> {
+  static __device__ __forceinline__ int j() { return lane_id() & 31; }
+  static __device__ __forceinline__ bool odd_row() { return (lane_id() & 16) != 0; }
+  // scalar of lane 16 (group 0) or 48 (group 1), as seen by this lane
+  static __device__ __forceinline__ float pair_first(float v) {
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return lane_id() < 32 ? a : b;
+  }
+  static __device__ __forceinline__ void scan_up(float& P, float& H) {
+    Grp<16>::scan_up(P, H);
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 row_bcast:15 row_mask:0xa bank_mask:0xf" : "+v"(H) : "v"(P));
+    asm("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf" : "+v"(P));
+  }
+  static __device__ __forceinline__ void scan_down(float& Q, float& C) {
+    Grp<16>::scan_down(Q, C);
+    const float Qn = pair_first(Q), Cn = pair_first(C);
+    if (!odd_row()) {
+      C = fmaf(Q, Cn, C);
+      Q *= Qn;
+    }
+  }
+  static __device__ __forceinline__ float prev(float v, float first) {  // lane j-1; `first` in lane 0
+    const float in_row = dpp_mov<kRowShr + 1>(v, first);  // lane 16 keeps `first` here
+    const float from_prev_row = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(first), __float_as_int(v), 0x142, 0xA, 0xF, false));  // row_bcast:15
+    return j() == 16 ? from_prev_row : in_row;
+  }
+  static __device__ __forceinline__ float next(float v, float last) {  // lane j+1; `last` in lane 31
+    const float in_row = dpp_mov<kRowShl + 1>(v, last);  // lane 15 keeps `last` here
+    const float from_next_row = pair_first(v);
+    return j() == 15 ? from_next_row : in_row;
+  }
+  // the group's sum in every lane of its even row (lane 0 included)
+  static __device__ __forceinline__ float sum(float v) {
+    v = Grp<16>::sum(v);
+    return v + pair_first(v);
+  }
+};
+
 }  // namespace bcm
