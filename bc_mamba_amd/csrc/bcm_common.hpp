@@ -21,6 +21,10 @@ constexpr int kTile = 64;
 // Defined in abi.hip; thread-local so concurrent callers do not clobber it.
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* fn);
+// The restore backward's fix-up pass (restore.hip): closes the runs that
+// cross tiles from the per-(tile, channel) head / tail / last-event arrays.
+int restore_bwd_fix(int64_t nT, int64_t n_rows, const float* head, const float* tail, const int32_t* tend,
+                    float* dy, int64_t n_events, hipStream_t stream, const char* fn);
 // Zero fill with a kernel (abi.hip).
 int zero_bytes(void* ptr, int64_t bytes, hipStream_t s, const char* fn);
 

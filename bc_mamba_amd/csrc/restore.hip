@@ -353,6 +353,13 @@ int64_t bcm_restore_bwd_workspace_bytes(int64_t n_rows, int64_t L) {
 
 namespace bcm {
 
+int restore_bwd_fix(int64_t nT, int64_t n_rows, const float* head, const float* tail, const int32_t* tend,
+                    float* dy, int64_t n_events, hipStream_t stream, const char* fn) {
+  hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, stream, nT,
+                     n_rows, head, tail, tend, dy, n_events);
+  return check_launch(fn);
+}
+
 // Checks shared by both restore backward entry points (0: go on; 1: done,
 // nothing to launch; negative: error code negated).
 static int restore_bwd_checks(const char* fn, const void* dout, int dtype, const uint32_t* bitmask,
@@ -387,9 +394,7 @@ static int restore_bwd_run(const char* fn, const void* dout, int dtype, const ui
   });
   const int rc = check_launch(fn);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_restore_bwd_fix, dim3((unsigned)((nT * n_rows + 255) / 256)), dim3(256), 0, stream,
-                     nT, n_rows, head, tail, tend, dy, n_events);
-  return check_launch(fn);
+  return restore_bwd_fix(nT, n_rows, head, tail, tend, dy, n_events, stream, fn);
 }
 
 }  // namespace bcm

@@ -1,0 +1,481 @@
+// Stage 3 fused with the block's output projection: zero-order-hold restore
+// -> out_proj, forward and backward, without the dense restore output.
+//
+// Reference behaviour: e_model.py:499-504 (y_dense = restore_dense_fn(...);
+// out = self.out_proj(y_dense)), i.e. out[b, t, :] = W z[b, t, :] + bias with
+// z[b, t, d] = y of channel (b, d)'s last event at or before t (0 before its
+// first; restore_dense_fwd_kernel.cuh:38-114) and W [d_model, D] the
+// nn.Linear weight. Backward: dW = sum over (b, t) of dOut[b, t, :] (x)
+// z[b, t, :], dz = dOut W, and dy[e] = sum of dz over the steps event e owns
+// (restore_dense_bwd_kernel.cuh:42-112).
+//
+// MI355X design: z [B, L, D] and dz never exist in HBM. The products run on
+// the matrix cores at their fp32 rate (v_mfma_f32_32x32x2_f32), on 64 x 64
+// output tiles of 4 waves (32 x 32 each). The contraction index of MFMA step
+// s pairs the two lane halves h as k = 16 h + s, so each lane's operand run
+// is 16 consecutive elements of one row (or of one channel's steps).
+//  - forward: per (b, 64-step tile j, 64 output columns), z is generated 32
+//    channels at a time into LDS from the event index (one tile-mask
+//    popcount and one gather per element, no search), double-buffered
+//    against the MFMAs; W fragments come from L2.
+//  - dy: the dz tile [64 steps x 64 channels] = dOut tile W[:, channels] is
+//    staged once in LDS; one wave then runs the restore backward's sweep
+//    over it (runs closed inside the tile go to dy; head, tail and last
+//    event to the fix-up arrays) and the restore backward's fix-up pass
+//    closes the runs that cross tiles. No atomics.
+//  - dW: per (64 rows of W, 64 channels, one sequence segment of up to
+//    1024 steps) a partial dOut^T z, with z generated per lane from the
+//    event index (16 consecutive steps of one channel per MFMA operand run),
+//    then a fixed-order sum of the partials (deterministic).
+// fp32 throughout: the MFMA products are exact and accumulate in fp32, as
+// the reference's fp32 GEMM does (in another order).
+#include "bcm_common.hpp"
+
+namespace bcm {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kPT = 64;          // output tile edge
+constexpr int kKC = 32;          // contraction chunk (16 MFMA steps)
+constexpr int kRS = kKC + 4;     // LDS row stride of an operand chunk (16-byte rows, conflict-free 16-byte reads)
+constexpr int kDS = kPT + 1;     // LDS row stride of a dz tile
+constexpr int kSeg = 1024;       // sequence steps per dW partial
+
+__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Row of the 32 x 32 MFMA result held in register r of lane half h (the
+// column is the lane index mod 32).
+__device__ __forceinline__ int acc_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// z of one channel at step s (0..63) of a tile: the value of the last event
+// at or before s. m: the tile's event mask, tsj: index of the channel's first
+// event at or after the tile start, first: index of the channel's first
+// event (earlier indices belong to other channels: z = 0).
+__device__ __forceinline__ uint32_t zoh_off(uint64_t m, int s, int32_t tsj, int32_t first, bool ok) {
+  const int32_t idx = tsj + (int32_t)__popcll(m << (63 - s)) - 1;
+  return (ok && idx >= first) ? (uint32_t)idx * 4u : kBufOOB;
+}
+
+// ---------------------------------------------------------------- forward
+// Item (b, j, nb): out rows t0 = 64 j .. t0 + 63 of sequence b, columns
+// n0 = 64 nb .. n0 + 63. Wave w: rows 32 (w & 1), columns 32 (w >> 1).
+// The tile's index words of every channel (mask, first event at or after
+// the tile, first event of the channel) are staged in LDS once. Per
+// 32-channel chunk both operands are staged in LDS, rows of 36 floats
+// (double-buffered, one barrier per chunk): the W rows from coalesced row
+// loads, and z with lane = step, so each gather instruction reads one
+// channel's events of the tile (one or two cache lines). MFMA operand runs
+// are read 4 at a time (16-byte LDS reads, conflict-free at this stride).
+__global__ __launch_bounds__(256) void k_restore_proj_fwd(const float* __restrict__ y, int64_t n_events,
+                                                          const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                          int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                          int nT, int dim, int L, const float* __restrict__ weight,
+                                                          const float* __restrict__ bias, int dm, int nNB,
+                                                          float* __restrict__ out) {
+  extern __shared__ float4 s_dyn[];
+  float* sZ = reinterpret_cast<float*>(s_dyn);  // [2][64][kRS]: z chunk [step][channel]
+  float* sW = sZ + 2 * kPT * kRS;               // [2][64][kRS]: W chunk [row][channel]
+  uint4* sIdx = reinterpret_cast<uint4*>(sW + 2 * kPT * kRS);  // [dim]: mask lo, mask hi, tsj, first
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int nb = item % nNB, bj = item / nNB;
+  const int j = bj % nT, b = bj / nT;
+  const int t0 = j * kTile, n0 = nb * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rb = 32 * (w & 1), cb = 32 * (w >> 1);
+  const int li = lane & 31, h = lane >> 5;
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y, n_events * 4);
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(weight, (int64_t)dm * dim * 4);
+  for (int d = tid; d < dim; d += blockDim.x) {
+    const int64_t ch = (int64_t)b * dim + d;
+    const uint64_t m = tile_mask(bitmask + (ch / mrd) * Wd, j);
+    const int32_t* ts = tile_start + ch * (nT + 1);
+    sIdx[d] = make_uint4((uint32_t)m, (uint32_t)(m >> 32), (uint32_t)ts[j], (uint32_t)ts[0]);
+  }
+  __syncthreads();
+  // z: wave w stages channels 8w .. 8w + 7 of the chunk, lane = step
+  float zr[8];
+  auto gen = [&](int c) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int d = c * kKC + 8 * w + q;  // wave-uniform
+      const bool ok = d < dim;
+      const uint4 ix = sIdx[ok ? d : 0];
+      const uint64_t m = (uint64_t)ix.x | ((uint64_t)ix.y << 32);
+      zr[q] = buf_load<float>(ry, zoh_off(m, lane, (int32_t)ix.z, (int32_t)ix.w, ok));
+    }
+  };
+  // W: row (tid >> 3) + 32 i of the column tile, channels 4 (tid & 7) .. + 3
+  float4 wr[2];
+  const int wc = 4 * (tid & 7), wrow = tid >> 3;
+  auto wload = [&](int c) {
+    const int k = c * kKC + wc;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int n = n0 + wrow + 32 * i;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = buf_load<float>(rw, (n < dm && k + e < dim) ? (uint32_t)(n * dim + k + e) * 4u : kBufOOB);
+      wr[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  const int nK = (dim + kKC - 1) / kKC;
+  f32x16 acc = {};
+  gen(0);
+  wload(0);
+  for (int c = 0; c < nK; ++c) {
+    float* zb = sZ + (c & 1) * kPT * kRS;
+    float* wb = sW + (c & 1) * kPT * kRS;
+    *reinterpret_cast<float4*>(zb + lane * kRS + 8 * w) = make_float4(zr[0], zr[1], zr[2], zr[3]);
+    *reinterpret_cast<float4*>(zb + lane * kRS + 8 * w + 4) = make_float4(zr[4], zr[5], zr[6], zr[7]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<float4*>(wb + (wrow + 32 * i) * kRS + wc) = wr[i];
+    __syncthreads();  // chunk c staged; every wave is done with chunk c - 1's buffers
+    if (c + 1 < nK) {  // the next chunk's loads fly under this chunk's MFMAs
+      gen(c + 1);
+      wload(c + 1);
+    }
+    const float4* za = reinterpret_cast<const float4*>(zb + (rb + li) * kRS + 16 * h);
+    const float4* wa = reinterpret_cast<const float4*>(wb + (cb + li) * kRS + 16 * h);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 a = za[v], bq = wa[v];
+      acc = mfma32(a.x, bq.x, acc);
+      acc = mfma32(a.y, bq.y, acc);
+      acc = mfma32(a.z, bq.z, acc);
+      acc = mfma32(a.w, bq.w, acc);
+    }
+  }
+  // out[b, t0 + row, n]: lanes 0-31 and 32-63 each store a 128-byte row piece
+  const int n = n0 + cb + li;
+  const int64_t obase = ((int64_t)b * L + t0) * dm;
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out + obase, ((int64_t)(L - t0) * dm) * 4);
+  const float bv = (bias && n < dm) ? bias[n] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = rb + acc_row(r, h);
+    const bool ok = n < dm && t0 + row < L;
+    buf_store_f32(ro, ok ? (uint32_t)(row * dm + n) * 4u : kBufOOB, acc[r] + bv);
+  }
+}
+
+// ------------------------------------------------------------- dy (dz pass)
+// Item (b, j, db): dz rows t0 .. t0 + 63, channels d0 = 64 db .. + 63. Per
+// 32-row chunk of W: the dOut tile columns [step][k] from coalesced row
+// loads, and W [k][channel] transposed into [channel][k] on its way to LDS,
+// so both MFMA operand runs are 16-byte LDS reads (double-buffered, one
+// barrier per chunk).
+__global__ __launch_bounds__(256) void k_restore_proj_dy(const float* __restrict__ dout, int64_t n_events,
+                                                         const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                         int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                         int nT, int dim, int L, int64_t n_rows,
+                                                         const float* __restrict__ weight, int dm, int nDB,
+                                                         float* __restrict__ dy, float* __restrict__ head,
+                                                         float* __restrict__ tail, int32_t* __restrict__ tend) {
+  __shared__ float4 s_ab[2 * 2 * kPT * kRS / 4];
+  float* sA = reinterpret_cast<float*>(s_ab);  // [2][64][kRS]: dOut chunk [step][k]
+  float* sB = sA + 2 * kPT * kRS;              // [2][64][kRS]: W chunk [channel][k]
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int db = item % nDB, bj = item / nDB;
+  const int j = bj % nT, b = bj / nT;
+  const int t0 = j * kTile, d0 = db * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rb = 32 * (w & 1), cb = 32 * (w >> 1);
+  const int li = lane & 31, h = lane >> 5;
+  const int64_t gbase = ((int64_t)b * L + t0) * dm;
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + gbase, ((int64_t)(L - t0) * dm) * 4);
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(weight, (int64_t)dm * dim * 4);
+  // dOut: step (tid >> 3) + 32 i, columns 4 (tid & 7) .. + 3 of the chunk;
+  // W: row (tid >> 6) + 4 i of the chunk, channel tid & 63
+  const int ac = 4 * (tid & 7), ar = tid >> 3, bc = tid & 63, br = tid >> 6;
+  float4 av[2];
+  float bv[8];
+  auto load = [&](int c) {
+    const int k = c * kKC + ac;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = ar + 32 * i;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = buf_load<float>(rg, (t0 + row < L && k + e < dm) ? (uint32_t)(row * dm + k + e) * 4u : kBufOOB);
+      av[i] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    const int d = d0 + bc;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kr = c * kKC + br + 4 * i;
+      bv[i] = buf_load<float>(rw, (kr < dm && d < dim) ? (uint32_t)(kr * dim + d) * 4u : kBufOOB);
+    }
+  };
+  const int nK = (dm + kKC - 1) / kKC;
+  f32x16 acc = {};
+  load(0);
+  for (int c = 0; c < nK; ++c) {
+    float* ab = sA + (c & 1) * kPT * kRS;
+    float* bb = sB + (c & 1) * kPT * kRS;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<float4*>(ab + (ar + 32 * i) * kRS + ac) = av[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bb[bc * kRS + br + 4 * i] = bv[i];
+    __syncthreads();
+    if (c + 1 < nK) load(c + 1);
+    const float4* aa = reinterpret_cast<const float4*>(ab + (rb + li) * kRS + 16 * h);
+    const float4* ba = reinterpret_cast<const float4*>(bb + (cb + li) * kRS + 16 * h);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 a = aa[v], bq = ba[v];
+      acc = mfma32(a.x, bq.x, acc);
+      acc = mfma32(a.y, bq.y, acc);
+      acc = mfma32(a.z, bq.z, acc);
+      acc = mfma32(a.w, bq.w, acc);
+    }
+  }
+  // dz tile [64 steps][64 channels] in LDS (over the operand buffers)
+  __syncthreads();
+  float* sD = sA;
+  static_assert(4 * kPT * kRS >= kPT * kDS, "dz tile fits the operand buffers");
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sD[(rb + acc_row(r, h)) * kDS + cb + li] = acc[r];
+  __syncthreads();
+  if (w != 0) return;
+  // one wave: lane = channel d0 + lane, the restore backward's sweep over
+  // the tile's 64 steps (rows past L hold 0 and have no event bits)
+  const int dd = d0 + lane;
+  const bool ok = dd < dim;
+  const int64_t ch = (int64_t)b * dim + (ok ? dd : dim - 1);
+  const uint64_t m = ok ? tile_mask(bitmask + (ch / mrd) * Wd, j) : 0ull;
+  const int32_t elo = tile_start[ch * (nT + 1) + j];
+  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy, n_events * 4);
+  const int first = m ? __builtin_ctzll(m) : kTile;
+  uint32_t r = 0;  // events seen so far in the tile
+  float sum = 0.0f, hsum = 0.0f;
+  for (int s = 0; s < kTile; ++s) {
+    const float gv = sD[s * kDS + lane];
+    const uint32_t bit = (uint32_t)(m >> s) & 1u;
+    // the run of event elo + r - 1 closes here when r >= 1
+    buf_store_f32(rdy, (bit && r) ? (uint32_t)(elo + (int32_t)r - 1) * 4u : kBufOOB, sum);
+    r += bit;
+    sum = (bit ? 0.0f : sum) + gv;
+    hsum += s < first ? gv : 0.0f;
+  }
+  if (ok) {
+    const int64_t o = (int64_t)j * n_rows + ch;
+    head[o] = hsum;
+    tail[o] = sum;
+    tend[o] = r ? elo + (int32_t)r : -1;
+  }
+}
+
+// ----------------------------------------------------------- dW partials
+// Item (p = b * nSeg + seg, nb, db): rows n0 = 64 nb .. of dW, channels
+// d0 = 64 db .., the steps of segment seg of sequence b in 32-step chunks.
+// Wave w: W rows 32 (w & 1), channels 32 (w >> 1). Per chunk, dOut
+// (transposed to [row of W][step] on its way to LDS) and z ([channel][step],
+// lane = step: each gather reads one channel's events, two channels per
+// instruction) are staged in LDS, so both operand runs (along the steps)
+// are 16-byte LDS reads.
+__global__ __launch_bounds__(256) void k_restore_proj_dw(const float* __restrict__ dout,
+                                                         const float* __restrict__ y, int64_t n_events,
+                                                         const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                         int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                         int nT, int dim, int L, int dm, int nNB, int nDB,
+                                                         int nSeg, float* __restrict__ part) {
+  __shared__ float4 s_ab[2 * 2 * kPT * kRS / 4];
+  float* sA = reinterpret_cast<float*>(s_ab);  // [2][64][kRS]: dOut chunk [row of W][step]
+  float* sZ = sA + 2 * kPT * kRS;              // [2][64][kRS]: z chunk [channel][step]
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int db = item % nDB, r1 = item / nDB;
+  const int nb = r1 % nNB, p = r1 / nNB;
+  const int seg = p % nSeg, b = p / nSeg;
+  const int n0 = nb * kPT, d0 = db * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rb = 32 * (w & 1), cb = 32 * (w >> 1);
+  const int li = lane & 31, h = lane >> 5;
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + (int64_t)b * L * dm, (int64_t)L * dm * 4);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y, n_events * 4);
+  // dOut: step (tid >> 6) + 4 i of the chunk, row n0 + (tid & 63)
+  const int an = tid & 63, at = tid >> 6;
+  // z: lane step li, channels d0 + 32 h + 8 w + q
+  int32_t zfirst[8];
+  const int32_t* zts[8];
+  const uint32_t* zmrow[8];
+  bool zok[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int d = d0 + 32 * h + 8 * w + q;
+    zok[q] = d < dim;
+    const int64_t ch = (int64_t)b * dim + (zok[q] ? d : dim - 1);
+    zmrow[q] = bitmask + (ch / mrd) * Wd;
+    zts[q] = tile_start + ch * (nT + 1);
+    zfirst[q] = zts[q][0];
+  }
+  float ar_[8], zr[8];
+  auto load = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = t0 + at + 4 * i;
+      ar_[i] = buf_load<float>(rg, (t < L && n0 + an < dm) ? (uint32_t)(t * dm + n0 + an) * 4u : kBufOOB);
+    }
+    const int jt = t0 >> 6, so = (t0 & 63) + li;  // the chunk's 32 steps lie in tile jt
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint64_t m = zok[q] ? tile_mask(zmrow[q], jt) : 0ull;
+      zr[q] = buf_load<float>(ry, zoh_off(m, so, zts[q][jt], zfirst[q], zok[q]));
+    }
+  };
+  const int tb = seg * kSeg, te = min(L, tb + kSeg);
+  f32x16 acc = {};
+  load(tb);
+  for (int t0 = tb, c = 0; t0 < te; t0 += kKC, ++c) {
+    float* ab = sA + (c & 1) * kPT * kRS;
+    float* zb = sZ + (c & 1) * kPT * kRS;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ab[an * kRS + at + 4 * i] = ar_[i];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) zb[(32 * h + 8 * w + q) * kRS + li] = zr[q];
+    __syncthreads();
+    if (t0 + kKC < te) load(t0 + kKC);
+    const float4* aa = reinterpret_cast<const float4*>(ab + (rb + li) * kRS + 16 * h);
+    const float4* za = reinterpret_cast<const float4*>(zb + (cb + li) * kRS + 16 * h);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 a = aa[v], bq = za[v];
+      acc = mfma32(a.x, bq.x, acc);
+      acc = mfma32(a.y, bq.y, acc);
+      acc = mfma32(a.z, bq.z, acc);
+      acc = mfma32(a.w, bq.w, acc);
+    }
+  }
+  float* pp = part + (int64_t)p * dm * dim;
+  const int dc = d0 + cb + li;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int nr = n0 + rb + acc_row(r, h);
+    if (nr < dm && dc < dim) pp[(int64_t)nr * dim + dc] = acc[r];
+  }
+}
+
+// dW = sum of the partials in partial order.
+__global__ __launch_bounds__(256) void k_restore_proj_dw_sum(const float* __restrict__ part, int64_t n_parts,
+                                                             int64_t count, float* __restrict__ dw) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  float v = 0.0f;
+  int64_t q = 0;
+  for (; q + 4 <= n_parts; q += 4) {  // 4 loads in flight, summed in order
+    const float a0 = part[q * count + i], a1 = part[(q + 1) * count + i];
+    const float a2 = part[(q + 2) * count + i], a3 = part[(q + 3) * count + i];
+    v = (((v + a0) + a1) + a2) + a3;
+  }
+  for (; q < n_parts; ++q) v += part[q * count + i];
+  dw[i] = v;
+}
+
+struct ProjShape {
+  int64_t W, nT, nNB, nDB, nSeg, n_parts;
+};
+
+static ProjShape proj_shape(int64_t n_rows, int64_t dim, int64_t L, int64_t dm) {
+  ProjShape s;
+  s.W = bitmask_words(L);
+  s.nT = tile_count(L);
+  s.nNB = (dm + kPT - 1) / kPT;
+  s.nDB = (dim + kPT - 1) / kPT;
+  s.nSeg = (L + kSeg - 1) / kSeg;
+  s.n_parts = (n_rows / dim) * s.nSeg;
+  return s;
+}
+
+static int check_proj(const char* fn, const uint32_t* bitmask, int64_t mrd, const int32_t* tile_start,
+                      int64_t n_rows, int64_t dim, int64_t L, const float* weight, int64_t dm, int64_t n_events) {
+  if (n_rows < 0 || dim < 1 || L < 1 || mrd < 1 || dm < 1) return set_error(BCM_EINVAL, "%s: invalid sizes", fn);
+  if (n_rows % dim) return set_error(BCM_EINVAL, "%s: n_rows must be a multiple of dim", fn);
+  if (n_rows && (!bitmask || !tile_start || !weight)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  if (n_events < 0 || n_events * 4 > INT32_MAX) return set_error(BCM_EINVAL, "%s: n_events out of range", fn);
+  // 32-bit buffer offsets: one W, one sequence of dout / out
+  if (dm * dim * 4 > INT32_MAX || L * dm * 4 > INT32_MAX || n_rows / dim * tile_count(L) * ((dm + kPT - 1) / kPT) >
+                                                                 INT32_MAX / 2)
+    return set_error(BCM_EINVAL, "%s: problem too large", fn);
+  return BCM_OK;
+}
+
+}  // namespace bcm
+
+using namespace bcm;
+
+extern "C" {
+
+int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitmask, int64_t mask_row_div,
+                         const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, const float* weight,
+                         const float* bias, int64_t d_model, float* out, bcm_stream_t stream) {
+  const char* fn = "bcm_restore_proj_fwd";
+  int rc = check_proj(fn, bitmask, mask_row_div, tile_start, n_rows, dim, L, weight, d_model, n_events);
+  if (rc) return rc;
+  if (n_rows == 0) return BCM_OK;
+  if (!out || (n_events > 0 && !y)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
+  const ProjShape s = proj_shape(n_rows, dim, L, d_model);
+  const int64_t items = (n_rows / dim) * s.nT * s.nNB;
+  const size_t lds = (size_t)(4 * kPT * kRS) * 4 + (size_t)dim * 16;  // operand buffers + per-channel index words
+  if ((int64_t)lds > max_lds_bytes())
+    return set_error(BCM_EINVAL, "%s: dim %lld needs %lld bytes of LDS", fn, (long long)dim, (long long)lds);
+  hipLaunchKernelGGL(k_restore_proj_fwd, dim3((unsigned)items), dim3(256), lds, hs(stream), y, n_events, bitmask, s.W,
+                     mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, weight, bias, (int)d_model, (int)s.nNB,
+                     out);
+  return check_launch(fn);
+}
+
+int64_t bcm_restore_proj_bwd_workspace_bytes(int64_t n_rows, int64_t dim, int64_t L, int64_t d_model) {
+  if (n_rows < 0 || dim < 1 || L < 1 || d_model < 1) return 0;
+  const ProjShape s = proj_shape(n_rows, dim, L, d_model);
+  return 3 * 4 * n_rows * s.nT + 4 * s.n_parts * d_model * dim;
+}
+
+int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events, const uint32_t* bitmask,
+                         int64_t mask_row_div, const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L,
+                         const float* weight, int64_t d_model, float* dy, float* dweight, void* workspace,
+                         int64_t workspace_bytes, bcm_stream_t stream) {
+  const char* fn = "bcm_restore_proj_bwd";
+  int rc = check_proj(fn, bitmask, mask_row_div, tile_start, n_rows, dim, L, weight, d_model, n_events);
+  if (rc) return rc;
+  if (!dout && n_rows) return set_error(BCM_EINVAL, "%s: null dout", fn);
+  if (dweight && n_events > 0 && !y) return set_error(BCM_EINVAL, "%s: dweight needs y", fn);
+  const int64_t need = bcm_restore_proj_bwd_workspace_bytes(n_rows, dim, L, d_model);
+  if (!workspace || workspace_bytes < need)
+    return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn, (long long)need);
+  const ProjShape s = proj_shape(n_rows, dim, L, d_model);
+  const hipStream_t st = hs(stream);
+  const int64_t B = n_rows / dim;
+  if (B * s.nT * s.nDB > INT32_MAX / 2 || s.n_parts * s.nNB * s.nDB > INT32_MAX / 2)
+    return set_error(BCM_EINVAL, "%s: problem too large", fn);
+  float* head = static_cast<float*>(workspace);
+  float* tail = head + s.nT * n_rows;
+  int32_t* tend = reinterpret_cast<int32_t*>(tail + s.nT * n_rows);
+  float* part = reinterpret_cast<float*>(tend + s.nT * n_rows);
+  if (dy && n_events > 0) {
+    hipLaunchKernelGGL(k_restore_proj_dy, dim3((unsigned)(B * s.nT * s.nDB)), dim3(256), 0, st, dout, n_events,
+                       bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, n_rows, weight,
+                       (int)d_model, (int)s.nDB, dy, head, tail, tend);
+    if ((rc = check_launch(fn))) return rc;
+    if ((rc = restore_bwd_fix(s.nT, n_rows, head, tail, tend, dy, n_events, st, fn))) return rc;
+  }
+  if (dweight) {  // no tokens (n_parts = 0): the sum writes dW = 0
+    if (s.n_parts > 0)
+      hipLaunchKernelGGL(k_restore_proj_dw, dim3((unsigned)(s.n_parts * s.nNB * s.nDB)), dim3(256), 0, st, dout, y,
+                       n_events, bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, (int)d_model,
+                       (int)s.nNB, (int)s.nDB, (int)s.nSeg, part);
+    if ((rc = check_launch(fn))) return rc;
+    const int64_t count = d_model * dim;
+    hipLaunchKernelGGL(k_restore_proj_dw_sum, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, part,
+                       s.n_parts, count, dweight);
+    if ((rc = check_launch(fn))) return rc;
+  }
+  return BCM_OK;
+}
+
+}  // extern "C"

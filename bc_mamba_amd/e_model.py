@@ -16,7 +16,13 @@ prob_head) take their weight gradients as split-K products
 (`projections`). With `conv_at_events=True` (default) the depthwise
 conv + SiLU is evaluated only at the events, by the extraction itself, and
 its backward goes from du straight to the conv input's gradient: no dense
-x_conv exists in either direction. Results match the unfused composition
+x_conv exists in either direction. With `fused_out_proj=True` (default; fp32)
+the restore and out_proj run as one op reading the event index: the dense
+restore output is not kept for the backward and its gradient is never
+formed (the input gradient of out_proj and the restore backward are one
+kernel); `fused_out_proj="mfma"` also runs the forward and the weight
+gradient as this package's matrix-core kernels, with no dense restore output
+at all. Results match the unfused composition
 (forward values identical; the conv weight gradients up to summation
 order).
 
@@ -234,6 +240,49 @@ class _IndexedRestoreFn(torch.autograd.Function):
         return dy, None, None, None, None
 
 
+class _IndexedRestoreProjFn(torch.autograd.Function):
+    """The restore followed by out_proj in one op, reading the event index of
+    the fused extraction. The dense restore output z [B, L, d_inner] is not
+    kept for the backward and its gradient dz is never formed: dy comes from
+    one kernel that computes dz tile by tile on the matrix cores and runs
+    the restore backward's sweep on it (bcm_restore_proj_bwd).
+
+    mode "gemm": z is formed for the forward GEMM (and again for the weight
+    gradient's split-K GEMM) and freed, hipBLASLt runs the two products.
+    mode "mfma": the forward and the weight gradient also run as this
+    package's kernels, with z generated from the event index inside them
+    (bcm_restore_proj_fwd, bcm_restore_proj_bwd): no dense z at all.
+    Same result as projections.linear(_IndexedRestoreFn.apply(...), weight,
+    bias), in another fp32 summation order."""
+
+    @staticmethod
+    def forward(ctx, y_flat, weight, bias, event_index, n_ch: int, dim: int, seqlen: int, mode: str):
+        ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen, ctx.mode = event_index, n_ch, dim, seqlen, mode
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(y_flat, weight)
+        if mode == "mfma":
+            return restore_dense_cuda_nodecay.restore_proj_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen,
+                                                                        weight, bias)
+        z = restore_dense_cuda_nodecay.restore_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen)
+        return F.linear(z, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dout):
+        y_flat, weight = ctx.saved_tensors
+        mfma = ctx.mode == "mfma"
+        need_dy, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dout = dout.contiguous()
+        with cuda_stage("restore_backward"):
+            dy, dw = restore_dense_cuda_nodecay.restore_proj_bwd_indexed(
+                dout, y_flat, ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen, weight, need_dy=need_dy,
+                need_dw=need_dw and mfma)
+        if need_dw and not mfma:
+            z = restore_dense_cuda_nodecay.restore_fwd_indexed(y_flat, ctx.event_index, ctx.n_ch, ctx.dim, ctx.seqlen)
+            dw = projections.weight_grad(dout.reshape(-1, dout.size(-1)), z.reshape(-1, ctx.dim))
+        db = dout.sum((0, 1)) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dy, dw, db, None, None, None, None, None
+
+
 class TwoLevelDelta(nn.Module):
     """Per-channel idle / active steps: dt = softplus(a) + eps (e_model.py:210-230)."""
 
@@ -322,7 +371,7 @@ class Mamba(nn.Module):
                  dt_init="random", dt_scale=1.0, dt_init_floor=1e-4, conv_bias=True, bias=False,
                  use_fast_path=False, spiking=True, spike_mode="ste", prob_activation="sigmoid",
                  sample_inference=False, threshold=0.5, layer_idx=None, device=None, dtype=None,
-                 fused_event_path=True, conv_at_events=True):
+                 fused_event_path=True, conv_at_events=True, fused_out_proj=True):
         factory_kwargs = {"device": device, "dtype": dtype}
         super().__init__()
         self.d_model, self.d_state, self.d_conv, self.expand = d_model, d_state, d_conv, expand
@@ -338,6 +387,7 @@ class Mamba(nn.Module):
         self.scan_impl = "flat_ch"
         self.fused_event_path = fused_event_path
         self.conv_at_events = conv_at_events
+        self.fused_out_proj = fused_out_proj
 
         self.in_proj = nn.Linear(self.d_model, self.d_inner, bias=bias, **factory_kwargs)
         self.conv1d = nn.Conv1d(in_channels=self.d_inner, out_channels=self.d_inner, bias=conv_bias,
@@ -404,6 +454,14 @@ class Mamba(nn.Module):
                 and x.stride(0) % 4 == 0 and x.stride(1) % 4 == 0 and x.data_ptr() % (4 * es) == 0 and rows_apart
                 and self.d_conv <= 8 and x.dtype in (torch.float32, torch.float16, torch.bfloat16))
 
+    def _restore_proj_ok(self, y_flat, seqlen):
+        """The restore -> out_proj op applies (fp32, 32-bit offsets)."""
+        w, b = self.out_proj.weight, self.out_proj.bias
+        f32 = torch.float32
+        return (self.fused_out_proj and y_flat.dtype == f32 and w.dtype == f32 and w.is_contiguous()
+                and (b is None or b.dtype == f32) and y_flat.numel() * 4 < 2 ** 31
+                and seqlen * self.d_model * 4 < 2 ** 31 and self.d_model * self.d_inner * 4 < 2 ** 31)
+
     def forward(self, hidden_states, inference_params=None):
         if inference_params is not None:
             raise RuntimeError("Mamba: the decode / inference-cache path is not part of the event-path build")
@@ -453,6 +511,10 @@ class Mamba(nn.Module):
                                                       tile_chunk_size=0, is_depthwise_bc=True, pw_B=None,
                                                       pw_C=None)
         with cuda_stage("dense_restoration_forward"):
+            if self.fused_event_path and self._restore_proj_ok(y_flat, seqlen):
+                return _IndexedRestoreProjFn.apply(y_flat, self.out_proj.weight, self.out_proj.bias, event_index,
+                                                   n_ch, self.d_inner, seqlen,
+                                                   "mfma" if self.fused_out_proj == "mfma" else "gemm")
             if self.fused_event_path:
                 y_dense = _IndexedRestoreFn.apply(y_flat, event_index, n_ch, self.d_inner, seqlen)
             else:

@@ -20,7 +20,7 @@ except ImportError:  # imported with this directory on sys.path
     import _native as _nat
 
 __all__ = ["restore_dense_fwd", "restore_dense_bwd", "build_event_index", "restore_fwd_indexed",
-           "restore_bwd_indexed"]
+           "restore_bwd_indexed", "restore_proj_fwd_indexed", "restore_proj_bwd_indexed"]
 
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 
@@ -66,6 +66,40 @@ def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy):
               4 * ws.numel(),
               _nat.stream_of(dout))
     return dy
+
+
+def restore_proj_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen, weight, bias=None):
+    """The restore followed by the block's out_proj, without the dense
+    restore output (bcm_restore_proj_fwd): F.linear(restore(y_flat), weight,
+    bias) as (B, L, d_model) float32. fp32 y_flat, weight and bias."""
+    fn = "restore_proj_fwd_indexed"
+    _check(y_flat.dtype == torch.float32 and weight.dtype == torch.float32, f"{fn}: fp32 y_flat and weight")
+    _check(bias is None or bias.dtype == torch.float32, f"{fn}: fp32 bias")
+    _check(weight.dim() == 2 and weight.size(1) == dim and weight.is_contiguous(), f"{fn}: weight [d_model, dim]")
+    bitmask, tile_start, mrd = event_index
+    dm = weight.size(0)
+    out = torch.empty((n_ch // dim, seqlen, dm), dtype=torch.float32, device=y_flat.device)
+    _nat.call("bcm_restore_proj_fwd", _nat.ptr(y_flat), int(y_flat.numel()), _nat.ptr(bitmask), int(mrd),
+              _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(weight),
+              _nat.ptr(bias.contiguous()) if bias is not None else None, dm, _nat.ptr(out), _nat.stream_of(y_flat))
+    return out
+
+
+def restore_proj_bwd_indexed(dout, y_flat, event_index, n_ch, dim, seqlen, weight, need_dy=True, need_dw=True):
+    """Backward of restore_proj_fwd_indexed (bcm_restore_proj_bwd) from dout
+    (B, L, d_model): (dy float32 [E] or None, dweight [d_model, dim] or
+    None). The bias gradient is dout's column sum (not computed here)."""
+    bitmask, tile_start, mrd = event_index
+    dout = dout.contiguous()
+    dm = weight.size(0)
+    ws = torch.empty(max(4, _nat.lib().bcm_restore_proj_bwd_workspace_bytes(n_ch, int(dim), int(seqlen), dm)) // 4,
+                     dtype=torch.float32, device=dout.device)
+    dy = torch.empty(y_flat.numel(), dtype=torch.float32, device=dout.device) if need_dy else None
+    dw = torch.empty_like(weight) if need_dw else None
+    _nat.call("bcm_restore_proj_bwd", _nat.ptr(dout), _nat.ptr(y_flat), int(y_flat.numel()), _nat.ptr(bitmask),
+              int(mrd), _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(weight), dm, _nat.ptr(dy),
+              _nat.ptr(dw), _nat.ptr(ws), 4 * ws.numel(), _nat.stream_of(dout))
+    return dy, dw
 
 
 def restore_dense_fwd(y_flat, time_steps, cu_seqlens, dim, seqlen, out_dtype=None):

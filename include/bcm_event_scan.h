@@ -428,6 +428,42 @@ int bcm_restore_bwd_noalloc(const void* dout, int dtype, const uint32_t* bitmask
                             int64_t n_rows, int64_t dim, int64_t L, float* dy,
                             int64_t n_events, bcm_stream_t stream);
 
+/* ---- (3') restore -> out_proj ------------------------------------------- */
+/* The block's restore followed by its output projection (e_model.py:499-504:
+ * y_dense = restore_dense_fn(y_flat, ...); out = self.out_proj(y_dense)),
+ * without the dense restore output: out[b, t, :] = weight z[b, t, :] + bias
+ * with z[b, t, d] the zero-order hold of bcm_restore_fwd. fp32 throughout;
+ * weight is the nn.Linear weight [d_model, dim] (row-major), bias [d_model]
+ * or NULL, out (n_rows/dim, L, d_model) is fully written. n_events * 4 must
+ * stay below 2 GiB. */
+int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitmask,
+                         int64_t mask_row_div, const int32_t* tile_start,
+                         int64_t n_rows, int64_t dim, int64_t L,
+                         const float* weight, const float* bias, int64_t d_model,
+                         float* out, bcm_stream_t stream);
+
+/* Workspace of bcm_restore_proj_bwd: the restore backward's per-tile
+ * arrays (3 * 4 * n_rows * tile_count(L)) and the weight gradient's
+ * partials (4 * d_model * dim per (sequence, 1024-step segment)). */
+int64_t bcm_restore_proj_bwd_workspace_bytes(int64_t n_rows, int64_t dim, int64_t L,
+                                             int64_t d_model);
+
+/* Backward of bcm_restore_proj_fwd (the out_proj backward of the
+ * reference's nn.Linear, then RestoreDenseFn.backward, e_model.py:146-157,
+ * restore_dense_bwd_kernel.cuh:42-112), from dout (n_rows/dim, L, d_model):
+ *   dy[e]   = sum over t in [t_e, t_next) of (dout[b, t, :] . weight[:, d]),
+ *             float32, every event written once (no zero-init, no atomics);
+ *   dweight = sum over (b, t) of dout[b, t, :] (x) z[b, t, :], [d_model, dim]
+ *             (fully written; partials summed in a fixed order).
+ * dy or dweight may be NULL to skip it; y is needed for dweight. The bias
+ * gradient (the column sums of dout) is not computed here. */
+int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events,
+                         const uint32_t* bitmask, int64_t mask_row_div,
+                         const int32_t* tile_start, int64_t n_rows, int64_t dim,
+                         int64_t L, const float* weight, int64_t d_model, float* dy,
+                         float* dweight, void* workspace, int64_t workspace_bytes,
+                         bcm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

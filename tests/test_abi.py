@@ -95,6 +95,25 @@ def test_restore_bwd_noalloc_rejects_before_launch(lib):
     assert lib.bcm_last_error().decode().startswith("bcm_restore_bwd_noalloc")
 
 
+def test_restore_proj_checks_before_launch(lib):
+    """The fused restore -> out_proj entry points: workspace size formula
+    (fix-up arrays + one d_model x dim partial per 1024-step segment of each
+    sequence) and argument errors raised before any launch."""
+    n_rows, dim, L, dm = 128, 64, 1100, 32
+    nT, n_parts = nat.tile_count(L), (n_rows // dim) * 2
+    ws = lib.bcm_restore_proj_bwd_workspace_bytes(n_rows, dim, L, dm)
+    assert ws == 3 * 4 * n_rows * nT + 4 * n_parts * dm * dim
+    assert lib.bcm_restore_proj_bwd_workspace_bytes(n_rows, 0, L, dm) == 0
+    # n_rows not a multiple of dim, d_model < 1
+    assert lib.bcm_restore_proj_fwd(16, 10, 16, 1, 16, 100, 64, L, 16, None, dm, 16, None) == 1
+    assert "multiple of dim" in lib.bcm_last_error().decode()
+    assert lib.bcm_restore_proj_fwd(16, 10, 16, 1, 16, n_rows, dim, L, 16, None, 0, 16, None) == 1
+    assert lib.bcm_last_error().decode().startswith("bcm_restore_proj_fwd")
+    # workspace one byte short
+    assert lib.bcm_restore_proj_bwd(16, 16, 10, 16, 1, 16, n_rows, dim, L, 16, dm, 16, 16, 16, ws - 1, None) == 1
+    assert "workspace" in lib.bcm_last_error().decode()
+
+
 def test_host_helpers(lib):
     assert lib.bcm_abi_version() == nat.ABI_VERSION == 3
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64

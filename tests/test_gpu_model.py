@@ -3,9 +3,10 @@ against the float64 oracle composition (oracle/block.py: torch float64
 dense parts around the numpy oracle's extraction, gather, scan and restore).
 
   block    the fused block (spike-bits head, conv at the events, indexed
-           extraction / scan / restore, split-K projections) with expand 1
-           and 2: output and every parameter and input gradient at the fp32
-           bar (rtol 1e-4, floor 1e-6 * max|ref|)
+           extraction / scan, the restore -> out_proj op in both modes,
+           split-K projections) with expand 1 and 2: output and every
+           parameter and input gradient at the fp32 bar (rtol 1e-4, floor
+           1e-6 * max|ref|)
   config 4 one full-size training step (B50 L1024, d_model 256, d_inner
            512, 6 layers): finite loss and gradients, the loss of the
            reference composition (fused_event_path=False), every layer's
@@ -30,14 +31,16 @@ def _grads(blk, h):
     return g
 
 
-@pytest.mark.parametrize("expand", [1, 2])
-def test_mamba_block_matches_oracle(cuda_device, expand):
+@pytest.mark.parametrize("expand,out_proj", [(1, True), (2, True), (2, "mfma")])
+def test_mamba_block_matches_oracle(cuda_device, expand, out_proj):
     """The fused block behind its spike head, against the float64 oracle
     composition on the same parameters: same spikes, then output and every
     gradient (in_proj, conv weight / bias, W_BC, A_log, D, the two dt
-    levels, out_proj, prob_head, and the head's input)."""
+    levels, out_proj, prob_head, and the head's input). out_proj: the
+    restore -> out_proj op's mode (hipBLASLt products around the fused dy
+    kernel, or all three of this package's matrix-core kernels)."""
     torch.manual_seed(0)
-    blk = e_model.Mamba(d_model=32, d_state=16, expand=expand, device=cuda_device)
+    blk = e_model.Mamba(d_model=32, d_state=16, expand=expand, device=cuda_device, fused_out_proj=out_proj)
     with torch.no_grad():  # non-trivial values where the initialisation is flat
         blk.W_BC.normal_(0.0, 0.3)
         blk.D.uniform_(0.5, 1.5)
