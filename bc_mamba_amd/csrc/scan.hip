@@ -460,12 +460,13 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
   // to their tiles at the transposed positions (opaque(): positions are not
   // hoisted and held in registers); they are issued one chunk ahead (the
   // first before the parameter set-up, the next after a chunk's last use of
-  // the tiles), so their latency overlaps other work. dout is loaded at the
-  // top of its chunk and goes through the u tile once u has been read.
+  // the tiles), so their latency overlaps other work. dout is loaded with
+  // them and held in registers until the chunk's set-up has read u; it then
+  // goes through the u tile.
   // Items past the channel's events load the next channel's values (or 0
   // past E): they are padding, whose Δ and dout·u the item set-up forces to
   // 0, and their outputs are never stored.
-  float rawu[R];
+  float rawu[R], rawd[R];
   int rawk[R];
   const TilePos<G, R> tp(j);
   auto issue = [&](int e0, int n, int c) {
@@ -475,6 +476,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
     for (int q = 0; q < R; ++q) {
       rawk[q] = buf_load_i32(rk, (eb + (uint32_t)(q * G)) * 4u);
       rawu[q] = buf_load<T>(ru, (eb + (uint32_t)(q * G)) * SZ);
+      rawd[q] = buf_load<T>(rdo, (eb + (uint32_t)(q * G)) * SZ);
     }
   };
   auto to_tiles = [&]() {
@@ -551,9 +553,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
         // ---- k (-> k-1 in place) and u from their tiles, then the gated
         // dout through the u tile (dz on the way)
         const int jo = opaque(j);
-        float dlv[R], uvv[R], rawd[R];
-#pragma unroll
-        for (int q = 0; q < R; ++q) rawd[q] = buf_load<T>(rdo, (eb + (uint32_t)(q * G + jo)) * SZ);
+        float dlv[R], uvv[R];
         wave_sync();
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -584,6 +584,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
             dv *= zv * sg;
           }
           tp.at(tile, q) = dv;
+          rawd[q] = 0.0f;  // consumed: not live into the state loop on any path
         }
         wave_sync();
 #pragma unroll
