@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void k_conv_bwd(const T* __restrict__ x, const
           if (k < K) pre = fmaf(wk[k], xv[PRE + i - (K - 1) + k], pre);
         if (SILU) {
           const float sg = 1.0f / (1.0f + __expf(-pre));
-          g[i] = go[i] * sg * (1.0f + pre * (1.0f - sg));
+          g[i] = go[i] * sg * fmaf(pre, 1.0f - sg, 1.0f);  // one rounding, in both conv backwards
         } else {
           g[i] = go[i];
         }
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256) void k_conv_bwd_events(
         float gv = dv[q][k];
         if (SILU) {
           const float sgm = 1.0f / (1.0f + __expf(-pre));
-          gv = dv[q][k] * sgm * (1.0f + pre * (1.0f - sgm));
+          gv = dv[q][k] * sgm * fmaf(pre, 1.0f - sgm, 1.0f);  // as k_conv_bwd: one rounding
         }
         g[k] = ((nib[q] >> k) & 1u) ? gv : 0.0f;
       }
