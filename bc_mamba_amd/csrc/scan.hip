@@ -58,6 +58,8 @@ constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
 constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
 constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
 constexpr int kFixSlots = 4;        // backward: item slots with a long gap that the table path fixes up
+constexpr int kFixMinR = 16;        // ... in shapes of at least this many items per lane (the fix-up's
+                                    // registers would cost R = 8 its fourth wave per SIMD)
 
 struct FwdLds {
   int N, nw, G, R, nslots;
@@ -559,8 +561,9 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
         for (int r = 0; r < R; ++r) {
           const bool valid = r < nv;
           const int kk = __float_as_int(gkm[r]);
-          // gaps past the table read its last entry; the state loop replaces it
-          tb[r] = valid ? (uint32_t)min(kk, kTabK) * 4u : 0u;
+          // with the fix-up, gaps past the table read its last entry and the
+          // state loop replaces it; without it such a chunk runs the exact path
+          tb[r] = valid ? (uint32_t)(R >= kFixMinR ? min(kk, kTabK) : kk) * 4u : 0u;
           dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
           gkm[r] = valid ? (float)(kk - 1) : 0.0f;
           big |= (valid && kk > kTabK) ? (1 << r) : 0;
@@ -606,8 +609,10 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
       const float* km = gkm + opaque(0);
       // items with a gap longer than the table (k > kTabK) compute their
       // decays directly, state by state, on the table path; bigm is the
-      // wave-uniform set of item slots that hold one in some lane
-      const uint32_t bigm = (uint32_t)__builtin_amdgcn_readfirstlane(wave_or(big));
+      // wave-uniform set of item slots that hold one in some lane (shapes
+      // without the fix-up: nonzero when some lane holds one)
+      const uint32_t bigm =
+          R >= kFixMinR ? (uint32_t)__builtin_amdgcn_readfirstlane(wave_or(big)) : (uint32_t)__any(big);
       wave_sync();  // cg0 written by the group's lanes
       // ---- state loop; EXACT: decays computed per item, products multiplied out
       // mode: 0 table, 1 table with the long-gap fix-up, 2 exact
@@ -741,9 +746,12 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
       using Exact = std::integral_constant<int, 2>;
       // the fix-up pays per marked slot and state: with many marked slots
       // (bursty events with long gaps) the exact path is cheaper
-      if constexpr (TBL) {
+      if constexpr (TBL && R >= kFixMinR) {
         if (exact_blk || __builtin_popcount(bigm) > kFixSlots) states(Exact{});
         else if (bigm) states(TableFix{});
+        else states(Table{});
+      } else if constexpr (TBL) {
+        if (exact_blk || bigm) states(Exact{});
         else states(Table{});
       } else {
         states(Exact{});

@@ -194,6 +194,10 @@ def main():
     ap.add_argument("--api", action="store_true", help="also time the drop-in Python API path (autograd)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure the dominant kernel's HBM bytes")
+    ap.add_argument("--out-proj", choices=["gemm", "mfma", "off"], default="gemm",
+                    help="config 4: the blocks' restore -> out_proj op (default gemm; off: restore then linear)")
+    ap.add_argument("--no-peak", action="store_true",
+                    help="config 4: skip the peak-memory steps (fused and reference composition) after timing")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -308,6 +312,9 @@ def model_step_bench(args, dev):
     import torch
     from bc_mamba_amd.workloads import make_model_workload
     model, tokens, labels = make_model_workload(device=dev)
+    mode = {"gemm": True, "mfma": "mfma", "off": False}[args.out_proj]
+    for blk in model.blocks:
+        blk.core.fused_out_proj = mode
     events = []
     hooks = [blk.core.register_forward_pre_hook(
         lambda mod, inp: events.append(int((inp[0] > mod.threshold).sum()) * mod.expand)) for blk in model.blocks]
@@ -331,14 +338,14 @@ def model_step_bench(args, dev):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    peak = peak_memory(model, step)
+    peak = None if args.no_peak else peak_memory(model, step)
     return {
         "metric": METRIC, "value": E / (ms * 1e-3), "unit": "events/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": "config 4: 6-layer model training step (fwd + CE loss + bwd), d_model 256, "
                                "d_inner 512, N 16, L 1024, B 50, byte tokens, random init",
-                   "events_per_step": E, "events_per_layer": per_layer,
+                   "out_proj": args.out_proj, "events_per_step": E, "events_per_layer": per_layer,
                    "density_per_layer": [e / (50 * 1024 * 512) for e in per_layer]},
         "peak_memory_bytes": peak,
         "roofline": None,
