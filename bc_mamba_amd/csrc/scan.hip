@@ -756,34 +756,27 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
       } else {
         states(Exact{});
       }
-      // ---- per item: du, dΔ -> ddt, dD (u and the gated dout staged again)
+      // ---- per item: du, dΔ -> ddt, dD. The gated dout is still in the u
+      // tile from the set-up (the state loop does not touch it); u is loaded
+      // again and staged through the k tile once k-1 is in registers.
       wave_sync();
       {
         const int jo = opaque(j);
-        float uvv[R], fu[R], fd[R];
+        float uvv[R], fu[R], kmr[R];
 #pragma unroll
-        for (int q = 0; q < R; ++q) {  // both loads in flight together
-          const uint32_t off = (eb + (uint32_t)(q * G + jo)) * SZ;
-          fu[q] = buf_load<T>(ru, off);
-          fd[q] = buf_load<T>(rdo, off);
-          if (HAS_Z) {
-            const float zv = buf_load<T>(rz, off);
-            fd[q] *= zv / (1.0f + __expf(-zv));
-          }
-        }
+        for (int q = 0; q < R; ++q) fu[q] = buf_load<T>(ru, (eb + (uint32_t)(q * G + jo)) * SZ);
 #pragma unroll
-        for (int q = 0; q < R; ++q) tp.at(tile, q) = fu[q];
+        for (int r = 0; r < R; ++r) kmr[r] = gkm[r];
         wave_sync();
 #pragma unroll
-        for (int r = 0; r < R; ++r) uvv[r] = gg[r];
+        for (int q = 0; q < R; ++q) tp.at(tilek, q) = fu[q];
         wave_sync();
 #pragma unroll
-        for (int q = 0; q < R; ++q) tp.at(tile, q) = fd[q];
-        wave_sync();
+        for (int r = 0; r < R; ++r) uvv[r] = gkm[r];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const float uv = uvv[r];
-          const float km1 = gkm[r];
+          const float km1 = kmr[r];
           const float dlr = tb[r] ? fmaf(dti, km1, dta) : 0.0f;
           const float duv = fmaf(gg[r], Dv + acc2[r], 2.0f * dlr * uv * acc1[r]);
           const float dd = uv * uv * acc1[r];  // the A-term of dΔ went into ddt in the state loop
