@@ -92,6 +92,19 @@ def test_restore_shape_checks(fake_cuda):
         rd.restore_dense_fwd(torch.zeros(4, dtype=torch.bfloat16), t, cu, 1, 8, torch.float32)
 
 
+def test_restore_proj_checks():
+    """The restore -> out_proj op is fp32 with the nn.Linear weight layout;
+    other inputs are refused before any device work."""
+    idx = (torch.zeros(2, 32, dtype=i32), torch.zeros(2, 2, dtype=i32), 1)
+    y, w = torch.randn(4), torch.randn(3, 2)
+    with pytest.raises(RuntimeError, match="restore_proj_fwd_indexed: fp32 y_flat and weight"):
+        rd.restore_proj_fwd_indexed(y.bfloat16(), idx, 2, 2, 8, w)
+    with pytest.raises(RuntimeError, match="restore_proj_fwd_indexed: fp32 bias"):
+        rd.restore_proj_fwd_indexed(y, idx, 2, 2, 8, w, torch.zeros(3, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="restore_proj_fwd_indexed: weight \\[d_model, dim\\]"):
+        rd.restore_proj_fwd_indexed(y, idx, 2, 2, 8, torch.randn(3, 5))
+
+
 def test_extract_checks():
     with pytest.raises(RuntimeError, match="base_input must be CUDA"):
         ee.extract_base_events(torch.zeros(1, 2, 3), 0.5)
