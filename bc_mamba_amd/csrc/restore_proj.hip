@@ -271,6 +271,131 @@ __global__ __launch_bounds__(256) void k_restore_proj_dy(const float* __restrict
   }
 }
 
+// ------------------------------------------------- dy, LDS-DMA form
+// The dy product with both operands brought in by LDS DMA (gfx950's
+// global_load_lds_dwordx4: 16 bytes per lane straight into LDS, no register
+// staging), two stages in flight; for d_model % 32 == 0 and dim % 64 == 0
+// (the items then never straddle the contraction or channel ends).
+// Item (b, jj, db): dz rows t0 = 128 jj .. t0 + 127 (two 64-step tiles),
+// channels d0 = 64 db .. + 63. Wave w: steps 64 (w & 1) .. + 63 (two 32-row
+// MFMA blocks sharing one W fragment), channels 32 (w >> 1) .. + 31.
+typedef __attribute__((address_space(3))) void* lds_vptr;
+__device__ __forceinline__ uint32_t lds_off(const void* p) { return (uint32_t)(size_t)(lds_vptr)p; }
+// 16 bytes per lane from gptr into LDS at the wave-uniform byte offset off +
+// 16 * lane. The compiler does not track these loads: the kernel waits for
+// them (vmcnt) before the barrier that hands the stage to the other waves.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t off) {
+  const uint32_t o = __builtin_amdgcn_readfirstlane(off);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(o) : "memory", "m0");
+}
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// 16-byte slot of a 128-byte LDS row: rows 2i and 2i+1 keep their slots,
+// the 8 row pairs rotate them, so 16 consecutive rows reading the same slot
+// hit 16 different bank groups
+__device__ __forceinline__ int qswz(int row) { return (row >> 1) & 7; }
+constexpr int kDyT = 128;  // dz rows (steps) per item of the DMA form
+
+__global__ __launch_bounds__(256) void k_restore_proj_dy_dma(const float* __restrict__ dout, int64_t n_events,
+                                                             const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                             int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                             int nT, int dim, int L, int64_t n_rows,
+                                                             const float* __restrict__ weight, int dm, int nDB,
+                                                             float* __restrict__ dy, float* __restrict__ head,
+                                                             float* __restrict__ tail, int32_t* __restrict__ tend) {
+  extern __shared__ float4 s_dyn[];
+  float* sA = reinterpret_cast<float*>(s_dyn);  // [2][128][32]: dOut rows, slots swizzled
+  float* sB = sA + 2 * kDyT * kKC;              // [2][32][64]: W rows of the item's channels
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int nJJ = (nT + 1) / 2;
+  const int db = item % nDB, bj = item / nDB;
+  const int jj = bj % nJJ, b = bj / nJJ;
+  const int t0 = jj * kDyT, d0 = db * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int li = lane & 31, h = lane >> 5;
+  const int rb = 64 * (w & 1), cb = 32 * (w >> 1);
+  const float* gb = dout + (int64_t)b * L * dm;
+  auto issue = [&](int c, int st) {
+    // dOut: 16 wave loads of 8 rows each (4 per wave); rows past L read row
+    // L - 1 (their dz is not used)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int blk = 4 * w + i;
+      const int row = blk * 8 + (lane >> 3);
+      const int q = (lane & 7) ^ qswz(row);
+      const int t = min(t0 + row, L - 1);
+      lds_dma16(gb + (int64_t)t * dm + c * kKC + 4 * q, lds_off(sA + st * kDyT * kKC + blk * 256));
+    }
+    // W: 8 wave loads of 4 rows of 64 channels (2 per wave)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int blk = 2 * w + i;
+      const int kr = blk * 4 + (lane >> 4);
+      lds_dma16(weight + (int64_t)(c * kKC + kr) * dim + d0 + 4 * (lane & 15),
+                lds_off(sB + st * kKC * kPT + blk * 256));
+    }
+  };
+  const int nK = dm / kKC;
+  f32x16 acc0 = {}, acc1 = {};
+  issue(0, 0);
+  for (int c = 0; c < nK; ++c) {
+    wait_vmcnt0();    // this wave's part of stage c has landed
+    __syncthreads();  // everyone's has, and every wave is done with stage c - 1
+    if (c + 1 < nK) issue(c + 1, (c + 1) & 1);
+    const float* ab = sA + (c & 1) * kDyT * kKC;
+    const float* bb = sB + (c & 1) * kKC * kPT;
+    const float4* a0 = reinterpret_cast<const float4*>(ab + (rb + li) * kKC);
+    const float4* a1 = reinterpret_cast<const float4*>(ab + (rb + 32 + li) * kKC);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 p0 = a0[(4 * h + v) ^ qswz(rb + li)], p1 = a1[(4 * h + v) ^ qswz(rb + 32 + li)];
+      const float* bk = bb + (16 * h + 4 * v) * kPT + cb + li;
+      acc0 = mfma32(p0.x, bk[0], acc0);
+      acc1 = mfma32(p1.x, bk[0], acc1);
+      acc0 = mfma32(p0.y, bk[kPT], acc0);
+      acc1 = mfma32(p1.y, bk[kPT], acc1);
+      acc0 = mfma32(p0.z, bk[2 * kPT], acc0);
+      acc1 = mfma32(p1.z, bk[2 * kPT], acc1);
+      acc0 = mfma32(p0.w, bk[3 * kPT], acc0);
+      acc1 = mfma32(p1.w, bk[3 * kPT], acc1);
+    }
+  }
+  // dz tile [128 steps][64 channels] in LDS over the operand stages
+  __syncthreads();
+  float* sD = sA;
+  static_assert(2 * kDyT * kKC + 2 * kKC * kPT >= kDyT * kDS, "dz tile fits the operand stages");
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    sD[(rb + acc_row(r, h)) * kDS + cb + li] = acc0[r];
+    sD[(rb + 32 + acc_row(r, h)) * kDS + cb + li] = acc1[r];
+  }
+  __syncthreads();
+  // waves 0 and 1: the restore backward's sweep over tile 2 jj + w, lane =
+  // channel d0 + lane (rows past L count as 0 and hold no event bits)
+  const int j = 2 * jj + w;
+  if (w > 1 || j >= nT) return;
+  const int64_t ch = (int64_t)b * dim + d0 + lane;
+  const uint64_t m = tile_mask(bitmask + (ch / mrd) * Wd, j);
+  const int32_t elo = tile_start[ch * (nT + 1) + j];
+  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy, n_events * 4);
+  const int first = m ? __builtin_ctzll(m) : kTile;
+  const int steps = min(kTile, L - j * kTile);
+  uint32_t r = 0;
+  float sum = 0.0f, hsum = 0.0f;
+  for (int s = 0; s < kTile; ++s) {
+    const float gv = s < steps ? sD[(64 * w + s) * kDS + lane] : 0.0f;
+    const uint32_t bit = (uint32_t)(m >> s) & 1u;
+    buf_store_f32(rdy, (bit && r) ? (uint32_t)(elo + (int32_t)r - 1) * 4u : kBufOOB, sum);
+    r += bit;
+    sum = (bit ? 0.0f : sum) + gv;
+    hsum += s < first ? gv : 0.0f;
+  }
+  const int64_t o = (int64_t)j * n_rows + ch;
+  head[o] = hsum;
+  tail[o] = sum;
+  tend[o] = r ? elo + (int32_t)r : -1;
+}
+
 // ----------------------------------------------------------- dW partials
 // Item (p = b * nSeg + seg, nb, db): rows n0 = 64 nb .. of dW, channels
 // d0 = 64 db .., the steps of segment seg of sequence b in 32-step chunks.
@@ -458,9 +583,21 @@ int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events, co
   int32_t* tend = reinterpret_cast<int32_t*>(tail + s.nT * n_rows);
   float* part = reinterpret_cast<float*>(tend + s.nT * n_rows);
   if (dy && n_events > 0) {
-    hipLaunchKernelGGL(k_restore_proj_dy, dim3((unsigned)(B * s.nT * s.nDB)), dim3(256), 0, st, dout, n_events,
-                       bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, n_rows, weight,
-                       (int)d_model, (int)s.nDB, dy, head, tail, tend);
+    // the LDS-DMA form wants whole 32-row chunks of W, whole 64-channel
+    // blocks and 16-byte aligned rows
+    const bool dma = d_model % kKC == 0 && dim % kPT == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(weight) & 15) == 0;
+    if (dma) {
+      const int64_t nJJ = (s.nT + 1) / 2;
+      const size_t lds = (size_t)(2 * kDyT * kKC + 2 * kKC * kPT) * 4;
+      hipLaunchKernelGGL(k_restore_proj_dy_dma, dim3((unsigned)(B * nJJ * s.nDB)), dim3(256), lds, st, dout,
+                         n_events, bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, n_rows,
+                         weight, (int)d_model, (int)s.nDB, dy, head, tail, tend);
+    } else {
+      hipLaunchKernelGGL(k_restore_proj_dy, dim3((unsigned)(B * s.nT * s.nDB)), dim3(256), 0, st, dout, n_events,
+                         bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, n_rows, weight,
+                         (int)d_model, (int)s.nDB, dy, head, tail, tend);
+    }
     if ((rc = check_launch(fn))) return rc;
     if ((rc = restore_bwd_fix(s.nT, n_rows, head, tail, tend, dy, n_events, st, fn))) return rc;
   }
