@@ -396,6 +396,112 @@ __global__ __launch_bounds__(256) void k_restore_proj_dy_dma(const float* __rest
   tend[o] = r ? elo + (int32_t)r : -1;
 }
 
+// --------------------------------------------- forward, LDS-DMA form
+// The forward with W brought in by LDS DMA and z generated into LDS, for
+// dim % 32 == 0 and d_model % 64 == 0. Item (b, jj, nb): out rows t0 = 128 jj
+// .. + 127 (two 64-step tiles), columns n0 = 64 nb .. + 63. Wave w: steps
+// 64 (w & 1) .. + 63 (two 32-row MFMA blocks sharing one W fragment),
+// columns 32 (w >> 1) .. + 31. Both operands sit in 128-byte LDS rows with
+// their 16-byte slots rotated per row pair (qswz), read 4 values at a time.
+// z of chunk c: wave w generates tile 2 jj + (w & 1), channels 16 (w >> 1)
+// .. + 15 of the chunk, lane = step (each gather reads one channel's events
+// of the tile); the tiles' index words are staged once per item.
+__global__ __launch_bounds__(256) void k_restore_proj_fwd_dma(const float* __restrict__ y, int64_t n_events,
+                                                              const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                              int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                              int nT, int dim, int L,
+                                                              const float* __restrict__ weight,
+                                                              const float* __restrict__ bias, int dm, int nNB,
+                                                              float* __restrict__ out) {
+  extern __shared__ float4 s_dyn[];
+  float* sZ = reinterpret_cast<float*>(s_dyn);                // [2][128][32]: z rows (steps)
+  float* sW = sZ + 2 * kDyT * kKC;                            // [2][64][32]: W rows (columns of out)
+  uint4* sIdx = reinterpret_cast<uint4*>(sW + 2 * kPT * kKC);  // [2][dim]: mask lo, hi, tsj, first
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int nJJ = (nT + 1) / 2;
+  const int nb = item % nNB, bj = item / nNB;
+  const int jj = bj % nJJ, b = bj / nJJ;
+  const int t0 = jj * kDyT, n0 = nb * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int li = lane & 31, h = lane >> 5;
+  const int rb = 64 * (w & 1), cb = 32 * (w >> 1);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y, n_events * 4);
+  for (int i = tid; i < 2 * dim; i += blockDim.x) {
+    const int th = i / dim, d = i - th * dim;
+    const int j = min(2 * jj + th, nT - 1);  // a second tile past the end repeats the last (rows not stored)
+    const int64_t ch = (int64_t)b * dim + d;
+    const uint64_t m = tile_mask(bitmask + (ch / mrd) * Wd, j);
+    const int32_t* ts = tile_start + ch * (nT + 1);
+    sIdx[i] = make_uint4((uint32_t)m, (uint32_t)(m >> 32), (uint32_t)ts[j], (uint32_t)ts[0]);
+  }
+  __syncthreads();
+  const int th = w & 1, zc = 16 * (w >> 1);
+  float zr[16];
+  auto gen = [&](int c) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const uint4 ix = sIdx[th * dim + c * kKC + zc + q];  // wave-uniform: an LDS broadcast
+      const uint64_t m = (uint64_t)ix.x | ((uint64_t)ix.y << 32);
+      zr[q] = buf_load<float>(ry, zoh_off(m, lane, (int32_t)ix.z, (int32_t)ix.w, true));
+    }
+  };
+  auto issue_w = [&](int c, int st) {  // 8 wave loads of 8 W rows (2 per wave)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int blk = 2 * w + i;
+      const int row = blk * 8 + (lane >> 3);
+      const int q = (lane & 7) ^ qswz(row);
+      lds_dma16(weight + (int64_t)(n0 + row) * dim + c * kKC + 4 * q, lds_off(sW + st * kPT * kKC + blk * 256));
+    }
+  };
+  const int nK = dim / kKC;
+  f32x16 acc0 = {}, acc1 = {};
+  issue_w(0, 0);
+  gen(0);
+  const int zrow = 64 * th + lane;
+  for (int c = 0; c < nK; ++c) {
+    float* zb = sZ + (c & 1) * kDyT * kKC;
+    float4* zrw = reinterpret_cast<float4*>(zb + zrow * kKC);
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+      zrw[((zc >> 2) + qq) ^ qswz(zrow)] = make_float4(zr[4 * qq], zr[4 * qq + 1], zr[4 * qq + 2], zr[4 * qq + 3]);
+    wait_vmcnt0();    // this wave's W rows of chunk c have landed
+    __syncthreads();  // z and W of chunk c are staged; every wave is done with chunk c - 1
+    if (c + 1 < nK) {
+      issue_w(c + 1, (c + 1) & 1);
+      gen(c + 1);
+    }
+    const float* wb = sW + (c & 1) * kPT * kKC;
+    const float4* a0 = reinterpret_cast<const float4*>(zb + (rb + li) * kKC);
+    const float4* a1 = reinterpret_cast<const float4*>(zb + (rb + 32 + li) * kKC);
+    const float4* bw = reinterpret_cast<const float4*>(wb + (cb + li) * kKC);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 p0 = a0[(4 * h + v) ^ qswz(rb + li)], p1 = a1[(4 * h + v) ^ qswz(rb + 32 + li)];
+      const float4 q = bw[(4 * h + v) ^ qswz(cb + li)];
+      acc0 = mfma32(p0.x, q.x, acc0);
+      acc1 = mfma32(p1.x, q.x, acc1);
+      acc0 = mfma32(p0.y, q.y, acc0);
+      acc1 = mfma32(p1.y, q.y, acc1);
+      acc0 = mfma32(p0.z, q.z, acc0);
+      acc1 = mfma32(p1.z, q.z, acc1);
+      acc0 = mfma32(p0.w, q.w, acc0);
+      acc1 = mfma32(p1.w, q.w, acc1);
+    }
+  }
+  const int n = n0 + cb + li;
+  const int64_t obase = ((int64_t)b * L + t0) * dm;
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out + obase, ((int64_t)(L - t0) * dm) * 4);
+  const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int r0 = rb + acc_row(r, h), r1 = r0 + 32;
+    buf_store_f32(ro, t0 + r0 < L ? (uint32_t)(r0 * dm + n) * 4u : kBufOOB, acc0[r] + bv);
+    buf_store_f32(ro, t0 + r1 < L ? (uint32_t)(r1 * dm + n) * 4u : kBufOOB, acc1[r] + bv);
+  }
+}
+
 // ----------------------------------------------------------- dW partials
 // Item (p = b * nSeg + seg, nb, db): rows n0 = 64 nb .. of dW, channels
 // d0 = 64 db .., the steps of segment seg of sequence b in 32-step chunks.
@@ -545,6 +651,19 @@ int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitma
   if (n_rows == 0) return BCM_OK;
   if (!out || (n_events > 0 && !y)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
   const ProjShape s = proj_shape(n_rows, dim, L, d_model);
+  // the LDS-DMA form wants whole 32-channel chunks, whole 64-column blocks
+  // and 16-byte aligned W rows
+  const bool dma = dim % kKC == 0 && d_model % kPT == 0 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0;
+  if (dma) {
+    const int64_t items = (n_rows / dim) * ((s.nT + 1) / 2) * s.nNB;
+    const size_t lds = (size_t)(2 * kDyT * kKC + 2 * kPT * kKC) * 4 + (size_t)dim * 32;
+    if ((int64_t)lds > max_lds_bytes())
+      return set_error(BCM_EINVAL, "%s: dim %lld needs %lld bytes of LDS", fn, (long long)dim, (long long)lds);
+    hipLaunchKernelGGL(k_restore_proj_fwd_dma, dim3((unsigned)items), dim3(256), lds, hs(stream), y, n_events, bitmask,
+                       s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, weight, bias, (int)d_model,
+                       (int)s.nNB, out);
+    return check_launch(fn);
+  }
   const int64_t items = (n_rows / dim) * s.nT * s.nNB;
   const size_t lds = (size_t)(4 * kPT * kRS) * 4 + (size_t)dim * 16;  // operand buffers + per-channel index words
   if ((int64_t)lds > max_lds_bytes())
