@@ -132,6 +132,28 @@ __device__ __forceinline__ bool exact_products(const float* sAl, int N, float dt
   return f;
 }
 
+// Length order of model channel d's channels (ch = d + b·dim, b < n_per_d),
+// used when channels span several passes: ord[rank] = b, longest first,
+// ties by b. keys is LDS scratch of n_per_d ints, dead after the return.
+constexpr int kSortMax = 256;  // most channels per model channel that are ranked
+__device__ __forceinline__ void rank_channels(const bcm_scan_args& a, int d, int n_per_d, int* keys, int* ord) {
+  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
+    const int64_t ch = (int64_t)d + (int64_t)i * a.dim;
+    keys[i] = a.cu_seqlens[ch + 1] - a.cu_seqlens[ch];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
+    const int ki = keys[i];
+    int r = 0;
+    for (int q = 0; q < n_per_d; ++q) {
+      const int kq = keys[q];
+      r += (kq > ki) | ((kq == ki) & (q < i));
+    }
+    ord[r] = i;
+  }
+  __syncthreads();
+}
+
 // Value i of model channel d's parameter-gradient block (dA[d, :],
 // dW_B[d, :], dW_C[d, :], ddt_idle[d], ddt_active[d], dD[d]).
 __device__ __forceinline__ void store_param_grad(const bcm_scan_args& a, int d, int N, int i, float v) {
@@ -151,7 +173,7 @@ __device__ __forceinline__ void report_seqlen(const bcm_scan_args& a, int n) {
 }
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
-__global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a) {
+__global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a, int sort_ch) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int C = G * R;
@@ -159,8 +181,9 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
-  // S workgroups per model channel d (S = gridDim.x / dim); workgroup sp
-  // takes the rounds of channels sp, sp + S, sp + 2S, ...
+  // S workgroups per model channel d (S = gridDim.x / dim). A round covers
+  // nslots·S channels: the slot at position pos of workgroup sp takes rank
+  // r0 + pos·S + sp of round r0 (chan_at below)
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
   const int nw = blockDim.x / kWave;
@@ -172,6 +195,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
   // the decay table is static LDS: its address is a compile-time constant,
   // which the table reads take as their instruction offset
   __shared__ float sTab[TBL ? kTabMaxN * kTabStride : 1];
+  __shared__ int sOrd[kSortMax];  // length order of the channels (sort_ch)
   extern __shared__ float smem[];
   float* sT = sTab;
   float* sAl = smem;
@@ -227,10 +251,23 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
     report_seqlen(a, n);
   };
+  // Channel b of the slot at position p in round r0 (n_per_d: none). With
+  // sort_ch the rank indexes the length order, so the S workgroups take
+  // every S-th channel of it and a wave's groups take neighbouring lengths;
+  // waves past the first half take positions in reverse, so the two waves
+  // of a SIMD (w and w + 4 of 8) pair a long wave with a short one.
+  const int hw = (nw + 1) / 2;
+  const int pos = (wave < hw ? wave : nw - 1 - (wave - hw)) * CPW + grp;
+  auto chan_at = [&](int r0, int p) {
+    const int v = r0 + p * S + sp;
+    return v < n_per_d ? (sort_ch ? sOrd[v] : v) : n_per_d;
+  };
+  static_assert(2 * kWave * (R + 1) >= kSortMax, "the staging tiles hold the ranking keys");
+  if (sort_ch) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(sWBC + N), sOrd);  // keys in the tiles
   int e0, n;
-  const int b_first = sp * nslots, b_step = nslots * S;
-  channel(b_first + slot, e0, n);
-  if (n_per_d > b_first) issue(e0, n, 0);
+  const int b_step = nslots * S;
+  channel(chan_at(0, pos), e0, n);
+  if (sp < n_per_d) issue(e0, n, 0);
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
@@ -241,14 +278,14 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
     sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
   }
   if (TBL) build_decay_table(sT, a, d, dti, dta);
-  if (n_per_d > b_first) to_tiles();
+  if (sp < n_per_d) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
-  for (int b0 = b_first; b0 < n_per_d; b0 += b_step) {
-    const int b = b0 + slot;
+  for (int r0 = 0; r0 + sp < n_per_d; r0 += b_step) {
+    const int b = chan_at(r0, pos);
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    if (b0 > b_first) channel(b, e0, n);
+    if (r0 > 0) channel(b, e0, n);
     const int nch = n > 0 ? (n + C - 1) / C : 0;
     const int wmax = wave_max_dpp(nch);
     for (int c = 0; c < wmax; ++c) {
@@ -260,7 +297,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
       const int cend = min(n, (c + 1) * C);
       const int xc = (cend - 1) / kXChunk;
       const bool xsave = c < nch && (cend % kXChunk == 0 || cend == n) && xc < nck;
-      if (b0 > b_first || c > 0) {
+      if (r0 > 0 || c > 0) {
         issue(e0, n, c);
         to_tiles();
       }
@@ -415,8 +452,9 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
-  // S workgroups per model channel d (S = gridDim.x / dim); workgroup sp
-  // takes the rounds of channels sp, sp + S, sp + 2S, ...
+  // S workgroups per model channel d (S = gridDim.x / dim). A round covers
+  // nslots·S channels: the slot at position pos of workgroup sp takes rank
+  // r0 + pos·S + sp of round r0 (chan_at below)
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
   const int nw = blockDim.x / kWave;
@@ -495,12 +533,21 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
     n = act ? a.cu_seqlens[ch + 1] - e0 : 0;
     report_seqlen(a, n);
   };
+  // Channel b of the slot at position p in round r0 (n_per_d: none): the
+  // forward's slot positions, taken in channel order (the forward's length
+  // order measured about 3 % slower here on bursty channels)
+  const int hw = (nw + 1) / 2;
+  const int pos = (wave < hw ? wave : nw - 1 - (wave - hw)) * CPW + grp;
+  auto chan_at = [&](int r0, int p) {
+    const int v = r0 + p * S + sp;
+    return v < n_per_d ? v : n_per_d;
+  };
   int e0, n;
-  const int b_first = sp * nslots, b_step = nslots * S;
-  channel(b_first + slot, e0, n);
+  const int b_step = nslots * S;
+  channel(chan_at(0, pos), e0, n);
   int nch = n > 0 ? (n + C - 1) / C : 0;
   int wmax = wave_max_dpp(nch);
-  if (n_per_d > b_first && wmax > 0) issue(e0, n, wmax - 1);
+  if (sp < n_per_d && wmax > 0) issue(e0, n, wmax - 1);
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
@@ -516,11 +563,11 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
   }
   for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   if (TBL) build_decay_table(sT, a, d, dti, dta);
-  if (n_per_d > b_first && wmax > 0) to_tiles();
+  if (sp < n_per_d && wmax > 0) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
-  for (int b0 = b_first; b0 < n_per_d; b0 += b_step) {
-    const int b = b0 + slot;
+  for (int r0 = 0; r0 + sp < n_per_d; r0 += b_step) {
+    const int b = chan_at(r0, pos);
     const bool act = b < n_per_d;
     const int64_t ch = (int64_t)d + (int64_t)b * dim;
     // e0, n, nch, wmax describe this channel, and the loads of its last
@@ -821,7 +868,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
       if (act) {
         // row and lane constants formed here (opaque: not hoisted into
         // registers that would stay live across the state loop)
-        const int64_t row = (int64_t)d + (int64_t)(b0 + opaque(slot)) * dim;
+        const int64_t row = (int64_t)d + (int64_t)chan_at(r0, opaque(pos)) * dim;
         const uint32_t* mrow = rw.bitmask + (row / rw.mrd) * rw.W;
         const int32_t* tsr = rw.ts + row * (rw.nT + 1);
         T* dr = static_cast<T*>(rw.dx) + row * rw.L;
@@ -905,8 +952,8 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
           seg(tile_mask(mrow, nfull), tsr[nfull], nfull * kTile + off);
       }
     }
-    if (b0 + b_step < n_per_d) {  // the next channel of this lane group
-      channel(b + b_step, e0, n);
+    if (r0 + b_step + sp < n_per_d) {  // the next round of this workgroup
+      channel(chan_at(r0 + b_step, pos), e0, n);
       nch = n > 0 ? (n + C - 1) / C : 0;
       wmax = wave_max_dpp(nch);
       if (wmax > 0) {
@@ -985,6 +1032,10 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
   // no (or too small a) workspace for the partials: one workgroup per model channel
   if (BWD && (!a.split_ws || a.split_ws_bytes < 4 * (int64_t)S * a.dim * (3 * a.dstate + 3))) S = 1;
   const dim3 grid((unsigned)((int64_t)a.dim * S));
+  // forward over channels of several passes: each workgroup ranks its model
+  // channel's channels by length, so the groups of a wave (and the
+  // workgroups of one model channel) get channels of similar pass counts
+  const int sort_ch = !BWD && per_d > 1 && per_d <= kSortMax && a.max_seqlen > G * R;
   if (BWD) {
     hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL, DXR>), grid, dim3(nw * kWave), (size_t)lds, s, a,
                        rw ? *rw : ScanRows{});
@@ -993,7 +1044,7 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
     const int64_t tot = (int64_t)a.dim * (3 * a.dstate + 3);
     hipLaunchKernelGGL(k_scan_param_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a, S);
   } else {
-    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a);
+    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a, sort_ch);
   }
   return check_launch(fn);
 }
