@@ -52,9 +52,13 @@ namespace bcm {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kScanThreads = 512;   // workgroup size bound (8 waves)
 template <int G, bool BWD> constexpr int kScanThreadsG = kScanThreads;
-constexpr int kTabK = 64;           // gaps k = 1..kTabK come from the decay table
+constexpr int kTabK = 64;           // gaps k = 1..kTabK (at least) come from the decay table
 constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
 constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
+constexpr int kTabElems = kTabMaxN * kTabStride;  // its static LDS array
+// Longest gap in the table for dstate N: the rows of fewer states are longer
+// (kTabElems / N entries each, at most 257), so sparser streams stay on it.
+__host__ __device__ constexpr int tab_gaps(int N) { return (kTabElems / N < 257 ? kTabElems / N : 257) - 1; }
 constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
 constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
 constexpr int kFixSlots = 4;        // backward: item slots with a long gap that the table path fixes up
@@ -112,11 +116,13 @@ __device__ __forceinline__ float tab(const float* sT, uint32_t row, uint32_t tb)
 }
 
 // Decay table of workgroup d: T[s][0] = 1 (padding), T[s][k] = the decay of
-// gap k (same expression and rounding as the per-event path).
+// gap k (same expression and rounding as the per-event path), rows of
+// tab_gaps(N) + 1 entries.
 __device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
   const int N = a.dstate;
-  for (int i = threadIdx.x; i < N * kTabStride; i += blockDim.x) {
-    const int s = i / kTabStride, q = i - s * kTabStride;
+  const int tstr = tab_gaps(N) + 1;
+  for (int i = threadIdx.x; i < N * tstr; i += blockDim.x) {
+    const int s = i / tstr, q = i - s * tstr;
     sT[i] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * (a.A[(int64_t)d * N + s] * kLog2e));
   }
 }
@@ -181,6 +187,8 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
+  // longest gap in the decay table (without a table tb only marks valid items)
+  const int tabk = TBL ? tab_gaps(N) : kTabK;
   // S workgroups per model channel d (S = gridDim.x / dim). A round covers
   // nslots·S channels: the slot at position pos of workgroup sp takes rank
   // r0 + pos·S + sp of round r0 (chan_at below)
@@ -194,7 +202,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
 
   // the decay table is static LDS: its address is a compile-time constant,
   // which the table reads take as their instruction offset
-  __shared__ float sTab[TBL ? kTabMaxN * kTabStride : 1];
+  __shared__ float sTab[TBL ? kTabElems : 1];
   __shared__ int sOrd[kSortMax];  // length order of the channels (sort_ch)
   extern __shared__ float smem[];
   float* sT = sTab;
@@ -316,7 +324,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
         const float uv = mine[r];  // u stays in the tile (read again for the outputs)
         du2[r] = dl[r] * uv * uv;
         tb[r] = (uint32_t)(km1 + 1) * 4u;
-        big |= km1 >= kTabK ? 1 : 0;
+        big |= km1 >= tabk ? 1 : 0;
         if (r < HR) Sa += dl[r];
         else Sb += dl[r];
         acc[r] = 0.0f;
@@ -355,7 +363,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
         const float gin = Ops::prev(gend, g0);
         if (!EXACT) {
           const int sn = s + 1 < N ? s + 1 : s;
-          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(sn * kTabStride * 4);
+          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(sn * (tabk + 1) * 4);
 #pragma unroll
           for (int r = 0; r < R; ++r) avn[r] = tab(sT, row, tb[r]);
         }
@@ -452,6 +460,8 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
   static_assert(R % 2 == 0, "R must be even");
   constexpr uint32_t SZ = sizeof(T);
   const int N = a.dstate;
+  // longest gap in the decay table (without a table tb only marks valid items)
+  const int tabk = TBL ? tab_gaps(N) : kTabK;
   // S workgroups per model channel d (S = gridDim.x / dim). A round covers
   // nslots·S channels: the slot at position pos of workgroup sp takes rank
   // r0 + pos·S + sp of round r0 (chan_at below)
@@ -466,7 +476,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
 
   // the decay table is static LDS: its address is a compile-time constant,
   // which the table reads take as their instruction offset
-  __shared__ float sTab[TBL ? kTabMaxN * kTabStride : 1];
+  __shared__ float sTab[TBL ? kTabElems : 1];
   extern __shared__ float smem[];
   float* sT = sTab;
   float* sAl = smem;
@@ -610,10 +620,10 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
           const int kk = __float_as_int(gkm[r]);
           // with the fix-up, gaps past the table read its last entry and the
           // state loop replaces it; without it such a chunk runs the exact path
-          tb[r] = valid ? (uint32_t)(R >= kFixMinR ? min(kk, kTabK) : kk) * 4u : 0u;
+          tb[r] = valid ? (uint32_t)(R >= kFixMinR ? min(kk, tabk) : kk) * 4u : 0u;
           dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
           gkm[r] = valid ? (float)(kk - 1) : 0.0f;
-          big |= (valid && kk > kTabK) ? (1 << r) : 0;
+          big |= (valid && kk > tabk) ? (1 << r) : 0;
           if (r < HR) Sa += dlv[r];
           else Sb += dlv[r];
           uvv[r] = gg[r];
@@ -654,7 +664,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
       // the state loop reads gkm through an index the compiler cannot see
       // through, so it re-reads LDS instead of keeping the stored values live
       const float* km = gkm + opaque(0);
-      // items with a gap longer than the table (k > kTabK) compute their
+      // items with a gap longer than the table (k > tabk) compute their
       // decays directly, state by state, on the table path; bigm is the
       // wave-uniform set of item slots that hold one in some lane (shapes
       // without the fix-up: nonzero when some lane holds one)
@@ -669,7 +679,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
 #pragma unroll 1
         for (int s = 0; s < N; ++s) {
           const float Al = sAl[s], wbc = sWBC[s], wbca = sWBCA[s];
-          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(s * kTabStride * 4);
+          const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane(s * (tabk + 1) * 4);
           const float g0 = c > 0 ? cg0[s] : 0.0f;
           const float ec = (c < nch - 1) ? cdx[s] : 0.0f;
           float av[R];
@@ -684,7 +694,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
             if constexpr (MODE == 1) {
 #pragma unroll
               for (int r = 0; r < R; ++r)
-                if ((bigm & (1u << r)) && tb[r] && km[r] >= (float)kTabK) av[r] = decay(fmaf(dti, km[r], dta) * Al);
+                if ((bigm & (1u << r)) && tb[r] && km[r] >= (float)tabk) av[r] = decay(fmaf(dti, km[r], dta) * Al);
             }
           }
 #pragma unroll
