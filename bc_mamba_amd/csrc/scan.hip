@@ -55,9 +55,10 @@ template <int G, bool BWD> constexpr int kScanThreadsG = kScanThreads;
 constexpr int kTabK = 64;           // gaps k = 1..kTabK (at least) come from the decay table
 constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
 constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
-constexpr int kTabElems = kTabMaxN * kTabStride;  // its static LDS array
-// Longest gap in the table for dstate N: the rows of fewer states are longer
-// (kTabElems / N entries each, at most 257), so sparser streams stay on it.
+constexpr int kTabElems = kTabMaxN * 129;  // its static LDS array (33 KB)
+// Longest gap in the table for dstate N: kTabElems / N entries per row, at
+// most 257 (gaps up to 128 at N = 64, 256 at N <= 32), so sparse streams
+// stay on it.
 __host__ __device__ constexpr int tab_gaps(int N) { return (kTabElems / N < 257 ? kTabElems / N : 257) - 1; }
 constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
 constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
