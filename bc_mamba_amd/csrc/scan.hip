@@ -606,6 +606,12 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
         }
       }
       float du2[R], doutu[R], acc1[R], acc2[R];
+      // Δ of each item (0 for padding), kept for the state loop's computed
+      // decays where registers allow (the 16-item shapes of up to 32 lanes;
+      // 8 items must stay within 128 VGPRs for their fourth wave per SIMD);
+      // the others recompute it from k-1 in LDS
+      constexpr bool kKeepDl = R == 16 && G <= 32;
+      float dlx[kKeepDl ? R : 1];
       uint32_t tb[R];  // byte offset of the item's gap k in a table row (4k; 0: padding)
       int big = 0;
       float Sa = 0.0f, Sb = 0.0f, dl0 = 0.0f, dlh = 0.0f;
@@ -623,6 +629,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
           // state loop replaces it; without it such a chunk runs the exact path
           tb[r] = valid ? (uint32_t)(R >= kFixMinR ? min(kk, tabk) : kk) * 4u : 0u;
           dlv[r] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+          if constexpr (kKeepDl) dlx[r] = dlv[r];
           gkm[r] = valid ? (float)(kk - 1) : 0.0f;
           big |= (valid && kk > tabk) ? (1 << r) : 0;
           if (r < HR) Sa += dlv[r];
@@ -695,15 +702,21 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
             if constexpr (MODE == 1) {
 #pragma unroll
               for (int r = 0; r < R; ++r)
-                if ((bigm & (1u << r)) && tb[r] && km[r] >= (float)tabk) av[r] = decay(fmaf(dti, km[r], dta) * Al);
+                if ((bigm & (1u << r)) && tb[r] && km[r] >= (float)tabk)
+                  av[r] = decay((kKeepDl ? dlx[kKeepDl ? r : 0] : fmaf(dti, km[r], dta)) * Al);
             }
           }
 #pragma unroll
           for (int i = 0; i < HR; ++i) {
             const int ra = i, rb = i + HR;
             if (EXACT) {
-              av[ra] = decay((tb[ra] ? fmaf(dti, km[ra], dta) : 0.0f) * Al);
-              av[rb] = decay((tb[rb] ? fmaf(dti, km[rb], dta) : 0.0f) * Al);
+              if constexpr (kKeepDl) {
+                av[ra] = decay(dlx[ra] * Al);
+                av[rb] = decay(dlx[rb] * Al);
+              } else {
+                av[ra] = decay((tb[ra] ? fmaf(dti, km[ra], dta) : 0.0f) * Al);
+                av[rb] = decay((tb[rb] ? fmaf(dti, km[rb], dta) : 0.0f) * Al);
+              }
             }
             Ha = fmaf(av[ra], Ha, du2[ra]);
             Hb = fmaf(av[rb], Hb, du2[rb]);
