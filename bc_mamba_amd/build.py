@@ -22,7 +22,7 @@ BUILDDIR = os.path.join(HERE, "lib", "_obj")
 LIBNAME = "libbcm_event_scan.so"
 ARCH = os.environ.get("BCM_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["abi.hip", "extract.hip", "scan.hip", "scan_var.hip", "restore.hip", "restore_proj.hip", "conv.hip"]
+SOURCES = ["abi.hip", "extract.hip", "scan.hip", "scan_sl.hip", "scan_var.hip", "restore.hip", "restore_proj.hip", "conv.hip"]
 
 # Packed FP32 (v_pk_*_f32) generation is switched off for all device code.
 HIPCC_FLAGS = [

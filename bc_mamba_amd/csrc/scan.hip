@@ -41,6 +41,7 @@
 //     carries a·e backward in LDS.
 //   * No MFMA: the work is a first-order recurrence, not a contraction.
 #include "bcm_common.hpp"
+#include "scan_common.hpp"
 #include "scan_group.hpp"
 
 #include <algorithm>
@@ -48,23 +49,6 @@
 #include <type_traits>
 
 namespace bcm {
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kScanThreads = 512;   // workgroup size bound (8 waves)
-template <int G, bool BWD> constexpr int kScanThreadsG = kScanThreads;
-constexpr int kTabK = 64;           // gaps k = 1..kTabK (at least) come from the decay table
-constexpr int kTabStride = kTabK + 1;  // entry 0 = 1.0: the decay of a padding item
-constexpr int kTabMaxN = 64;        // the table is used when dstate <= kTabMaxN
-constexpr int kTabElems = kTabMaxN * 129;  // its static LDS array (33 KB)
-// Longest gap in the table for dstate N: kTabElems / N entries per row, at
-// most 257 (gaps up to 128 at N = 64, 256 at N <= 32), so sparse streams
-// stay on it.
-__host__ __device__ constexpr int tab_gaps(int N) { return (kTabElems / N < 257 ? kTabElems / N : 257) - 1; }
-constexpr int kSchedBlock = 8;      // items per scheduling block in the backward's long passes
-constexpr int kXChunk = 2048;       // events per saved-state chunk of x (selective_scan.cpp:795)
-constexpr int kFixSlots = 4;        // backward: item slots with a long gap that the table path fixes up
-constexpr int kFixMinR = 16;        // ... in shapes of at least this many items per lane (the fix-up's
-                                    // registers would cost R = 8 its fourth wave per SIMD)
 
 struct FwdLds {
   int N, nw, G, R, nslots;
@@ -109,75 +93,6 @@ template <int G, int R> struct TilePos {
   }
 };
 
-// Decay of an item from the table: `tb` is the item's byte offset in a table
-// row, `row` the state's row base in bytes (wave-uniform), so each read costs
-// one address add.
-__device__ __forceinline__ float tab(const float* sT, uint32_t row, uint32_t tb) {
-  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + (row + tb));
-}
-
-// Decay table of workgroup d: T[s][0] = 1 (padding), T[s][k] = the decay of
-// gap k (same expression and rounding as the per-event path), rows of
-// tab_gaps(N) + 1 entries.
-__device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
-  const int N = a.dstate;
-  const int tstr = tab_gaps(N) + 1;
-  for (int i = threadIdx.x; i < N * tstr; i += blockDim.x) {
-    const int s = i / tstr, q = i - s * tstr;
-    sT[i] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * (a.A[(int64_t)d * N + s] * kLog2e));
-  }
-}
-
-// Barrier after the LDS set-up, then: true if some decay exponent of
-// workgroup d can be positive (A > 0 or Δ < 0); lane products are then
-// multiplied out exactly. Every thread reads the N values of A·log2e from
-// LDS (same sign as A), so the kernel needs no static LDS for a vote.
-__device__ __forceinline__ bool exact_products(const float* sAl, int N, float dti, float dta) {
-  __syncthreads();
-  bool f = dti < 0.0f || dta < 0.0f;
-  for (int s = 0; s < N; ++s) f |= sAl[s] > 0.0f;
-  return f;
-}
-
-// Length order of model channel d's channels (ch = d + b·dim, b < n_per_d),
-// used when channels span several passes: ord[rank] = b, longest first,
-// ties by b. keys is LDS scratch of n_per_d ints, dead after the return.
-constexpr int kSortMax = 256;  // most channels per model channel that are ranked
-__device__ __forceinline__ void rank_channels(const bcm_scan_args& a, int d, int n_per_d, int* keys, int* ord) {
-  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
-    const int64_t ch = (int64_t)d + (int64_t)i * a.dim;
-    keys[i] = a.cu_seqlens[ch + 1] - a.cu_seqlens[ch];
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
-    const int ki = keys[i];
-    int r = 0;
-    for (int q = 0; q < n_per_d; ++q) {
-      const int kq = keys[q];
-      r += (kq > ki) | ((kq == ki) & (q < i));
-    }
-    ord[r] = i;
-  }
-  __syncthreads();
-}
-
-// Value i of model channel d's parameter-gradient block (dA[d, :],
-// dW_B[d, :], dW_C[d, :], ddt_idle[d], ddt_active[d], dD[d]).
-__device__ __forceinline__ void store_param_grad(const bcm_scan_args& a, int d, int N, int i, float v) {
-  if (i < N) a.dA[(int64_t)d * N + i] = v;
-  else if (i < 2 * N) a.dW_B[(int64_t)d * N + (i - N)] = v;
-  else if (i < 3 * N) a.dW_C[(int64_t)d * N + (i - 2 * N)] = v;
-  else if (i == 3 * N) a.ddt_idle[d] = v;
-  else if (i == 3 * N + 1) a.ddt_active[d] = v;
-  else if (a.dD) a.dD[d] = v;
-}
-
-// A channel of n events longer than the caller's max_seqlen: its saved
-// states (x, chunk_g) have fewer rows than its passes need. Flagged in the
-// caller's status word (a plain vector store; several lanes may write it).
-__device__ __forceinline__ void report_seqlen(const bcm_scan_args& a, int n) {
-  if (n > a.max_seqlen && a.status) a.status[0] = BCM_SCAN_SEQLEN_EXCEEDED;
-}
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
 __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a, int sort_ch) {
@@ -440,16 +355,6 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
     }
   }
 }
-
-// Dense gradient rows of the fused gather backward (bcm_scan_bwd_rows): the
-// extraction's event index of every channel row and the [NC, L] output.
-struct ScanRows {
-  const uint32_t* bitmask;  // channel ch reads mask row ch / mrd (words W)
-  int64_t mrd, W;
-  const int32_t* ts;        // [NC, nT + 1] absolute index of each tile's first event
-  int64_t nT, L;
-  void* dx;                 // [NC, L] of T
-};
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL, bool DXR>
 __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw) {
@@ -1016,6 +921,12 @@ __global__ __launch_bounds__(256) void k_scan_param_reduce(const bcm_scan_args a
 }
 
 // ------------------------------------------------------------ host dispatch
+int sl_param_reduce(const bcm_scan_args& a, int S, hipStream_t s, const char* fn) {
+  const int64_t tot = (int64_t)a.dim * (3 * a.dstate + 3);
+  hipLaunchKernelGGL(k_scan_param_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a, S);
+  return check_launch(fn);
+}
+
 struct Plan {
   int nw;      // waves per workgroup
   int64_t lds; // dynamic LDS bytes
@@ -1115,7 +1026,7 @@ static ShapeId pick_shape(const bcm_scan_args& a) {
 
 static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* needs_chunk_g) {
   const ShapeId id = pick_shape(a);
-  const int C = kShapeG[id] * kShapeR[id];
+  const int C = sl_applies(a) ? kSLPass : kShapeG[id] * kShapeR[id];
   *pass_len = C;
   *n_pass = a.max_seqlen > 0 ? (a.max_seqlen + C - 1) / C : 1;
   *needs_chunk_g = (*n_pass > 1 && C < kXChunk) ? 1 : 0;
@@ -1158,6 +1069,7 @@ static int dispatch_shape(const bcm_scan_args& a, hipStream_t s, const char* fn,
 // a 16-lane shape whose one pass holds every channel, no z, 4-step aligned
 // rows.
 static bool rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
+  if (sl_applies(a)) return sl_rows_fusable(a, r);
   const ShapeId id = pick_shape(a);
   if ((kShapeG[id] != 16 && kShapeG[id] != 32) || a.max_seqlen > kShapeG[id] * kShapeR[id] || a.z) return false;
   const uintptr_t p = reinterpret_cast<uintptr_t>(r.dx);
@@ -1207,6 +1119,7 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
       return set_error(BCM_EINVAL, "%s: out and dz required with z", fn);
   }
   const hipStream_t s = hs(stream);
+  if (sl_applies(a)) return BWD ? sl_launch_bwd(a, s, fn, rw) : sl_launch_fwd(a, s, fn);
   int rc = BCM_OK;
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
@@ -1253,6 +1166,10 @@ int64_t bcm_scan_bwd_workspace_bytes(const bcm_scan_args* args) {
   if (!args || !bcm::dtype_ok(args->dtype) || args->dim < 1 || args->dstate < 1 || args->dstate > 256 ||
       args->n_channels < 1)
     return 0;
+  if (bcm::sl_applies(*args)) {
+    const int S = bcm::sl_split(*args);
+    return S > 1 ? 4 * (int64_t)S * args->dim * (3 * args->dstate + 3) : 0;
+  }
   bcm::Plan q{1, 0, 1};
   int rc = BCM_OK;
   const bool z = args->z != nullptr;

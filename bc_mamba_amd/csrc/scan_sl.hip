@@ -1,0 +1,681 @@
+// Stage 2, dstate 16: the depthwise flat selective scan with one lane per
+// (channel, state), forward and backward.
+//
+// Reference behaviour: as scan.hip (selective_scan_fwd_kernel.cuh:403-728,
+// selective_scan_bwd_kernel.cuh:635-1169, the exponent clamp of
+// selective_scan_common.h:43-52).
+//
+// MI355X design
+//   * The 16 lanes of a DPP row own one channel, one state each; a wave holds
+//     four channels of one model channel d (one workgroup per d, as in
+//     scan.hip, so the per-d decay table and the parameter-gradient sums stay
+//     in the workgroup). Each lane walks its channel's events in order: the
+//     recurrence costs one table read and one fma per event and state, with
+//     no lane scans and no padding beyond a block's tail.
+//   * Events come in blocks of 16, one per lane of the row: lane j loads
+//     event 16·blk + j (coalesced), forms Δ, Δu², its table offset (and the
+//     backward's dout·u, k-1), and DPP row_newbcast:q hands event q's values
+//     to the whole row. The next blocks' loads are in flight while a block
+//     computes (a ring of registers), so memory latency overlaps the VALU.
+//   * Sums over the states of one event (y, and the backward's Σ_s W_B W_C e
+//     and Σ_s W_B W_C g) go through a padded LDS tile per row: state lane s
+//     writes its 16 values of the block at (q·17 + s), event lane j reads its
+//     16 states at (j·17 + m): conflict-free both ways, one fma per value
+//     with the per-state weight.
+//   * The forward saves the state h at the start of every 32-event pass in
+//     chunk_g; the backward walks a channel's passes last to first, rebuilds
+//     the pass's states and decays in registers from that row, then runs the
+//     adjoint recurrence e_i = a_{i+1} e_{i+1} + dout_i u_i backward through
+//     them.
+//   * Scaled recurrences as in scan.hip: g = h / W_B (g = a·g + Δu²) and
+//     e = dh / W_C.
+
+#include "bcm_common.hpp"
+#include "scan_common.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+
+namespace bcm {
+
+constexpr int kSLB = 16;                   // events per block (one per lane of a row)
+constexpr int kSLRows = kWave / kSLN;      // channels per wave
+constexpr int kSLTileSz = kSLN * (kSLN + 1);  // floats of one row's transpose tile (stride 17)
+constexpr int kSLTab = tab_gaps(kSLN);     // longest gap in the decay table (256)
+constexpr int kSLPF = 4;                   // blocks per load round (a round ahead in flight)
+
+// Value of lane Q of this lane's DPP row.
+template <int Q> __device__ __forceinline__ int bcast_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x150 + Q, 0xF, 0xF, true);  // row_newbcast:Q
+}
+template <int Q> __device__ __forceinline__ float bcast_f(float v) {
+  return __int_as_float(bcast_i<Q>(__float_as_int(v)));
+}
+
+// Decays of the 16 events of a block for this lane's state: each event's
+// byte offset in a table row (lane q's tb) plus the lane's row base, one DPP
+// add per event. One s_nop 1 first: a DPP read needs two wait states after
+// the VALU write of its source, whichever instruction the compiler placed
+// just before; the adds themselves write no source of a later one.
+__device__ __forceinline__ void tab16(float (&av)[16], const float* sT, uint32_t rowb, uint32_t tb) {
+  uint32_t o[16];
+  asm("s_nop 1\n\t"
+      "v_add_u32_dpp %0, %16, %17 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %1, %16, %17 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %2, %16, %17 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %3, %16, %17 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %4, %16, %17 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %5, %16, %17 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %6, %16, %17 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %7, %16, %17 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %8, %16, %17 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %9, %16, %17 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %10, %16, %17 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %11, %16, %17 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %12, %16, %17 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %13, %16, %17 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %14, %16, %17 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_add_u32_dpp %15, %16, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7]),
+        "=&v"(o[8]), "=&v"(o[9]), "=&v"(o[10]), "=&v"(o[11]), "=&v"(o[12]), "=&v"(o[13]), "=&v"(o[14]), "=&v"(o[15])
+      : "v"(tb), "v"(rowb));
+#pragma unroll
+  for (int q = 0; q < 16; ++q) av[q] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + o[q]);
+}
+
+// acc += (value of lane Q of the row's src) * v as one v_fmac_f32_dpp (the
+// compiler keeps a separate move for a float DPP operand). NOP: s_nop 1
+// first, for the first use of src after its VALU write.
+template <int Q, bool NOP> __device__ __forceinline__ void fmac_bcast(float& acc, float src, float v) {
+  if constexpr (NOP)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc) : "v"(src), "v"(v), "n"(Q));
+  else
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(src), "v"(v), "n"(Q));
+}
+
+// Calls f(std::integral_constant<int, q>) for q = 0..15 (compile-time lane
+// indices for the DPP controls).
+template <typename F, int... Q> __device__ __forceinline__ void for16_impl(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q>{}), ...);
+}
+template <typename F> __device__ __forceinline__ void for16(F&& f) {
+  for16_impl(f, std::make_integer_sequence<int, 16>{});
+}
+template <typename F, int... Q> __device__ __forceinline__ void rfor16_impl(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, 15 - Q>{}), ...);
+}
+template <typename F> __device__ __forceinline__ void rfor16(F&& f) {  // q = 15..0
+  rfor16_impl(f, std::make_integer_sequence<int, 16>{});
+}
+
+// Sum over the 16 lanes of a row, in every lane of it.
+__device__ __forceinline__ float row_sum(float v) {
+  v += __uint_as_float(dpp<kDppXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kDppXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp<0x140>(__float_as_uint(v)));  // row_mirror
+  return v;
+}
+
+// True if some decay exponent of model channel d can be positive (A > 0 or
+// Δ < 0): lane products of decays are then multiplied out instead of taken
+// as exp2 of a Δ sum.
+__device__ __forceinline__ bool sl_exact(const bcm_scan_args& a, int d) {
+  bool ex = a.dt_idle[d] < 0.0f || a.dt_active[d] < 0.0f;
+#pragma unroll
+  for (int m = 0; m < kSLN; ++m) ex |= a.A[(int64_t)d * kSLN + m] > 0.0f;
+  return ex;
+}
+
+// Decay table of model channel d, row by row: T[m][0] = 1 (padding),
+// T[m][k] = the decay of gap k, the same expression as the per-event path.
+// A[d, m] is wave-uniform (a scalar load), so the build waits on no vector
+// load: the first events' loads, issued before it, stay in flight.
+__device__ __forceinline__ void sl_build_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
+#pragma unroll 1
+  for (int m = 0; m < kSLN; ++m) {
+    const float Alm = a.A[(int64_t)d * kSLN + m] * kLog2e;
+    for (int q = threadIdx.x; q <= kSLTab; q += blockDim.x)
+      sT[m * (kSLTab + 1) + q] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * Alm);
+  }
+}
+
+// Slot order of a workgroup's channels (ch = d + b·dim, b < n_per_d): with
+// several channels, ord[rank] = b longest first (rank_channels); the slot at
+// position pos of workgroup sp in round r0 takes rank r0 + pos·S + sp, the
+// first half of the waves positions 0.., the second half in reverse, so the
+// two waves of a SIMD (w and w + 4 of 8) pair long channels with short ones
+// and a wave's four rows hold neighbouring lengths.
+__device__ __forceinline__ int sl_pos(int wave, int grp, int nw) {
+  const int hw = (nw + 1) / 2;
+  return (wave < hw ? wave : nw - 1 - (wave - hw)) * kSLRows + grp;
+}
+
+// ------------------------------------------------------------------ forward
+template <typename T, bool HAS_Z, bool EXACT>
+__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int* sOrd) {
+#pragma clang fp contract(off)  // fmas are written out where they are meant
+  constexpr uint32_t SZ = sizeof(T);
+  constexpr int N = kSLN;
+  const int d = blockIdx.x % a.dim;
+  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
+  const int nw = blockDim.x / kWave;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
+  const int nslots = nw * kSLRows;
+  const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
+  const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
+  const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
+
+  const float dti = a.dt_idle[d], dta = a.dt_active[d];
+  const float Dv = a.D ? a.D[d] : 0.0f;
+  const float Al = a.A[(int64_t)d * N + s] * kLog2e;
+  const float wb = a.W_B[(int64_t)d * N + s];
+  float wbc[N];  // W_B·W_C of every state (the event lanes' weights; wave-uniform, scalar registers)
+#pragma unroll
+  for (int m = 0; m < N; ++m)
+    wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
+        __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  const uint32_t rowb = (uint32_t)(s * (kSLTab + 1) * 4);
+
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.out, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), roz = buf_rsrc(a.out_z, HAS_Z ? E * SZ : 0);
+
+  // Channel b of round r0, and the loads of its first block round. The
+  // first channel's loads are issued before the decay table is built, so
+  // their latency overlaps the set-up.
+  auto off = [&](int e0, int bk) { return (uint32_t)(e0 + bk * kSLB + s); };
+  float Un[kSLPF], Zn[kSLPF];
+  int Kn[kSLPF];
+  auto issue = [&](int e0, int r) {  // unconditional: the registers never merge with old values
+#pragma unroll
+    for (int t = 0; t < kSLPF; ++t) {
+      Un[t] = buf_load<T>(ru, off(e0, r * kSLPF + t) * SZ);
+      Kn[t] = buf_load_i32(rk, off(e0, r * kSLPF + t) * 4u);
+      Zn[t] = HAS_Z ? buf_load<T>(rz, off(e0, r * kSLPF + t) * SZ) : 0.0f;
+    }
+  };
+  const bool sorted = n_per_d > 1 && n_per_d <= kSortMax;
+  if (sorted) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(xt - (wave * kSLRows + grp) * kSLTileSz), sOrd);
+  const int pos = sl_pos(wave, grp, nw);
+  auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
+    const int v = r0 + pos * S + sp;
+    return v < n_per_d ? (sorted ? sOrd[v] : v) : n_per_d;
+  };
+  auto channel = [&](int r0, int& e0, int& n) {
+    const int b = chan_at(r0);
+    const int64_t ch = (int64_t)d + (int64_t)b * dim;
+    e0 = b < n_per_d ? a.cu_seqlens[ch] : 0;
+    n = b < n_per_d ? a.cu_seqlens[ch + 1] - e0 : 0;
+    report_seqlen(a, n);
+  };
+  int e0, n;
+  channel(0, e0, n);
+  issue(e0, 0);
+  sl_build_table(sT, a, d, dti, dta);
+  __syncthreads();
+
+  for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
+    const int b = chan_at(r0);
+    const bool act = b < n_per_d;
+    const int64_t ch = (int64_t)d + (int64_t)b * dim;
+    if (r0 > 0) {
+      channel(r0, e0, n);
+      issue(e0, 0);
+    }
+    const int nblk = (n + kSLB - 1) / kSLB;
+    const int wblk = wave_max_dpp(nblk);
+    // The lane's event of block bk is e0 + 16·bk + s (out of range past the
+    // channel's end: the loads read the next channel's values or 0, unused).
+    // Blocks go in rounds of kSLPF: a round's loads are issued when the round
+    // before it starts, so each has a round of compute to arrive in.
+    float g = 0.0f, P = 1.0f, sdl = 0.0f;
+    auto block = [&](const int bk, const float uv, const int kk, const float zv) {
+      const int i = bk * kSLB + s;
+      const bool valid = i < n;
+      // padding events are identities: Δ = 0 -> a = 1 (table entry 0), Δu² = 0
+      const float dl = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+      const float du2 = dl * uv * uv;
+      const int big = valid && kk > kSLTab;
+      sdl += dl;
+      float av[kSLB];
+      tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * 4u : 0u);
+      if (__builtin_expect(__any(big), 0)) {  // gaps past the table: computed decays
+        for16([&](auto q) {
+          constexpr int Q = decltype(q)::value;
+          const float dq = bcast_f<Q>(dl);  // row-uniform condition: lane Q of the row is active
+          if (bcast_i<Q>(big)) av[Q] = decay(dq * Al);
+        });
+      }
+      for16([&](auto q) {
+        g = fmaf(av[q], g, bcast_f<decltype(q)::value>(du2));
+        if (EXACT) P *= av[q];
+        xt[q * (kSLN + 1) + s] = g;
+      });
+      wave_sync();
+      float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
+#pragma unroll
+      for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+      wave_sync();  // the tile is rewritten by the next block
+      const float y = fmaf(Dv, uv, uv * acc);
+      const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
+      buf_store<T>(ro, eo, y);
+      if (HAS_Z) buf_store<T>(roz, eo, y * (zv / (1.0f + __expf(-zv))));
+      // saved states at the block end: x after every 2048 events and after
+      // the channel's last one; chunk_g at every pass start
+      const int cend = min(n, (bk + 1) * kSLB);
+      const int xc = (cend - 1) / kXChunk;
+      const bool xsave = bk < nblk && (cend % kXChunk == 0 || cend == n) && xc < nck;
+      if (__any(xsave)) {
+        const float sd = row_sum(sdl);
+        if (xsave) {
+          const float Pn = EXACT ? P : decay(sd * Al);
+          reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, g * wb);
+        }
+      }
+      const int pend = (bk + 1) * kSLB;  // events before the next pass start, when it is one
+      if (a.chunk_g && pend % kSLPass == 0 && pend < n && pend / kSLPass < g_rows)
+        a.chunk_g[(ch * g_rows + pend / kSLPass) * N + s] = g * wb;
+    };
+    for (int r = 0; r * kSLPF < wblk; ++r) {
+      float U[kSLPF], Z[kSLPF];
+      int K[kSLPF];
+#pragma unroll
+      for (int t = 0; t < kSLPF; ++t) {
+        U[t] = Un[t];
+        K[t] = Kn[t];
+        Z[t] = Zn[t];
+      }
+      issue(e0, r + 1);
+#pragma unroll
+      for (int t = 0; t < kSLPF; ++t)
+        if (r * kSLPF + t < wblk) block(r * kSLPF + t, U[t], K[t], Z[t]);
+    }
+    // chunks past the channel's end keep the reference's zero state
+    if (act) {
+      for (int c = (n + kXChunk - 1) / kXChunk; c < nck; ++c) {
+        a.x[(ch * nck + c) * 2 * N + s] = 0.0f;
+        a.x[(ch * nck + c) * 2 * N + N + s] = 0.0f;
+      }
+    }
+  }
+}
+
+template <typename T, bool HAS_Z>
+__global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a) {
+  __shared__ float sT[kSLN * (kSLTab + 1)];
+  __shared__ int sOrd[kSortMax];
+  __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
+  const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
+  float* xt = &sX[wave][grp * kSLTileSz];
+  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt, sOrd);
+  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt, sOrd);
+}
+
+// ----------------------------------------------------------------- backward
+// A channel's passes of kSLPass events, last to first. Each pass rebuilds its
+// states g and decays a in registers from the pass-start state the forward
+// saved (phase A, blocks 0..3), then runs the adjoint backward through them
+// (phase B, blocks 3..0): e_i = doutu_i + f, f = a_i e_i carried to the
+// event before (and across passes). Per state lane: T0 = Σ tg, T1 = Σ tg·(k-1)
+// with tg = f·g_{i-1}, and Σ e·Δu² (dW_B; dW_C is the same sum, since
+// Σ_i dout_i u_i g_i = Σ_i e_i Δ_i u_i² over a channel). Per event lane:
+// Σ_s W_B W_C g_s (phase A) and Σ_s W_B W_C e_s (phase B) through the
+// transpose tile, then du, the Δ terms of ddt and dD.
+constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its dense row
+
+template <typename T, bool HAS_Z, bool DXR>
+__device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
+                                            float* sacc, int* sOrd, float* sdu) {
+  // no implicit fma contraction: the instantiations (with and without the
+  // dense rows) round alike, so their gradients are bit-equal; fmas are
+  // written out where they are meant
+#pragma clang fp contract(off)
+  constexpr uint32_t SZ = sizeof(T);
+  constexpr int N = kSLN;
+  constexpr int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
+  constexpr int NB = kSLPass / kSLB;  // blocks per pass
+  const int d = blockIdx.x % a.dim;
+  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
+  const int nw = blockDim.x / kWave;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
+  const int slot = wave * kSLRows + grp, nslots = nw * kSLRows;
+  const int NC = a.n_channels, dim = a.dim;
+  const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
+  const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
+
+  const float dti = a.dt_idle[d], dta = a.dt_active[d];
+  const float Dv = a.D ? a.D[d] : 0.0f;
+  const float Av = a.A[(int64_t)d * N + s];
+  const float Al = Av * kLog2e;
+  const float wb = a.W_B[(int64_t)d * N + s], wc = a.W_C[(int64_t)d * N + s];
+  const float wbc_s = wb * wc, wbca = wbc_s * Av;
+  float wbc[N];  // W_B·W_C of every state (the event lanes' weights; wave-uniform, scalar registers)
+#pragma unroll
+  for (int m = 0; m < N; ++m)
+    wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
+        __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  const uint32_t rowb = (uint32_t)(s * (kSLTab + 1) * 4);
+
+  for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
+  float* cacc = sacc + slot * NA;
+
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
+  const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.chunk_g, a.chunk_g ? a.chunk_g_bytes : 0);
+
+  // The lane's events of pass p: e0 + 32p + 16t + s (t = 0, 1); loads past
+  // the channel's end read the next channel's values or 0 and are unused.
+  // A pass's loads are issued when the pass after it (in the walk: before
+  // it) starts; unconditional, so the registers never merge with old values.
+  float Un[NB], Dn[NB], Zn[NB], On[NB], Gn;
+  int Kn[NB];
+  auto issue = [&](int e0, int64_t ch, int p) {
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const uint32_t o = (uint32_t)(e0 + p * kSLPass + t * kSLB + s);
+      Un[t] = buf_load<T>(ru, o * SZ);
+      Kn[t] = buf_load_i32(rk, o * 4u);
+      Dn[t] = buf_load<T>(rdo, o * SZ);
+      Zn[t] = HAS_Z ? buf_load<T>(rz, o * SZ) : 0.0f;
+      On[t] = HAS_Z ? buf_load<T>(ros, o * SZ) : 0.0f;
+    }
+    // pass-start state h of pass p (chunk_g row p, written by the forward)
+    Gn = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+        rg, (uint32_t)(((ch * g_rows + p) * N + s) * 4), 0, 0));
+  };
+  const bool sorted = n_per_d > 1 && n_per_d <= kSortMax;
+  if (sorted) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(xt - (wave * kSLRows + grp) * kSLTileSz), sOrd);
+  const int pos = sl_pos(wave, grp, nw);
+  auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
+    const int v = r0 + pos * S + sp;
+    return v < n_per_d ? (sorted ? sOrd[v] : v) : n_per_d;
+  };
+  auto channel = [&](int r0, int& e0, int& n, int64_t& ch) {
+    const int b = chan_at(r0);
+    ch = (int64_t)d + (int64_t)b * dim;
+    e0 = b < n_per_d ? a.cu_seqlens[ch] : 0;
+    n = b < n_per_d ? a.cu_seqlens[ch + 1] - e0 : 0;
+    report_seqlen(a, n);
+  };
+  int e0, n;
+  int64_t ch;
+  channel(0, e0, n, ch);
+  // at least one pass: the dense rows of empty channels are written by it
+  int wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
+  issue(e0, ch, wp - 1);
+  sl_build_table(sT, a, d, dti, dta);
+  __syncthreads();
+
+  for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
+    if (r0 > 0) {
+      channel(r0, e0, n, ch);
+      wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
+      issue(e0, ch, wp - 1);
+    }
+    const bool act = chan_at(r0) < n_per_d;
+    const int np = (n + kSLPass - 1) / kSLPass;
+    float f = 0.0f;  // a·e of the event after the current one
+    float T0 = 0.0f, T1 = 0.0f, dWB = 0.0f, ddti_l = 0.0f, ddta_l = 0.0f, dD_l = 0.0f;
+    for (int p = wp - 1; p >= 0; --p) {
+      float uv[NB], gg[NB], dl[NB], km[NB], du2[NB], doutu[NB], acc2[NB];
+      uint32_t tb[NB];
+      int big[NB];
+      // the lane's own events of the pass: Δ, Δu², the gated dout (and dz)
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        const int i = p * kSLPass + t * kSLB + s;
+        const bool valid = i < n;
+        const int kk = Kn[t];
+        uv[t] = Un[t];
+        float dv = Dn[t];
+        if (HAS_Z) {
+          const float zv = Zn[t], ov = On[t];
+          const float sg = 1.0f / (1.0f + __expf(-zv));
+          buf_store<T>(rdz, valid ? (uint32_t)(e0 + i) * SZ : kBufOOB, dv * ov * sg * (1.0f + zv * (1.0f - sg)));
+          dv *= zv * sg;
+        }
+        gg[t] = dv;
+        dl[t] = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+        km[t] = valid ? (float)(kk - 1) : 0.0f;
+        du2[t] = dl[t] * uv[t] * uv[t];
+        doutu[t] = valid ? dv * uv[t] : 0.0f;
+        tb[t] = valid ? (uint32_t)min(kk, kSLTab) * 4u : 0u;
+        big[t] = valid && kk > kSLTab;
+      }
+      const float h0 = Gn;
+      const float g_in = (p >= 1 && p < np && p < g_rows && wb != 0.0f) ? h0 / wb : 0.0f;
+      issue(e0, ch, p - 1);  // the next pass of the walk (past the start: unused)
+      // ---- phase A: states and decays of the pass, Σ_s W_B W_C g_s per event
+      float gb[kSLPass], ab[kSLPass];
+      float g = g_in;
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        float av[kSLB];
+        tab16(av, sT, rowb, tb[t]);
+        if (__builtin_expect(__any(big[t]), 0)) {  // gaps past the table: computed decays
+          for16([&](auto q) {
+            constexpr int Q = decltype(q)::value;
+            const float dq = bcast_f<Q>(dl[t]);  // row-uniform condition: lane Q of the row is active
+            if (bcast_i<Q>(big[t])) av[Q] = decay(dq * Al);
+          });
+        }
+        for16([&](auto q) {
+          constexpr int Q = decltype(q)::value;
+          g = fmaf(av[Q], g, bcast_f<Q>(du2[t]));
+          gb[t * kSLB + Q] = g;
+          ab[t * kSLB + Q] = av[Q];
+          xt[Q * (kSLN + 1) + s] = g;
+        });
+        wave_sync();
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+        acc2[t] = acc;
+        wave_sync();
+      }
+      // ---- phase B: the adjoint, blocks and events last to first
+#pragma unroll
+      for (int tt = 0; tt < NB; ++tt) {
+        const int t = NB - 1 - tt;
+        rfor16([&](auto q) {
+          constexpr int Q = decltype(q)::value;
+          const int I = t * kSLB + Q;
+          const float e = f + bcast_f<Q>(doutu[t]);
+          f = ab[I] * e;
+          const float tg = f * (I > 0 ? gb[I > 0 ? I - 1 : 0] : g_in);
+          T0 += tg;
+          fmac_bcast<Q, Q == kSLB - 1>(T1, km[t], tg);   // T1 += (k-1)·tg
+          fmac_bcast<Q, Q == kSLB - 1>(dWB, du2[t], e);  // dWB += Δu²·e
+          xt[Q * (kSLN + 1) + s] = e;
+        });
+        wave_sync();
+        float acc1 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < N; ++m) acc1 = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc1);
+        wave_sync();
+        // the lane's own event of block t: du, the Δu² terms of ddt, dD
+        const int i = p * kSLPass + t * kSLB + s;
+        const float duv = fmaf(gg[t], Dv + acc2[t], 2.0f * dl[t] * uv[t] * acc1);
+        const float dd = uv[t] * uv[t] * acc1;  // the A-term of dΔ goes into ddt through T0, T1
+        ddti_l = fmaf(dd, km[t], ddti_l);
+        ddta_l += dd;
+        dD_l += doutu[t];
+        const bool valid = i < n;
+        buf_store<T>(rdu, valid ? (uint32_t)(e0 + i) * SZ : kBufOOB, duv);
+        if (DXR && valid) sdu[i] = duv;  // the channel's du in event order, for its dense row
+      }
+    }
+    // the channel's parameter-gradient terms into the slot's accumulators
+    ddti_l = fmaf(wbca, T1, ddti_l);
+    ddta_l = fmaf(wbca, T0, ddta_l);
+    ddti_l = row_sum(ddti_l);
+    ddta_l = row_sum(ddta_l);
+    dD_l = row_sum(dD_l);
+    if (act) {
+      cacc[s] = fmaf(wbc_s, fmaf(dti, T1, dta * T0), cacc[s]);
+      cacc[N + s] = fmaf(dWB, wc, cacc[N + s]);
+      cacc[2 * N + s] = fmaf(dWB, wb, cacc[2 * N + s]);
+      if (s == 0) {
+        cacc[3 * N] += ddti_l;
+        cacc[3 * N + 1] += ddta_l;
+        cacc[3 * N + 2] += dD_l;
+      }
+    }
+    if constexpr (DXR) {
+      // dense gradient row of the channel from its du in LDS (event order):
+      // the row's 16 lanes take one 64-step tile per store, lane j writing
+      // steps 4j..4j+3, each value the next event's du masked by the step's
+      // bit (0 / -1), the LDS index advancing one slot per set bit
+      wave_sync();
+      if (act) {
+        const uint32_t* mrow = rw.bitmask + (ch / rw.mrd) * rw.W;
+        const int32_t* tsr = rw.ts + ch * (rw.nT + 1);
+        T* dr = static_cast<T*>(rw.dx) + ch * rw.L;
+        const int L = (int)rw.L;
+        const int off = 4 * s;  // the lane's first step in a tile
+        const uint32_t lo_keep = off >= 32 ? 0xFFFFFFFFu : (1u << off) - 1u;
+        const uint32_t hi_keep = off > 32 ? (1u << (off - 32)) - 1u : 0u;
+        const uint32_t sh = (uint32_t)off & 31u;
+        auto seg = [&](uint64_t m, int32_t tv, int t0) {
+          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+          int e = tv - e0 + (int)(__builtin_popcount(mlo & lo_keep) + __builtin_popcount(mhi & hi_keep));
+          const uint32_t w = off >= 32 ? mhi : mlo;
+          uint32_t o[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int32_t mk = __builtin_amdgcn_sbfe((int32_t)w, sh + (uint32_t)k, 1u);
+            o[k] = __float_as_uint(sdu[min(max(e, 0), kSLRowCap - 1)]) & (uint32_t)mk;
+            e -= mk;
+          }
+          if constexpr (sizeof(T) == 4) {
+            st_stream(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(dr + t0));
+          } else {
+            T h[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) h[k] = from_f<T>(__uint_as_float(o[k]));
+            st_stream(*reinterpret_cast<u32x2*>(h), reinterpret_cast<u32x2*>(dr + t0));
+          }
+        };
+        const int nfull = L / kTile;  // tiles whose 64 steps are all < L
+        constexpr int BAT = 8;
+        int q0 = 0;
+        for (; q0 + BAT <= nfull; q0 += BAT) {
+          uint64_t m[BAT];
+          int32_t tv[BAT];
+#pragma unroll
+          for (int i = 0; i < BAT; ++i) {  // masks and table entries in flight together
+            m[i] = tile_mask(mrow, q0 + i);
+            tv[i] = tsr[q0 + i];
+          }
+#pragma unroll
+          for (int i = 0; i < BAT; ++i) seg(m[i], tv[i], (q0 + i) * kTile + off);
+        }
+        for (; q0 < nfull; ++q0) seg(tile_mask(mrow, q0), tsr[q0], q0 * kTile + off);
+        // a last partial tile (L % 64 != 0; L % 4 == 0, so a lane's 4 steps
+        // are all in range or all past the end)
+        if (nfull * kTile < L && nfull * kTile + off < L) seg(tile_mask(mrow, nfull), tsr[nfull], nfull * kTile + off);
+      }
+      wave_sync();  // the du row is rewritten by the next round's channel
+    }
+  }
+  // the workgroup's parameter gradients: slots summed in a fixed order
+  __syncthreads();
+  for (int i = threadIdx.x; i < NA; i += blockDim.x) {
+    float v = 0.0f;
+    for (int sl = 0; sl < nslots; ++sl) v += sacc[sl * NA + i];
+    if (S > 1) a.split_ws[((int64_t)sp * a.dim + d) * NA + i] = v;  // summed by k_scan_param_reduce
+    else store_param_grad(a, d, N, i, v);
+  }
+}
+
+template <typename T, bool HAS_Z, bool DXR>
+__global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw) {
+  __shared__ float sT[kSLN * (kSLTab + 1)];
+  __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
+  __shared__ float sacc[kScanThreads / kWave * kSLRows * (3 * kSLN + 3)];
+  __shared__ int sOrd[kSortMax];
+  extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
+  const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
+  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sOrd, sdu + (wave * kSLRows + grp) * kSLRowCap);
+}
+
+// ------------------------------------------------------------------- host
+// Which family runs a dstate-16 scan. The state lanes give one wave per four
+// channels, so they pay when the channels fill two waves per SIMD (below
+// that, each wave's dependent chain is exposed and the lane groups of
+// scan.hip, which split a channel over 16 lanes, are faster: config 2 has
+// 4096 channels and runs 2.7 µs per step slower on the state lanes).
+// BCM_SCAN_KERNEL=lanes / items overrides the choice (read on every call:
+// the tests run both families on the same shapes).
+bool sl_applies(const bcm_scan_args& a) {
+  if (a.dstate != kSLN) return false;
+  const char* v = std::getenv("BCM_SCAN_KERNEL");
+  if (v && v[0] == 'l') return true;
+  if (v && v[0] == 'i') return false;
+  return (int64_t)a.n_channels >= 2ll * kSLRows * 4 * device_cus();
+}
+
+int sl_split(const bcm_scan_args& a) {
+  const int per_d = (a.n_channels + a.dim - 1) / a.dim;
+  const int nslots = (kScanThreads / kWave) * kSLRows;
+  const int rounds = (per_d + nslots - 1) / nslots;
+  const int cus = device_cus();
+  if (a.dim < cus && rounds > 1) return std::min(rounds, std::max(1, cus / a.dim));
+  return 1;
+}
+
+static int sl_waves(const bcm_scan_args& a) {
+  const int per_d = (a.n_channels + a.dim - 1) / a.dim;
+  const int nw = (per_d + kSLRows - 1) / kSLRows;
+  return std::max(1, std::min(kScanThreads / kWave, nw));
+}
+
+int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
+  const dim3 grid((unsigned)((int64_t)a.dim * sl_split(a))), block((unsigned)(sl_waves(a) * kWave));
+  static const size_t pad = [] {
+    const char* v = std::getenv("BCM_SL_PAD");
+    return v ? (size_t)std::atoi(v) : (size_t)0;
+  }();
+  dispatch_dtype(a.dtype, [&](auto tag) {
+    using T = decltype(tag);
+    if (a.z) hipLaunchKernelGGL((k_scan_fwd_sl<T, true>), grid, block, pad, st, a);
+    else hipLaunchKernelGGL((k_scan_fwd_sl<T, false>), grid, block, pad, st, a);
+  });
+  return check_launch(fn);
+}
+
+int sl_launch_bwd(const bcm_scan_args& a, hipStream_t st, const char* fn, const ScanRows* rw) {
+  int S = sl_split(a);
+  // no (or too small a) workspace for the partials: one workgroup per model channel
+  if (!a.split_ws || a.split_ws_bytes < 4 * (int64_t)S * a.dim * (3 * a.dstate + 3)) S = 1;
+  const int nw = sl_waves(a);
+  const dim3 grid((unsigned)((int64_t)a.dim * S)), block((unsigned)(nw * kWave));
+  const ScanRows rows = rw ? *rw : ScanRows{};
+  dispatch_dtype(a.dtype, [&](auto tag) {
+    using T = decltype(tag);
+    if (rw) hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st, a, rows);
+    else if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false>), grid, block, 0, st, a, rows);
+    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false>), grid, block, 0, st, a, rows);
+  });
+  int rc = check_launch(fn);
+  if (rc || S == 1) return rc;
+  return sl_param_reduce(a, S, st, fn);
+}
+
+// The dense rows come from the kernel for channels whose events fit the
+// LDS row (max_seqlen <= kSLRowCap), no z, 4-step aligned rows.
+bool sl_rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(r.dx);
+  return !a.z && a.max_seqlen <= kSLRowCap && r.seqlen % 4 == 0 && p % (4 * dtype_size(a.dtype)) == 0;
+}
+
+}  // namespace bcm

@@ -39,3 +39,12 @@ def cuda_device():
     import bc_mamba_amd._native as nat
     nat.lib()  # fail loudly if the library is not built
     return torch.device("cuda:0")
+
+
+@pytest.fixture(params=["items", "lanes"])
+def scan_kernel(request, monkeypatch):
+    """Runs a test under each dstate-16 depthwise scan family: the lane
+    groups over items (scan.hip) and the lanes over states (scan_sl.hip),
+    forced with BCM_SCAN_KERNEL (the library reads it on every call)."""
+    monkeypatch.setenv("BCM_SCAN_KERNEL", request.param)
+    return request.param

@@ -123,9 +123,10 @@ def check_param_grads(st, grads_ref, rtol=1e-4):
 
 
 @pytest.mark.parametrize("cfg", [1, 2])
-def test_config_full_size_bench_kernels(cuda_device, cfg):
+def test_config_full_size_bench_kernels(cuda_device, cfg, scan_kernel):
     """Configs 1 (fp32, 15 %) and 2 (bf16 u / out / dout, token embedding,
-    L 4096, 10 %): the whole step at full size, every channel."""
+    L 4096, 10 %): the whole step at full size, every channel, under both
+    dstate-16 scan families."""
     w, st = run_step(cfg, cuda_device)
     och, ot, ok, ocu, oms = check_indices(w, st)
     check_restore(w, st, och, ot, ocu)

@@ -12,7 +12,8 @@ from bc_mamba_amd import selective_scan_interface as ssi
 from conftest import assert_close
 from oracle import event_path as orc
 
-pytestmark = pytest.mark.gpu
+# every case under both dstate-16 kernel families (other dstates: the same kernel twice)
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("scan_kernel")]
 
 TOL = {torch.float32: (1e-4, 1e-6), torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3)}
 

@@ -14,7 +14,8 @@ from bc_mamba_amd import restore_dense_cuda_nodecay as rdc
 from bc_mamba_amd import selective_scan_cuda as ssc
 from test_gpu_scan import _case
 
-pytestmark = pytest.mark.gpu
+# every case under both dstate-16 kernel families (other dstates: the same kernel twice)
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("scan_kernel")]
 
 CASES = [  # B, D, L, density, N, dtype, with_z, p_short  (one kernel unless noted)
     (2, 8, 100, 0.5, 16, torch.float32, False, None),    # one 64-step tile and a partial one
