@@ -129,33 +129,33 @@ __device__ __forceinline__ bool sl_exact(const bcm_scan_args& a, int d) {
   return ex;
 }
 
-// Decay table of model channel d, row by row: T[m][0] = 1 (padding),
-// T[m][k] = the decay of gap k, the same expression as the per-event path.
-// A[d, m] is wave-uniform (a scalar load), so the build waits on no vector
-// load: the first events' loads, issued before it, stay in flight.
-__device__ __forceinline__ void sl_build_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
-#pragma unroll 1
-  for (int m = 0; m < kSLN; ++m) {
-    const float Alm = a.A[(int64_t)d * kSLN + m] * kLog2e;
-    for (int q = threadIdx.x; q <= kSLTab; q += blockDim.x)
-      sT[m * (kSLTab + 1) + q] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * Alm);
-  }
-}
+// The decay table holds two copies interleaved, T[k][m][parity]: lane
+// (row g, state m) reads word 32k + 2m + (g & 1), so the two rows (channels)
+// of a half-wave read disjoint banks whatever their gaps k (one bank per
+// lane: conflict-free). Byte offset of gap k in it, and a lane's base.
+constexpr uint32_t kSLTabGap = 2 * kSLN * 4;
+constexpr int kSLTabSz = 2 * kSLN * (kSLTab + 1);  // floats
+__device__ __forceinline__ uint32_t sl_tab_lane(int s, int grp) { return (uint32_t)(2 * s + (grp & 1)) * 4u; }
 
-// Slot order of a workgroup's channels (ch = d + b·dim, b < n_per_d): with
-// several channels, ord[rank] = b longest first (rank_channels); the slot at
-// position pos of workgroup sp in round r0 takes rank r0 + pos·S + sp, the
-// first half of the waves positions 0.., the second half in reverse, so the
-// two waves of a SIMD (w and w + 4 of 8) pair long channels with short ones
-// and a wave's four rows hold neighbouring lengths.
-__device__ __forceinline__ int sl_pos(int wave, int grp, int nw) {
-  const int hw = (nw + 1) / 2;
-  return (wave < hw ? wave : nw - 1 - (wave - hw)) * kSLRows + grp;
+// Decay table of model channel d: T[m][0] = 1 (padding), T[m][k] = the
+// decay of gap k, the same expression as the per-event path. Thread t
+// builds the entries of state t % 16 (consecutive threads: consecutive
+// words); its A value is loaded at the kernel's start (al), before the
+// first events' loads, so the build waits on no data load.
+__device__ __forceinline__ float sl_table_al(const bcm_scan_args& a, int d) {
+  return a.A[(int64_t)d * kSLN + threadIdx.x % kSLN] * kLog2e;
+}
+__device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, float dta) {
+  const int m = threadIdx.x % kSLN;
+  for (int q = threadIdx.x / kSLN; q <= kSLTab; q += blockDim.x / kSLN) {
+    const float v = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * al);
+    reinterpret_cast<float2*>(sT)[q * kSLN + m] = make_float2(v, v);
+  }
 }
 
 // ------------------------------------------------------------------ forward
 template <typename T, bool HAS_Z, bool EXACT>
-__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int* sOrd) {
+__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt) {
 #pragma clang fp contract(off)  // fmas are written out where they are meant
   constexpr uint32_t SZ = sizeof(T);
   constexpr int N = kSLN;
@@ -169,6 +169,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
   const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
 
+  const float al = sl_table_al(a, d);  // first load of the kernel: the table build waits for it alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
   const float Al = a.A[(int64_t)d * N + s] * kLog2e;
@@ -178,7 +179,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   for (int m = 0; m < N; ++m)
     wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
         __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
-  const uint32_t rowb = (uint32_t)(s * (kSLTab + 1) * 4);
+  const uint32_t rowb = sl_tab_lane(s, grp);
 
   const int64_t E = a.n_events;
   const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
@@ -199,12 +200,10 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
       Zn[t] = HAS_Z ? buf_load<T>(rz, off(e0, r * kSLPF + t) * SZ) : 0.0f;
     }
   };
-  const bool sorted = n_per_d > 1 && n_per_d <= kSortMax;
-  if (sorted) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(xt - (wave * kSLRows + grp) * kSLTileSz), sOrd);
-  const int pos = sl_pos(wave, grp, nw);
+  const int slot = wave * kSLRows + grp;
   auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
-    const int v = r0 + pos * S + sp;
-    return v < n_per_d ? (sorted ? sOrd[v] : v) : n_per_d;
+    const int v = r0 + slot * S + sp;
+    return v < n_per_d ? v : n_per_d;
   };
   auto channel = [&](int r0, int& e0, int& n) {
     const int b = chan_at(r0);
@@ -216,7 +215,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   int e0, n;
   channel(0, e0, n);
   issue(e0, 0);
-  sl_build_table(sT, a, d, dti, dta);
+  sl_build_table(sT, al, dti, dta);
   __syncthreads();
 
   for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
@@ -243,7 +242,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
       const int big = valid && kk > kSLTab;
       sdl += dl;
       float av[kSLB];
-      tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * 4u : 0u);
+      tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u);
       if (__builtin_expect(__any(big), 0)) {  // gaps past the table: computed decays
         for16([&](auto q) {
           constexpr int Q = decltype(q)::value;
@@ -307,13 +306,12 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
 
 template <typename T, bool HAS_Z>
 __global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a) {
-  __shared__ float sT[kSLN * (kSLTab + 1)];
-  __shared__ int sOrd[kSortMax];
+  __shared__ float sT[kSLTabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
   float* xt = &sX[wave][grp * kSLTileSz];
-  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt, sOrd);
-  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt, sOrd);
+  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt);
+  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt);
 }
 
 // ----------------------------------------------------------------- backward
@@ -330,7 +328,7 @@ constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its den
 
 template <typename T, bool HAS_Z, bool DXR>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
-                                            float* sacc, int* sOrd, float* sdu) {
+                                            float* sacc, float* sdu) {
   // no implicit fma contraction: the instantiations (with and without the
   // dense rows) round alike, so their gradients are bit-equal; fmas are
   // written out where they are meant
@@ -349,6 +347,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
   const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
 
+  const float al = sl_table_al(a, d);  // first load of the kernel: the table build waits for it alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
   const float Av = a.A[(int64_t)d * N + s];
@@ -360,7 +359,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   for (int m = 0; m < N; ++m)
     wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
         __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
-  const uint32_t rowb = (uint32_t)(s * (kSLTab + 1) * 4);
+  const uint32_t rowb = sl_tab_lane(s, grp);
 
   for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
   float* cacc = sacc + slot * NA;
@@ -392,12 +391,9 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
     Gn = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
         rg, (uint32_t)(((ch * g_rows + p) * N + s) * 4), 0, 0));
   };
-  const bool sorted = n_per_d > 1 && n_per_d <= kSortMax;
-  if (sorted) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(xt - (wave * kSLRows + grp) * kSLTileSz), sOrd);
-  const int pos = sl_pos(wave, grp, nw);
   auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
-    const int v = r0 + pos * S + sp;
-    return v < n_per_d ? (sorted ? sOrd[v] : v) : n_per_d;
+    const int v = r0 + slot * S + sp;
+    return v < n_per_d ? v : n_per_d;
   };
   auto channel = [&](int r0, int& e0, int& n, int64_t& ch) {
     const int b = chan_at(r0);
@@ -412,7 +408,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   // at least one pass: the dense rows of empty channels are written by it
   int wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
   issue(e0, ch, wp - 1);
-  sl_build_table(sT, a, d, dti, dta);
+  sl_build_table(sT, al, dti, dta);
   __syncthreads();
 
   for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
@@ -448,7 +444,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         km[t] = valid ? (float)(kk - 1) : 0.0f;
         du2[t] = dl[t] * uv[t] * uv[t];
         doutu[t] = valid ? dv * uv[t] : 0.0f;
-        tb[t] = valid ? (uint32_t)min(kk, kSLTab) * 4u : 0u;
+        tb[t] = valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u;
         big[t] = valid && kk > kSLTab;
       }
       const float h0 = Gn;
@@ -599,13 +595,12 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
 
 template <typename T, bool HAS_Z, bool DXR>
 __global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw) {
-  __shared__ float sT[kSLN * (kSLTab + 1)];
+  __shared__ float sT[kSLTabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   __shared__ float sacc[kScanThreads / kWave * kSLRows * (3 * kSLN + 3)];
-  __shared__ int sOrd[kSortMax];
   extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
-  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sOrd, sdu + (wave * kSLRows + grp) * kSLRowCap);
+  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sdu + (wave * kSLRows + grp) * kSLRowCap);
 }
 
 // ------------------------------------------------------------------- host
