@@ -22,13 +22,18 @@ namespace bcm {
 // Sum and maximum of the block's row counts (one value per wave, uniform in
 // the wave) to bsum[blockIdx] / bmax[blockIdx]. Every wave of the block
 // calls it once (rows past the end with 0).
+// Threads per block of the count and fill launches: kernels use the constant,
+// not blockDim (whose load from the launch's implicit arguments would come
+// first, one more round trip before any work).
+constexpr int kExBlock = 256;
+
 __device__ __forceinline__ void block_totals(int cnt, int32_t* bsum, int32_t* bmax) {
   __shared__ int s_c[4];
   if (lane_id() == 0) s_c[threadIdx.x / kWave] = cnt;
   __syncthreads();
   if (threadIdx.x == 0) {
     int sm = 0, mx = 0;
-    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+    for (int w = 0; w < kExBlock / kWave; ++w) {
       sm += s_c[w];
       mx = max(mx, s_c[w]);
     }
@@ -54,7 +59,7 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   constexpr int WPG = GS / 32;         // words per group
   constexpr int BATCH = 8;
   const int lane = lane_id();
-  const int64_t row = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int64_t row = (int64_t)blockIdx.x * (kExBlock / kWave) + threadIdx.x / kWave;
   // the row's bits and event count (0 for a row past the end)
   auto count_row = [&]() {
     const T* xr = x + row * L;
@@ -320,11 +325,11 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
     const bool first = blockIdx.x == 0 && bpre == nullptr;
     int sm = 0, mx = 0;  // blocks before this one (all blocks for block 0's totals)
     const int64_t lim = bpre ? 0 : (first ? nblk : (int64_t)blockIdx.x);
-    for (int64_t i0 = 0; i0 < lim; i0 += 8 * (int64_t)blockDim.x) {  // 8 independent loads per thread in flight
+    for (int64_t i0 = 0; i0 < lim; i0 += 8 * kExBlock) {  // 8 independent loads per thread in flight
       int vs[8], vm[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int64_t i = i0 + q * (int64_t)blockDim.x + threadIdx.x;
+        const int64_t i = i0 + q * kExBlock + threadIdx.x;
         vs[q] = i < lim ? bsum[i] : 0;
         vm[q] = (first && i < lim) ? bmax[i] : 0;
       }

@@ -70,12 +70,20 @@ struct TileWave {
 // past `dim` are clamped to the group's last channel (addresses stay valid)
 // and flagged !ok.
 // nPos: positions along time per (b, g); nT: tiles per row of the tile table.
-__device__ __forceinline__ TileWave tile_wave(int nPos, int nG, int dim, const int32_t* tile_start, int nT) {
+// The tile kernels run 256-thread blocks, (waves + 3) / 4 of them: the wave id
+// comes from these constants and the `waves` argument, not from the launch's
+// implicit arguments (whose loads would come first, one round trip each).
+constexpr int kTileWaves = 4;  // waves per block
+__device__ __forceinline__ int tile_wave_id(int waves) {
+  return xcd_block(blockIdx.x, (waves + kTileWaves - 1) / kTileWaves) * kTileWaves + (int)(threadIdx.x / kWave);
+}
+
+__device__ __forceinline__ TileWave tile_wave(int nPos, int nG, int dim, const int32_t* tile_start, int nT,
+                                              int waves) {
   TileWave w;
   // wave-uniform by construction; readfirstlane lets the compiler keep it (and
   // the buffer descriptors built from it) in SGPRs
-  const int wid = __builtin_amdgcn_readfirstlane(xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
-                                                 (int)(threadIdx.x / kWave));
+  const int wid = __builtin_amdgcn_readfirstlane(tile_wave_id(waves));
   w.g = wid % nG;
   const int bj = wid / nG;
   w.j = bj % nPos;
@@ -94,8 +102,8 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
                                                      const int32_t* __restrict__ tile_start, int nT, int nG,
                                                      int waves, int dim, int64_t L, int64_t out_elems,
                                                      TO* __restrict__ out) {
-  if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
-  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT);
+  if (tile_wave_id(waves) >= waves) return;
+  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT, waves);
   const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
   const int32_t cu0 = ts[0], elo = ts[w.j];
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
@@ -153,8 +161,8 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
                                                               float* __restrict__ head, float* __restrict__ tail,
                                                               int32_t* __restrict__ tend) {
   __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
-  if (xcd_block(blockIdx.x, gridDim.x) * (blockDim.x / kWave) + (int)(threadIdx.x / kWave) >= waves) return;
-  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT);
+  if (tile_wave_id(waves) >= waves) return;
+  const TileWave w = tile_wave(nT, nG, dim, tile_start, nT, waves);
   const int wave = threadIdx.x / kWave, lane = lane_id();
   // dout rows of the tile; steps past L and lanes past dim read 0
   const int64_t t0 = (int64_t)w.j * kTile;
@@ -234,7 +242,7 @@ __global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_r
                                                          const float* __restrict__ tail,
                                                          const int32_t* __restrict__ tend, float* __restrict__ dy,
                                                          int64_t n_events) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
   if (i >= nT * n_rows) return;
   const int32_t e_end = tend[i];
   // no event in the tile (its head belongs to an earlier tile's owner); an

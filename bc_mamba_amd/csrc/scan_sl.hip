@@ -145,9 +145,9 @@ __device__ __forceinline__ uint32_t sl_tab_lane(int s, int grp) { return (uint32
 __device__ __forceinline__ float sl_table_al(const bcm_scan_args& a, int d) {
   return a.A[(int64_t)d * kSLN + threadIdx.x % kSLN] * kLog2e;
 }
-__device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, float dta) {
+__device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, float dta, int nw) {
   const int m = threadIdx.x % kSLN;
-  for (int q = threadIdx.x / kSLN; q <= kSLTab; q += blockDim.x / kSLN) {
+  for (int q = threadIdx.x / kSLN; q <= kSLTab; q += nw * (kWave / kSLN)) {
     const float v = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * al);
     reinterpret_cast<float2*>(sT)[q * kSLN + m] = make_float2(v, v);
   }
@@ -155,13 +155,12 @@ __device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, f
 
 // ------------------------------------------------------------------ forward
 template <typename T, bool HAS_Z, bool EXACT>
-__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt) {
+__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int nw, int S) {
 #pragma clang fp contract(off)  // fmas are written out where they are meant
   constexpr uint32_t SZ = sizeof(T);
   constexpr int N = kSLN;
   const int d = blockIdx.x % a.dim;
-  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
-  const int nw = blockDim.x / kWave;
+  const int sp = blockIdx.x / a.dim;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
   const int nslots = nw * kSLRows;
@@ -215,7 +214,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   int e0, n;
   channel(0, e0, n);
   issue(e0, 0);
-  sl_build_table(sT, al, dti, dta);
+  sl_build_table(sT, al, dti, dta, nw);
   __syncthreads();
 
   for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
@@ -304,14 +303,17 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   }
 }
 
+// nw: waves per workgroup, S: workgroups per model channel (the launch's
+// shape, passed rather than read from blockDim / gridDim, whose loads would
+// come before any other work)
 template <typename T, bool HAS_Z>
-__global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a) {
+__global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a, int nw, int S) {
   __shared__ float sT[kSLTabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
   float* xt = &sX[wave][grp * kSLTileSz];
-  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt);
-  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt);
+  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt, nw, S);
+  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt, nw, S);
 }
 
 // ----------------------------------------------------------------- backward
@@ -328,7 +330,7 @@ constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its den
 
 template <typename T, bool HAS_Z, bool DXR>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
-                                            float* sacc, float* sdu) {
+                                            float* sacc, float* sdu, int nw, int S) {
   // no implicit fma contraction: the instantiations (with and without the
   // dense rows) round alike, so their gradients are bit-equal; fmas are
   // written out where they are meant
@@ -338,8 +340,8 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   constexpr int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
   constexpr int NB = kSLPass / kSLB;  // blocks per pass
   const int d = blockIdx.x % a.dim;
-  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
-  const int nw = blockDim.x / kWave;
+  const int sp = blockIdx.x / a.dim;
+  const int nthr = nw * kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
   const int slot = wave * kSLRows + grp, nslots = nw * kSLRows;
@@ -361,7 +363,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
   const uint32_t rowb = sl_tab_lane(s, grp);
 
-  for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
+  for (int i = threadIdx.x; i < nslots * NA; i += nthr) sacc[i] = 0.0f;
   float* cacc = sacc + slot * NA;
 
   const int64_t E = a.n_events;
@@ -408,7 +410,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   // at least one pass: the dense rows of empty channels are written by it
   int wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
   issue(e0, ch, wp - 1);
-  sl_build_table(sT, al, dti, dta);
+  sl_build_table(sT, al, dti, dta, nw);
   __syncthreads();
 
   for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
@@ -585,7 +587,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   }
   // the workgroup's parameter gradients: slots summed in a fixed order
   __syncthreads();
-  for (int i = threadIdx.x; i < NA; i += blockDim.x) {
+  for (int i = threadIdx.x; i < NA; i += nthr) {
     float v = 0.0f;
     for (int sl = 0; sl < nslots; ++sl) v += sacc[sl * NA + i];
     if (S > 1) a.split_ws[((int64_t)sp * a.dim + d) * NA + i] = v;  // summed by k_scan_param_reduce
@@ -594,13 +596,15 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
 }
 
 template <typename T, bool HAS_Z, bool DXR>
-__global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw) {
+__global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw, int nw,
+                                                               int S) {
   __shared__ float sT[kSLTabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   __shared__ float sacc[kScanThreads / kWave * kSLRows * (3 * kSLN + 3)];
   extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
-  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sdu + (wave * kSLRows + grp) * kSLRowCap);
+  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sdu + (wave * kSLRows + grp) * kSLRowCap,
+                             nw, S);
 }
 
 // ------------------------------------------------------------------- host
@@ -635,15 +639,12 @@ static int sl_waves(const bcm_scan_args& a) {
 }
 
 int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
-  const dim3 grid((unsigned)((int64_t)a.dim * sl_split(a))), block((unsigned)(sl_waves(a) * kWave));
-  static const size_t pad = [] {
-    const char* v = std::getenv("BCM_SL_PAD");
-    return v ? (size_t)std::atoi(v) : (size_t)0;
-  }();
+  const int S = sl_split(a), nw = sl_waves(a);
+  const dim3 grid((unsigned)((int64_t)a.dim * S)), block((unsigned)(nw * kWave));
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (a.z) hipLaunchKernelGGL((k_scan_fwd_sl<T, true>), grid, block, pad, st, a);
-    else hipLaunchKernelGGL((k_scan_fwd_sl<T, false>), grid, block, pad, st, a);
+    if (a.z) hipLaunchKernelGGL((k_scan_fwd_sl<T, true>), grid, block, 0, st, a, nw, S);
+    else hipLaunchKernelGGL((k_scan_fwd_sl<T, false>), grid, block, 0, st, a, nw, S);
   });
   return check_launch(fn);
 }
@@ -657,9 +658,11 @@ int sl_launch_bwd(const bcm_scan_args& a, hipStream_t st, const char* fn, const 
   const ScanRows rows = rw ? *rw : ScanRows{};
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (rw) hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st, a, rows);
-    else if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false>), grid, block, 0, st, a, rows);
-    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false>), grid, block, 0, st, a, rows);
+    if (rw)
+      hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st, a,
+                         rows, nw, S);
+    else if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false>), grid, block, 0, st, a, rows, nw, S);
+    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false>), grid, block, 0, st, a, rows, nw, S);
   });
   int rc = check_launch(fn);
   if (rc || S == 1) return rc;
