@@ -102,6 +102,9 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
                                                      const int32_t* __restrict__ tile_start, int nT, int nG,
                                                      int waves, int dim, int64_t L, int64_t out_elems,
                                                      TO* __restrict__ out) {
+  // the arguments of the first loads come in the first batch of argument
+  // loads (one wait), not on demand one batch later
+  asm volatile("" ::"s"(tile_start), "s"(bitmask), "s"(y), "s"(W), "s"(mrd), "s"(L), "s"(out_elems));
   if (tile_wave_id(waves) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start, nT, waves);
   const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
@@ -161,6 +164,9 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
                                                               float* __restrict__ head, float* __restrict__ tail,
                                                               int32_t* __restrict__ tend) {
   __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
+  // the arguments of the first loads come in the first batch of argument
+  // loads (one wait), not on demand one batch later
+  asm volatile("" ::"s"(tile_start), "s"(bitmask), "s"(dout), "s"(W), "s"(mrd), "s"(L), "s"(n_rows));
   if (tile_wave_id(waves) >= waves) return;
   const TileWave w = tile_wave(nT, nG, dim, tile_start, nT, waves);
   const int wave = threadIdx.x / kWave, lane = lane_id();

@@ -119,16 +119,6 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
-// True if some decay exponent of model channel d can be positive (A > 0 or
-// Δ < 0): lane products of decays are then multiplied out instead of taken
-// as exp2 of a Δ sum.
-__device__ __forceinline__ bool sl_exact(const bcm_scan_args& a, int d) {
-  bool ex = a.dt_idle[d] < 0.0f || a.dt_active[d] < 0.0f;
-#pragma unroll
-  for (int m = 0; m < kSLN; ++m) ex |= a.A[(int64_t)d * kSLN + m] > 0.0f;
-  return ex;
-}
-
 // The decay table holds two copies interleaved, T[k][m][parity]: lane
 // (row g, state m) reads word 32k + 2m + (g & 1), so the two rows (channels)
 // of a half-wave read disjoint banks whatever their gaps k (one bank per
@@ -154,11 +144,14 @@ __device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, f
 }
 
 // ------------------------------------------------------------------ forward
-template <typename T, bool HAS_Z, bool EXACT>
+template <typename T, bool HAS_Z>
 __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int nw, int S) {
 #pragma clang fp contract(off)  // fmas are written out where they are meant
   constexpr uint32_t SZ = sizeof(T);
   constexpr int N = kSLN;
+  // the kernel arguments that the first loads need arrive with the first
+  // batch of argument loads (one wait), not on demand one batch later
+  asm volatile("" ::"s"(a.u), "s"(a.k), "s"(a.cu_seqlens), "s"(a.n_events), "s"(nw), "s"(S), "s"(a.D));
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim;
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -168,7 +161,32 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
   const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
 
-  const float al = sl_table_al(a, d);  // first load of the kernel: the table build waits for it alone
+  const int64_t E = a.n_events;
+  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.out, E * SZ);
+  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), roz = buf_rsrc(a.out_z, HAS_Z ? E * SZ : 0);
+
+  // The slot's first channel leads the kernel's loads: the first events'
+  // loads wait for its bounds alone, and their latency overlaps the rest of
+  // the set-up (parameters, decay table).
+  const int slot = wave * kSLRows + grp;
+  auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
+    const int v = r0 + slot * S + sp;
+    return v < n_per_d ? v : n_per_d;
+  };
+  auto channel = [&](int r0, int& e0, int& n) {  // unconditional loads (a clamped row), then selected
+    const int b = chan_at(r0);
+    const int64_t ch = (int64_t)d + (int64_t)b * dim;
+    const int64_t cc = ch < NC ? ch : NC - 1;
+    const int c0 = a.cu_seqlens[cc], c1 = a.cu_seqlens[cc + 1];
+    e0 = b < n_per_d ? c0 : 0;
+    n = b < n_per_d ? c1 - c0 : 0;
+    report_seqlen(a, n);
+  };
+  int e0, n;
+  channel(0, e0, n);
+
+  const float al = sl_table_al(a, d);  // the table build waits for this load alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
   const float Al = a.A[(int64_t)d * N + s] * kLog2e;
@@ -180,14 +198,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
         __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
   const uint32_t rowb = sl_tab_lane(s, grp);
 
-  const int64_t E = a.n_events;
-  const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
-  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.out, E * SZ);
-  const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), roz = buf_rsrc(a.out_z, HAS_Z ? E * SZ : 0);
-
-  // Channel b of round r0, and the loads of its first block round. The
-  // first channel's loads are issued before the decay table is built, so
-  // their latency overlaps the set-up.
+  // the loads of a channel's block round r
   auto off = [&](int e0, int bk) { return (uint32_t)(e0 + bk * kSLB + s); };
   float Un[kSLPF], Zn[kSLPF];
   int Kn[kSLPF];
@@ -199,108 +210,103 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
       Zn[t] = HAS_Z ? buf_load<T>(rz, off(e0, r * kSLPF + t) * SZ) : 0.0f;
     }
   };
-  const int slot = wave * kSLRows + grp;
-  auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
-    const int v = r0 + slot * S + sp;
-    return v < n_per_d ? v : n_per_d;
-  };
-  auto channel = [&](int r0, int& e0, int& n) {
-    const int b = chan_at(r0);
-    const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    e0 = b < n_per_d ? a.cu_seqlens[ch] : 0;
-    n = b < n_per_d ? a.cu_seqlens[ch + 1] - e0 : 0;
-    report_seqlen(a, n);
-  };
-  int e0, n;
-  channel(0, e0, n);
   issue(e0, 0);
+  // a decay exponent that can be positive (A > 0 or Δ < 0): lane products
+  // of decays are multiplied out instead of taken as exp2 of a Δ sum (the
+  // rows' 16 lanes hold all of A[d]; uniform over the workgroup)
+  const bool exact = __any(al > 0.0f) || dti < 0.0f || dta < 0.0f;
   sl_build_table(sT, al, dti, dta, nw);
   __syncthreads();
 
-  for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
-    const int b = chan_at(r0);
-    const bool act = b < n_per_d;
-    const int64_t ch = (int64_t)d + (int64_t)b * dim;
-    if (r0 > 0) {
-      channel(r0, e0, n);
-      issue(e0, 0);
-    }
-    const int nblk = (n + kSLB - 1) / kSLB;
-    const int wblk = wave_max_dpp(nblk);
-    // The lane's event of block bk is e0 + 16·bk + s (out of range past the
-    // channel's end: the loads read the next channel's values or 0, unused).
-    // Blocks go in rounds of kSLPF: a round's loads are issued when the round
-    // before it starts, so each has a round of compute to arrive in.
-    float g = 0.0f, P = 1.0f, sdl = 0.0f;
-    auto block = [&](const int bk, const float uv, const int kk, const float zv) {
-      const int i = bk * kSLB + s;
-      const bool valid = i < n;
-      // padding events are identities: Δ = 0 -> a = 1 (table entry 0), Δu² = 0
-      const float dl = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
-      const float du2 = dl * uv * uv;
-      const int big = valid && kk > kSLTab;
-      sdl += dl;
-      float av[kSLB];
-      tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u);
-      if (__builtin_expect(__any(big), 0)) {  // gaps past the table: computed decays
-        for16([&](auto q) {
-          constexpr int Q = decltype(q)::value;
-          const float dq = bcast_f<Q>(dl);  // row-uniform condition: lane Q of the row is active
-          if (bcast_i<Q>(big)) av[Q] = decay(dq * Al);
-        });
+  auto run = [&](auto exact_tag) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+    for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
+      const int b = chan_at(r0);
+      const bool act = b < n_per_d;
+      const int64_t ch = (int64_t)d + (int64_t)b * dim;
+      if (r0 > 0) {
+        channel(r0, e0, n);
+        issue(e0, 0);
       }
-      for16([&](auto q) {
-        g = fmaf(av[q], g, bcast_f<decltype(q)::value>(du2));
-        if (EXACT) P *= av[q];
-        xt[q * (kSLN + 1) + s] = g;
-      });
-      wave_sync();
-      float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
+      const int nblk = (n + kSLB - 1) / kSLB;
+      const int wblk = wave_max_dpp(nblk);
+      // The lane's event of block bk is e0 + 16·bk + s (out of range past the
+      // channel's end: the loads read the next channel's values or 0, unused).
+      // Blocks go in rounds of kSLPF: a round's loads are issued when the round
+      // before it starts, so each has a round of compute to arrive in.
+      float g = 0.0f, P = 1.0f, sdl = 0.0f;
+      auto block = [&](const int bk, const float uv, const int kk, const float zv) {
+        const int i = bk * kSLB + s;
+        const bool valid = i < n;
+        // padding events are identities: Δ = 0 -> a = 1 (table entry 0), Δu² = 0
+        const float dl = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
+        const float du2 = dl * uv * uv;
+        const int big = valid && kk > kSLTab;
+        sdl += dl;
+        float av[kSLB];
+        tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u);
+        if (__builtin_expect(__any(big), 0)) {  // gaps past the table: computed decays
+          for16([&](auto q) {
+            constexpr int Q = decltype(q)::value;
+            const float dq = bcast_f<Q>(dl);  // row-uniform condition: lane Q of the row is active
+            if (bcast_i<Q>(big)) av[Q] = decay(dq * Al);
+          });
+        }
+        for16([&](auto q) {
+          g = fmaf(av[q], g, bcast_f<decltype(q)::value>(du2));
+          if (EXACT) P *= av[q];
+          xt[q * (kSLN + 1) + s] = g;
+        });
+        wave_sync();
+        float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
 #pragma unroll
-      for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
-      wave_sync();  // the tile is rewritten by the next block
-      const float y = fmaf(Dv, uv, uv * acc);
-      const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
-      buf_store<T>(ro, eo, y);
-      if (HAS_Z) buf_store<T>(roz, eo, y * (zv / (1.0f + __expf(-zv))));
-      // saved states at the block end: x after every 2048 events and after
-      // the channel's last one; chunk_g at every pass start
-      const int cend = min(n, (bk + 1) * kSLB);
-      const int xc = (cend - 1) / kXChunk;
-      const bool xsave = bk < nblk && (cend % kXChunk == 0 || cend == n) && xc < nck;
-      if (__any(xsave)) {
-        const float sd = row_sum(sdl);
-        if (xsave) {
-          const float Pn = EXACT ? P : decay(sd * Al);
-          reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, g * wb);
+        for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+        wave_sync();  // the tile is rewritten by the next block
+        const float y = fmaf(Dv, uv, uv * acc);
+        const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
+        buf_store<T>(ro, eo, y);
+        if (HAS_Z) buf_store<T>(roz, eo, y * (zv / (1.0f + __expf(-zv))));
+        // saved states at the block end: x after every 2048 events and after
+        // the channel's last one; chunk_g at every pass start
+        const int cend = min(n, (bk + 1) * kSLB);
+        const int xc = (cend - 1) / kXChunk;
+        const bool xsave = bk < nblk && (cend % kXChunk == 0 || cend == n) && xc < nck;
+        if (__any(xsave)) {
+          const float sd = row_sum(sdl);
+          if (xsave) {
+            const float Pn = EXACT ? P : decay(sd * Al);
+            reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, g * wb);
+          }
+        }
+        const int pend = (bk + 1) * kSLB;  // events before the next pass start, when it is one
+        if (a.chunk_g && pend % kSLPass == 0 && pend < n && pend / kSLPass < g_rows)
+          a.chunk_g[(ch * g_rows + pend / kSLPass) * N + s] = g * wb;
+      };
+      for (int r = 0; r * kSLPF < wblk; ++r) {
+        float U[kSLPF], Z[kSLPF];
+        int K[kSLPF];
+#pragma unroll
+        for (int t = 0; t < kSLPF; ++t) {
+          U[t] = Un[t];
+          K[t] = Kn[t];
+          Z[t] = Zn[t];
+        }
+        issue(e0, r + 1);
+#pragma unroll
+        for (int t = 0; t < kSLPF; ++t)
+          if (r * kSLPF + t < wblk) block(r * kSLPF + t, U[t], K[t], Z[t]);
+      }
+      // chunks past the channel's end keep the reference's zero state
+      if (act) {
+        for (int c = (n + kXChunk - 1) / kXChunk; c < nck; ++c) {
+          a.x[(ch * nck + c) * 2 * N + s] = 0.0f;
+          a.x[(ch * nck + c) * 2 * N + N + s] = 0.0f;
         }
       }
-      const int pend = (bk + 1) * kSLB;  // events before the next pass start, when it is one
-      if (a.chunk_g && pend % kSLPass == 0 && pend < n && pend / kSLPass < g_rows)
-        a.chunk_g[(ch * g_rows + pend / kSLPass) * N + s] = g * wb;
-    };
-    for (int r = 0; r * kSLPF < wblk; ++r) {
-      float U[kSLPF], Z[kSLPF];
-      int K[kSLPF];
-#pragma unroll
-      for (int t = 0; t < kSLPF; ++t) {
-        U[t] = Un[t];
-        K[t] = Kn[t];
-        Z[t] = Zn[t];
-      }
-      issue(e0, r + 1);
-#pragma unroll
-      for (int t = 0; t < kSLPF; ++t)
-        if (r * kSLPF + t < wblk) block(r * kSLPF + t, U[t], K[t], Z[t]);
     }
-    // chunks past the channel's end keep the reference's zero state
-    if (act) {
-      for (int c = (n + kXChunk - 1) / kXChunk; c < nck; ++c) {
-        a.x[(ch * nck + c) * 2 * N + s] = 0.0f;
-        a.x[(ch * nck + c) * 2 * N + N + s] = 0.0f;
-      }
-    }
-  }
+  };
+  if (exact) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // nw: waves per workgroup, S: workgroups per model channel (the launch's
@@ -312,8 +318,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_arg
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
   float* xt = &sX[wave][grp * kSLTileSz];
-  if (sl_exact(a, blockIdx.x % a.dim)) sl_fwd_body<T, HAS_Z, true>(a, sT, xt, nw, S);
-  else sl_fwd_body<T, HAS_Z, false>(a, sT, xt, nw, S);
+  sl_fwd_body<T, HAS_Z>(a, sT, xt, nw, S);
 }
 
 // ----------------------------------------------------------------- backward
