@@ -58,6 +58,9 @@ __global__ __launch_bounds__(256) void k_count(const T* __restrict__ x, int64_t 
   constexpr int LPW = 32 / PER;        // lanes per 32-bit word
   constexpr int WPG = GS / 32;         // words per group
   constexpr int BATCH = 8;
+  // the arguments of the first loads come in the first batch of argument
+  // loads (one wait), not on demand one batch later
+  asm volatile("" ::"s"(x), "s"(L), "s"(n_rows), "s"(thr), "s"(bitmask), "s"(W));
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * (kExBlock / kWave) + threadIdx.x / kWave;
   // the row's bits and event count (0 for a row past the end)
@@ -305,6 +308,9 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
                                               const int32_t* __restrict__ bpre, int32_t* __restrict__ meta,
                                               int32_t* __restrict__ cu_out, const ConvAt cv) {
   static_assert(KM == 0 || GATHER, "the conv form writes x_ev");
+  // the arguments of the first loads come in the first batch of argument
+  // loads (one wait), not on demand batch after batch
+  asm volatile("" ::"s"(bitmask), "s"(W), "s"(n_rows), "s"(L), "s"(counts), "s"(bsum));
   __shared__ int32_t s_t[4][kFillSeg];
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int64_t c = (int64_t)blockIdx.x * 4 + wave;
@@ -313,14 +319,19 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
   const bool live = c < n_rows;
   const int64_t nwords = (L + 31) / 32;
   const uint32_t* br = bitmask + (live ? c : 0) * W;
-  const uint32_t word_first = (live && lane < nwords) ? br[lane] : 0u;
+  // unconditional (a clamped index, the value selected where it is used), so
+  // that no wait for it comes before the offsets' loads are issued
+  const uint32_t word_raw = br[lane < nwords ? lane : 0];
+  const bool word_ok = live && lane < nwords;
   int32_t cu0, n;
   if constexpr (BLK) {
     __shared__ int s_part[4][2];
     const int64_t r0 = (int64_t)blockIdx.x * 4;
-    int cb[4];  // the block's row counts
+    int cb[4];  // the block's row counts (clamped loads issued together, then selected)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) cb[q] = r0 + q < n_rows ? counts[r0 + q] : 0;
+    for (int q = 0; q < 4; ++q) cb[q] = counts[r0 + q < n_rows ? r0 + q : n_rows - 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cb[q] = r0 + q < n_rows ? cb[q] : 0;
     const int64_t nblk = (n_rows + 3) / 4;
     const bool first = blockIdx.x == 0 && bpre == nullptr;
     int sm = 0, mx = 0;  // blocks before this one (all blocks for block 0's totals)
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(256) void k_fill(const uint32_t* __restrict__ bitma
   int off = 0;
   for (int64_t w0 = 0; w0 < nwords; w0 += kWave) {
     const int64_t w = w0 + lane;
-    const uint32_t word = w0 == 0 ? word_first : (w < nwords ? br[w] : 0u);
+    const uint32_t word = w0 == 0 ? (word_ok ? word_raw : 0u) : (w < nwords ? br[w] : 0u);
     const int pc = __popc(word);
     const int incl = wave_incl_sum(pc);
     const int excl = incl - pc;
