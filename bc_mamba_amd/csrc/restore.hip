@@ -248,16 +248,30 @@ __global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_r
                                                          const float* __restrict__ tail,
                                                          const int32_t* __restrict__ tend, float* __restrict__ dy,
                                                          int64_t n_events) {
+  // the arguments come in one batch of argument loads
+  asm volatile("" ::"s"(nT), "s"(n_rows), "s"(head), "s"(tail), "s"(tend), "s"(dy), "s"(n_events));
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
-  if (i >= nT * n_rows) return;
-  const int32_t e_end = tend[i];
+  const int64_t n = nT * n_rows;
+  if (i >= n) return;
+  // the tile's entries and the next tile's (where the run usually ends) in
+  // one round trip
+  const int64_t q1 = i + n_rows;
+  const int64_t q1c = q1 < n ? q1 : i;
+  const int32_t e_end = tend[i], e1 = tend[q1c];
+  const float tl = tail[i], h1 = head[q1c];
+  asm volatile("" ::"v"(tl), "v"(h1), "v"(e1));  // all four loads before the branch below: one wait
   // no event in the tile (its head belongs to an earlier tile's owner); an
   // index outside dy (a workspace the tile pass did not fill) is never stored
   if (e_end <= 0 || e_end > n_events) return;
-  float acc = tail[i];
-  for (int64_t q = i + n_rows; q < nT * n_rows; q += n_rows) {
-    acc += head[q];
-    if (tend[q] >= 0) break;
+  float acc = tl;
+  if (q1 < n) {
+    acc += h1;
+    if (e1 < 0) {
+      for (int64_t q = q1 + n_rows; q < n; q += n_rows) {
+        acc += head[q];
+        if (tend[q] >= 0) break;
+      }
+    }
   }
   dy[e_end - 1] = acc;
 }
