@@ -343,6 +343,9 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   constexpr uint32_t SZ = sizeof(T);
   constexpr int N = kSLN;
   constexpr int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
+  // the arguments of the channel bounds' loads come in the first batch of
+  // argument loads (more operands here cost scalar-register spills)
+  asm volatile("" ::"s"(a.cu_seqlens), "s"(nw), "s"(S));
   constexpr int NB = kSLPass / kSLB;  // blocks per pass
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim;
@@ -402,11 +405,13 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
     const int v = r0 + slot * S + sp;
     return v < n_per_d ? v : n_per_d;
   };
-  auto channel = [&](int r0, int& e0, int& n, int64_t& ch) {
+  auto channel = [&](int r0, int& e0, int& n, int64_t& ch) {  // unconditional loads (a clamped row), then selected
     const int b = chan_at(r0);
     ch = (int64_t)d + (int64_t)b * dim;
-    e0 = b < n_per_d ? a.cu_seqlens[ch] : 0;
-    n = b < n_per_d ? a.cu_seqlens[ch + 1] - e0 : 0;
+    const int64_t cc = ch < NC ? ch : NC - 1;
+    const int c0 = a.cu_seqlens[cc], c1 = a.cu_seqlens[cc + 1];
+    e0 = b < n_per_d ? c0 : 0;
+    n = b < n_per_d ? c1 - c0 : 0;
     report_seqlen(a, n);
   };
   int e0, n;
