@@ -95,7 +95,7 @@ template <int G, int R> struct TilePos {
 
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL>
-__global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a, int sort_ch) {
+__global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bcm_scan_args a, int sort_ch, int nw, int S) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int C = G * R;
@@ -105,12 +105,15 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
   const int N = a.dstate;
   // longest gap in the decay table (without a table tb only marks valid items)
   const int tabk = TBL ? tab_gaps(N) : kTabK;
-  // S workgroups per model channel d (S = gridDim.x / dim). A round covers
-  // nslots·S channels: the slot at position pos of workgroup sp takes rank
-  // r0 + pos·S + sp of round r0 (chan_at below)
+  // S workgroups per model channel d (the grid is dim·S workgroups of nw
+  // waves; both are arguments, not read from gridDim / blockDim, whose loads
+  // would come first). A round covers nslots·S channels: the slot at
+  // position pos of workgroup sp takes rank r0 + pos·S + sp of round r0
+  // (chan_at below)
+  asm volatile("" ::"s"(a.cu_seqlens), "s"(nw), "s"(S));  // in the first batch of argument loads
   const int d = blockIdx.x % a.dim;
-  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
-  const int nw = blockDim.x / kWave;
+  const int sp = blockIdx.x / a.dim;
+  const int nthr = nw * kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / G, j = lane % G;
   const int nslots = nw * CPW;
@@ -187,7 +190,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
     return v < n_per_d ? (sort_ch ? sOrd[v] : v) : n_per_d;
   };
   static_assert(2 * kWave * (R + 1) >= kSortMax, "the staging tiles hold the ranking keys");
-  if (sort_ch) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(sWBC + N), sOrd);  // keys in the tiles
+  if (sort_ch) rank_channels(a, d, n_per_d, reinterpret_cast<int*>(sWBC + N), sOrd, nthr);  // keys in the tiles
   int e0, n;
   const int b_step = nslots * S;
   channel(chan_at(0, pos), e0, n);
@@ -195,13 +198,13 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  for (int s = threadIdx.x; s < N; s += blockDim.x) {
+  for (int s = threadIdx.x; s < N; s += nthr) {
     const float wb = a.W_B[(int64_t)d * N + s];
     sAl[s] = a.A[(int64_t)d * N + s] * kLog2e;
     sWB[s] = wb;
     sWBC[s] = wb * a.W_C[(int64_t)d * N + s];
   }
-  if (TBL) build_decay_table(sT, a, d, dti, dta);
+  if (TBL) build_decay_table(sT, a, d, dti, dta, nthr);
   if (sp < n_per_d) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
@@ -357,7 +360,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
 }
 
 template <int G, int R, typename T, bool HAS_Z, bool TBL, bool DXR>
-__global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw) {
+__global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm_scan_args a, const ScanRows rw, int nw, int S) {
   using Ops = Grp<G>;
   constexpr int CPW = kWave / G;
   constexpr int RS = R + 1;
@@ -368,12 +371,15 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
   const int N = a.dstate;
   // longest gap in the decay table (without a table tb only marks valid items)
   const int tabk = TBL ? tab_gaps(N) : kTabK;
-  // S workgroups per model channel d (S = gridDim.x / dim). A round covers
-  // nslots·S channels: the slot at position pos of workgroup sp takes rank
-  // r0 + pos·S + sp of round r0 (chan_at below)
+  // S workgroups per model channel d (the grid is dim·S workgroups of nw
+  // waves; both are arguments, not read from gridDim / blockDim, whose loads
+  // would come first). A round covers nslots·S channels: the slot at
+  // position pos of workgroup sp takes rank r0 + pos·S + sp of round r0
+  // (chan_at below)
+  asm volatile("" ::"s"(a.cu_seqlens), "s"(nw), "s"(S));  // in the first batch of argument loads
   const int d = blockIdx.x % a.dim;
-  const int sp = blockIdx.x / a.dim, S = gridDim.x / a.dim;
-  const int nw = blockDim.x / kWave;
+  const int sp = blockIdx.x / a.dim;
+  const int nthr = nw * kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int grp = lane / G, j = lane % G;
   const int nslots = nw * CPW;
@@ -467,7 +473,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
 
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  for (int s = threadIdx.x; s < N; s += blockDim.x) {
+  for (int s = threadIdx.x; s < N; s += nthr) {
     const float Av = a.A[(int64_t)d * N + s];
     const float wb = a.W_B[(int64_t)d * N + s], wc = a.W_C[(int64_t)d * N + s];
     sA[s] = Av;
@@ -477,8 +483,8 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
     sWBC[s] = wb * wc;
     sWBCA[s] = wb * wc * Av;
   }
-  for (int i = threadIdx.x; i < nslots * NA; i += blockDim.x) sacc[i] = 0.0f;
-  if (TBL) build_decay_table(sT, a, d, dti, dta);
+  for (int i = threadIdx.x; i < nslots * NA; i += nthr) sacc[i] = 0.0f;
+  if (TBL) build_decay_table(sT, a, d, dti, dta, nthr);
   if (sp < n_per_d && wmax > 0) to_tiles();
   const bool exact_blk = exact_products(sAl, N, dti, dta);  // also the barrier after the LDS set-up
 
@@ -893,7 +899,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < NA; i += blockDim.x) {
+  for (int i = threadIdx.x; i < NA; i += nthr) {
     float v = 0.0f;
     for (int sl = 0; sl < nslots; ++sl) v += sacc[sl * NA + i];
     if (S > 1) a.split_ws[((int64_t)sp * a.dim + d) * NA + i] = v;  // summed by k_scan_param_reduce
@@ -973,13 +979,13 @@ static int launch(const bcm_scan_args& a, hipStream_t s, const char* fn, Plan* q
   const int sort_ch = !BWD && per_d > 1 && per_d <= kSortMax && a.max_seqlen > G * R;
   if (BWD) {
     hipLaunchKernelGGL((k_scan_bwd<G, R, T, Z, TBL, DXR>), grid, dim3(nw * kWave), (size_t)lds, s, a,
-                       rw ? *rw : ScanRows{});
+                       rw ? *rw : ScanRows{}, nw, S);
     int rc = check_launch(fn);
     if (rc || S == 1) return rc;
     const int64_t tot = (int64_t)a.dim * (3 * a.dstate + 3);
     hipLaunchKernelGGL(k_scan_param_reduce, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, a, S);
   } else {
-    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a, sort_ch);
+    hipLaunchKernelGGL((k_scan_fwd<G, R, T, Z, TBL>), grid, dim3(nw * kWave), (size_t)lds, s, a, sort_ch, nw, S);
   }
   return check_launch(fn);
 }

@@ -31,11 +31,12 @@ __device__ __forceinline__ float tab(const float* sT, uint32_t row, uint32_t tb)
 
 // Decay table of workgroup d: T[s][0] = 1 (padding), T[s][k] = the decay of
 // gap k (same expression and rounding as the per-event path), rows of
-// tab_gaps(N) + 1 entries.
-__device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta) {
+// tab_gaps(N) + 1 entries. nthr: the workgroup's threads.
+__device__ __forceinline__ void build_decay_table(float* sT, const bcm_scan_args& a, int d, float dti, float dta,
+                                                  int nthr) {
   const int N = a.dstate;
   const int tstr = tab_gaps(N) + 1;
-  for (int i = threadIdx.x; i < N * tstr; i += blockDim.x) {
+  for (int i = threadIdx.x; i < N * tstr; i += nthr) {
     const int s = i / tstr, q = i - s * tstr;
     sT[i] = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * (a.A[(int64_t)d * N + s] * kLog2e));
   }
@@ -55,14 +56,16 @@ __device__ __forceinline__ bool exact_products(const float* sAl, int N, float dt
 // Length order of model channel d's channels (ch = d + b·dim, b < n_per_d),
 // used when channels span several passes: ord[rank] = b, longest first,
 // ties by b. keys is LDS scratch of n_per_d ints, dead after the return.
+// nthr: the workgroup's threads.
 constexpr int kSortMax = 256;  // most channels per model channel that are ranked
-__device__ __forceinline__ void rank_channels(const bcm_scan_args& a, int d, int n_per_d, int* keys, int* ord) {
-  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
+__device__ __forceinline__ void rank_channels(const bcm_scan_args& a, int d, int n_per_d, int* keys, int* ord,
+                                              int nthr) {
+  for (int i = threadIdx.x; i < n_per_d; i += nthr) {
     const int64_t ch = (int64_t)d + (int64_t)i * a.dim;
     keys[i] = a.cu_seqlens[ch + 1] - a.cu_seqlens[ch];
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < n_per_d; i += blockDim.x) {
+  for (int i = threadIdx.x; i < n_per_d; i += nthr) {
     const int ki = keys[i];
     int r = 0;
     for (int q = 0; q < n_per_d; ++q) {
