@@ -177,11 +177,13 @@ __global__ __launch_bounds__(256, 4) void k_restore_bwd_tiles(const TI* __restri
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + gbase, (n_rows * L - gbase) * (int64_t)sizeof(TI));
   const uint32_t lane_off = w.ok ? (uint32_t)lane * (uint32_t)sizeof(TI) : kBufOOB;
   const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TI);
+  // the tile's first event index and mask before its rows, so that the
+  // sweep below starts when the first rows are in (in-order load counts)
+  const int32_t elo = tile_start[(int64_t)w.ch * (nT + 1) + w.j];
+  const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   float gv[kTile];
 #pragma unroll
   for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI, kStream>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
-  const int32_t elo = tile_start[(int64_t)w.ch * (nT + 1) + w.j];
-  const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
   const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
   const int nev = __popcll(m);
