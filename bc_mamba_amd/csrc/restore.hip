@@ -112,8 +112,14 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
   const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
   const int e_base = __builtin_amdgcn_readfirstlane(w.e_base);
   const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y + e_base, (n_events - e_base) * (int64_t)sizeof(TI));
-  // event values of the tile: one load per step, out-of-range offsets for
-  // steps without an event (no branches, all loads independent)
+  // the value held before the tile (its previous event's), then the tile's
+  // event values, one load per step with out-of-range offsets for steps
+  // without an event (no branches, all loads independent), in the order the
+  // stores below use them, so that the first stores wait for the first
+  // loads only (the empty asm on val, after the loads are issued, keeps the
+  // compiler from folding the first select into a predicated reload of
+  // val's register issued last; it waits for val's load alone)
+  float val = buf_load<TI>(ry, elo > cu0 ? (uint32_t)(elo - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
   float v[kTile];
   uint32_t idx = (uint32_t)(elo - e_base);
 #pragma unroll
@@ -122,7 +128,7 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
     v[s] = buf_load<TI>(ry, bit ? idx * (uint32_t)sizeof(TI) : kBufOOB);
     idx += bit;
   }
-  float val = buf_load<TI>(ry, elo > cu0 ? (uint32_t)(elo - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
+  asm volatile("" : "+v"(val));
   // One straight-line pass for every tile (v[] stays in registers): lanes
   // past dim and steps past L get an out-of-range offset, so their stores
   // are dropped by the buffer unit instead of branched around.
