@@ -140,6 +140,22 @@ def test_scan_clamped_decays(cuda_device):
     _run_and_check(c, torch.float32, cuda_device)
 
 
+@pytest.mark.parametrize("kind", ["A_positive", "dt_negative"])
+def test_scan_exact_products(cuda_device, kind):
+    """Decay exponents that can be positive (A > 0 for some states, or a
+    negative Δ): the saved x then carries the multiplied-out decay products
+    instead of exp2 of a Δ sum (the kernels' exact path)."""
+    c = _case(2, 4, 300, 0.3, 16, torch.float32, seed=31)
+    g = torch.Generator().manual_seed(32)
+    if kind == "A_positive":  # small growth rates on a third of the states
+        grow = torch.rand(c["A"].shape, generator=g) < 0.33
+        c["A"] = torch.where(grow, 0.05 * torch.rand(c["A"].shape, generator=g), c["A"])
+    else:  # Δ = dt_idle·(k-1) + dt_active below 0 for long gaps on two channels
+        c["dt_i"] = c["dt_i"].clone()
+        c["dt_i"][:2] = -0.01
+    _run_and_check(c, torch.float32, cuda_device)
+
+
 def test_autograd_function_matches_raw(cuda_device):
     c = _case(2, 8, 800, 0.2, 16, torch.float32, seed=10, with_z=True)
     dev = cuda_device
