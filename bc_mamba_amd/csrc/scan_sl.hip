@@ -619,18 +619,19 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_arg
 
 // ------------------------------------------------------------------- host
 // Which family runs a dstate-16 scan. The state lanes give one wave per four
-// channels, so they pay when the channels fill two waves per SIMD (below
-// that, each wave's dependent chain is exposed and the lane groups of
-// scan.hip, which split a channel over 16 lanes, are faster: config 2 has
-// 4096 channels and runs 2.7 µs per step slower on the state lanes).
-// BCM_SCAN_KERNEL=lanes / items overrides the choice (read on every call:
-// the tests run both families on the same shapes).
+// channels, so they pay when the channels fill every SIMD with at least one
+// wave (config 2, 4096 channels on 256 CUs: 125-127 against 130-131 µs per
+// step; the forward is 2-3 µs slower there, the backward 5-7 µs faster);
+// below that the lane groups of scan.hip, which split a channel over 16
+// lanes, keep more of the chip busy. BCM_SCAN_KERNEL=lanes / items
+// overrides the choice (read on every call: the tests run both families on
+// the same shapes).
 bool sl_applies(const bcm_scan_args& a) {
   if (a.dstate != kSLN) return false;
   const char* v = std::getenv("BCM_SCAN_KERNEL");
   if (v && v[0] == 'l') return true;
   if (v && v[0] == 'i') return false;
-  return (int64_t)a.n_channels >= 2ll * kSLRows * 4 * device_cus();
+  return (int64_t)a.n_channels >= (int64_t)kSLRows * 4 * device_cus();
 }
 
 int sl_split(const bcm_scan_args& a) {

@@ -199,7 +199,7 @@ def test_conv_events_backward_rejects_overlapping_rows(lib):
 
 def test_scan_family_choice_and_passes(monkeypatch):
     """The dstate-16 scan family: the state lanes (32-event passes kept in
-    chunk_g) from 8192 channels on a 256-CU part (two waves of four channels
+    chunk_g) from 4096 channels on a 256-CU part (a wave of four channels
     per SIMD), the lane groups below that, other dstates always the lane
     groups; BCM_SCAN_KERNEL overrides the choice on every call. Without a
     device the library assumes 256 CUs."""
@@ -209,10 +209,11 @@ def test_scan_family_choice_and_passes(monkeypatch):
         return nat.scan_chunking(a)
     monkeypatch.delenv("BCM_SCAN_KERNEL", raising=False)
     assert chunking(8192, 16, 367) == (32, 12, 1)      # config 1: lanes, chunk_g rows every 32 events
-    assert chunking(4096, 16, 482)[0] > 32             # config 2: lane groups
+    assert chunking(4096, 16, 482) == (32, 16, 1)      # config 2: lanes
+    assert chunking(2048, 16, 482)[0] > 32             # half the SIMDs: lane groups
     assert chunking(8192, 64, 367)[0] > 32             # dstate 64: lane groups
     assert chunking(8192, 16, 20) == (32, 1, 0)        # one pass: no chunk_g
     monkeypatch.setenv("BCM_SCAN_KERNEL", "lanes")
-    assert chunking(4096, 16, 482) == (32, 16, 1)
+    assert chunking(2048, 16, 482) == (32, 16, 1)
     monkeypatch.setenv("BCM_SCAN_KERNEL", "items")
     assert chunking(8192, 16, 367)[0] > 32
