@@ -15,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("BCM_LIB_PATH", os.path.join(_HERE, "lib", "libbcm_event_scan.so"))
 
 F32, F16, BF16, U8 = 0, 1, 2, 3
-ABI_VERSION = 3  # BCM_ABI_VERSION of include/bcm_event_scan.h
+ABI_VERSION = 4  # BCM_ABI_VERSION of include/bcm_event_scan.h
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.bool: U8, torch.uint8: U8}
 
 c_i32, c_i64, c_f32, c_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -33,7 +33,7 @@ class ScanArgs(ctypes.Structure):
         ("dout", c_p), ("x_saved", c_p), ("out_saved", c_p),
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
         ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("chunk_g_bytes", c_i64),
-        ("split_ws", c_p), ("split_ws_bytes", c_i64), ("status", c_p),
+        ("split_ws", c_p), ("split_ws_bytes", c_i64), ("status", c_p), ("chunk_g_pass", c_i32),
     ]
 
 
@@ -82,6 +82,7 @@ SIGNATURES = {
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd_rows": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanRows), c_p]),
     "bcm_scan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(ScanArgs)]),
+    "bcm_set_scan_family": (c_i32, [c_i32]),
     "bcm_scan_chunking": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(c_i32), ctypes.POINTER(c_i32),
                                   ctypes.POINTER(c_i32)]),
     "bcm_scan_var_fwd": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBC), c_p]),
@@ -170,6 +171,31 @@ def scan_chunking(a):
     p, q, r = c_i32(), c_i32(), c_i32()
     call("bcm_scan_chunking", a, ctypes.byref(p), ctypes.byref(q), ctypes.byref(r))
     return p.value, q.value, bool(r.value)
+
+
+SCAN_FAMILIES = {"auto": 0, "lanes": 1, "items": 2}  # enum bcm_scan_family of the header
+
+
+def set_scan_family(name):
+    """Process-wide depthwise scan family (bcm_set_scan_family): "auto",
+    "lanes" (state lanes) or "items" (lane groups). Returns the previous
+    setting's name. A forward and the backward that reads its chunk_g must
+    run under the same setting."""
+    prev = lib().bcm_set_scan_family(SCAN_FAMILIES[name])
+    if prev < 0:
+        raise RuntimeError(lib().bcm_last_error().decode())
+    return {v: k for k, v in SCAN_FAMILIES.items()}[prev]
+
+
+def attach_chunk_g(a, chunk_g):
+    """Point ScanArgs `a` at a chunk_g buffer from the pass-state allocator
+    (selective_scan_cuda.chunk_states_buffer or an equivalent that records
+    the pass length it was sized for as `bcm_pass_len`)."""
+    if chunk_g is None:
+        a.chunk_g, a.chunk_g_bytes, a.chunk_g_pass = None, 0, 0
+        return
+    a.chunk_g, a.chunk_g_bytes = chunk_g.data_ptr(), chunk_g.numel() * 4
+    a.chunk_g_pass = int(getattr(chunk_g, "bcm_pass_len", 0))
 
 
 class HostMeta:

@@ -652,13 +652,15 @@ int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitma
   if (!out || (n_events > 0 && !y)) return set_error(BCM_EINVAL, "%s: null pointer", fn);
   const ProjShape s = proj_shape(n_rows, dim, L, d_model);
   // the LDS-DMA form wants whole 32-channel chunks, whole 64-column blocks
-  // and 16-byte aligned W rows
-  const bool dma = dim % kKC == 0 && d_model % kPT == 0 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0;
+  // and 16-byte aligned W rows; its per-channel index words take 32 bytes
+  // of LDS per channel, so wide layers (dim above ~3.5k on a 160 KB part)
+  // take the register-staged form, which needs 16
+  const size_t lds_dma = (size_t)(2 * kDyT * kKC + 2 * kPT * kKC) * 4 + (size_t)dim * 32;
+  const bool dma = dim % kKC == 0 && d_model % kPT == 0 && (reinterpret_cast<uintptr_t>(weight) & 15) == 0 &&
+                   (int64_t)lds_dma <= max_lds_bytes();
   if (dma) {
     const int64_t items = (n_rows / dim) * ((s.nT + 1) / 2) * s.nNB;
-    const size_t lds = (size_t)(2 * kDyT * kKC + 2 * kPT * kKC) * 4 + (size_t)dim * 32;
-    if ((int64_t)lds > max_lds_bytes())
-      return set_error(BCM_EINVAL, "%s: dim %lld needs %lld bytes of LDS", fn, (long long)dim, (long long)lds);
+    const size_t lds = lds_dma;
     hipLaunchKernelGGL(k_restore_proj_fwd_dma, dim3((unsigned)items), dim3(256), lds, hs(stream), y, n_events, bitmask,
                        s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, weight, bias, (int)d_model,
                        (int)s.nNB, out);
@@ -689,10 +691,11 @@ int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events, co
   if (rc) return rc;
   if (!dout && n_rows) return set_error(BCM_EINVAL, "%s: null dout", fn);
   if (dweight && n_events > 0 && !y) return set_error(BCM_EINVAL, "%s: dweight needs y", fn);
-  const int64_t need = bcm_restore_proj_bwd_workspace_bytes(n_rows, dim, L, d_model);
+  const ProjShape s = proj_shape(n_rows, dim, L, d_model);
+  // the fix-up arrays always, the weight gradient's partials only with dweight
+  const int64_t need = 3 * 4 * n_rows * s.nT + (dweight ? 4 * s.n_parts * d_model * dim : 0);
   if (!workspace || workspace_bytes < need)
     return set_error(BCM_EINVAL, "%s: workspace of %lld bytes required", fn, (long long)need);
-  const ProjShape s = proj_shape(n_rows, dim, L, d_model);
   const hipStream_t st = hs(stream);
   const int64_t B = n_rows / dim;
   if (B * s.nT * s.nDB > INT32_MAX / 2 || s.n_parts * s.nNB * s.nDB > INT32_MAX / 2)

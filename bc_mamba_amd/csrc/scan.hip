@@ -1102,6 +1102,11 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
   if (a.chunk_g) {
     int pass_len, n_pass, needs_g;
     chunking(a, &pass_len, &n_pass, &needs_g);
+    if (a.chunk_g_pass != pass_len)
+      return set_error(BCM_EINVAL,
+                       "%s: chunk_g is laid out for passes of %d events, this scan runs passes of %d (size it "
+                       "with bcm_scan_chunking under the scan family of both the forward and the backward)",
+                       fn, a.chunk_g_pass, pass_len);
     const int64_t need = 4ll * a.n_channels * n_pass * a.dstate;
     if (a.chunk_g_bytes < need)
       return set_error(BCM_EINVAL, "%s: chunk_g needs %lld bytes (n_channels x %d passes x dstate floats)", fn,

@@ -111,6 +111,8 @@ constexpr int kSLPass = 32;  // events per pass: chunk_g rows, the backward's un
 // True when the state-lane kernels run this scan (forward and backward
 // alike, so that chunk_g has the passes the backward expects).
 bool sl_applies(const bcm_scan_args& a);
+// The process-wide family setting (BCM_SCAN_AUTO / _LANES / _ITEMS).
+int scan_family();
 // Workgroups per model channel the state-lane kernels use for these arguments.
 int sl_split(const bcm_scan_args& a);
 int sl_launch_fwd(const bcm_scan_args& a, hipStream_t s, const char* fn);

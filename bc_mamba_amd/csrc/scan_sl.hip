@@ -34,6 +34,7 @@
 #include "scan_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdlib>
 
@@ -519,7 +520,10 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         dD_l += doutu[t];
         const bool valid = i < n;
         buf_store<T>(rdu, valid ? (uint32_t)(e0 + i) * SZ : kBufOOB, duv);
-        if (DXR && valid) sdu[i] = duv;  // the channel's du in event order, for its dense row
+        // the channel's du in event order, for its dense row (an understated
+        // max_seqlen, flagged in the status word, must not spill into the
+        // neighbouring slots' rows)
+        if (DXR && valid && i < kSLRowCap) sdu[i] = duv;
       }
     }
     // the channel's parameter-gradient terms into the slot's accumulators
@@ -618,19 +622,36 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_arg
 }
 
 // ------------------------------------------------------------------- host
+// The process-wide family setting of bcm_set_scan_family: -1 until the first
+// scan call, which takes it from BCM_SCAN_KERNEL ("lanes" / "items", else
+// automatic). One setting for the process, not one per call: the family
+// fixes chunk_g's pass length, which the forward and its backward share.
+static std::atomic<int> g_scan_family{-1};
+
+int scan_family() {
+  int f = g_scan_family.load(std::memory_order_acquire);
+  if (f < 0) {
+    const char* v = std::getenv("BCM_SCAN_KERNEL");
+    const int e = v && v[0] == 'l' ? BCM_SCAN_LANES : (v && v[0] == 'i' ? BCM_SCAN_ITEMS : BCM_SCAN_AUTO);
+    int unset = -1;
+    g_scan_family.compare_exchange_strong(unset, e, std::memory_order_acq_rel);
+    f = g_scan_family.load(std::memory_order_acquire);
+  }
+  return f;
+}
+
 // Which family runs a dstate-16 scan. The state lanes give one wave per four
 // channels, so they pay when the channels fill every SIMD with at least one
 // wave (config 2, 4096 channels on 256 CUs: 125-127 against 130-131 µs per
 // step; the forward is 2-3 µs slower there, the backward 5-7 µs faster);
 // below that the lane groups of scan.hip, which split a channel over 16
-// lanes, keep more of the chip busy. BCM_SCAN_KERNEL=lanes / items
-// overrides the choice (read on every call: the tests run both families on
-// the same shapes).
+// lanes, keep more of the chip busy. bcm_set_scan_family forces either
+// family (the tests run both on the same shapes).
 bool sl_applies(const bcm_scan_args& a) {
   if (a.dstate != kSLN) return false;
-  const char* v = std::getenv("BCM_SCAN_KERNEL");
-  if (v && v[0] == 'l') return true;
-  if (v && v[0] == 'i') return false;
+  const int f = scan_family();
+  if (f == BCM_SCAN_LANES) return true;
+  if (f == BCM_SCAN_ITEMS) return false;
   return (int64_t)a.n_channels >= (int64_t)kSLRows * 4 * device_cus();
 }
 
@@ -688,3 +709,13 @@ bool sl_rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
 }
 
 }  // namespace bcm
+
+extern "C" int bcm_set_scan_family(int family) {
+  if (family != BCM_SCAN_AUTO && family != BCM_SCAN_LANES && family != BCM_SCAN_ITEMS) {
+    bcm::set_error(BCM_EINVAL, "bcm_set_scan_family: unknown family %d", family);
+    return -1;
+  }
+  const int prev = bcm::scan_family();
+  bcm::g_scan_family.store(family, std::memory_order_release);
+  return prev;
+}

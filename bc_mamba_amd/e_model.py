@@ -455,12 +455,16 @@ class Mamba(nn.Module):
                 and self.d_conv <= 8 and x.dtype in (torch.float32, torch.float16, torch.bfloat16))
 
     def _restore_proj_ok(self, y_flat, seqlen):
-        """The restore -> out_proj op applies (fp32, 32-bit offsets)."""
+        """The restore -> out_proj op applies (fp32, 32-bit offsets; in the
+        all-kernel mode, d_inner within the forward kernel's LDS: 16 bytes of
+        index words per channel beside 36 KB of operand buffers on a 160 KB
+        part, so up to 7936 channels)."""
         w, b = self.out_proj.weight, self.out_proj.bias
         f32 = torch.float32
         return (self.fused_out_proj and y_flat.dtype == f32 and w.dtype == f32 and w.is_contiguous()
                 and (b is None or b.dtype == f32) and y_flat.numel() * 4 < 2 ** 31
-                and seqlen * self.d_model * 4 < 2 ** 31 and self.d_model * self.d_inner * 4 < 2 ** 31)
+                and seqlen * self.d_model * 4 < 2 ** 31 and self.d_model * self.d_inner * 4 < 2 ** 31
+                and (self.fused_out_proj != "mfma" or self.d_inner <= 7936))
 
     def forward(self, hidden_states, inference_params=None):
         if inference_params is not None:

@@ -136,11 +136,12 @@ class FusedStep:
             a.n_events, a.max_seqlen, a.n_chunks = E, ms, max(1, -(-ms // 2048))
             # pass-start states of channels longer than one pass (written by
             # the forward, read by the backward)
-            _, n_pass, needs = nat.scan_chunking(a)
+            pass_len, n_pass, needs = nat.scan_chunking(a)
             self.chunk_g = torch.empty((self.NC, n_pass, w.N), dtype=torch.float32, device=self.dev) \
                 if needs else None
-            a.chunk_g = self.chunk_g.data_ptr() if needs else None
-            a.chunk_g_bytes = self.chunk_g.numel() * 4 if needs else 0
+            if needs:
+                self.chunk_g.bcm_pass_len = pass_len
+            nat.attach_chunk_g(a, self.chunk_g)
             # parameter-gradient partials when model channels are split over workgroups
             nb = int(nat.lib().bcm_scan_bwd_workspace_bytes(a))
             self.split_ws = torch.empty(max(nb, 4) // 4, dtype=torch.float32, device=self.dev) if nb else None

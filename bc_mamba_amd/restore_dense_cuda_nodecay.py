@@ -92,8 +92,11 @@ def restore_proj_bwd_indexed(dout, y_flat, event_index, n_ch, dim, seqlen, weigh
     bitmask, tile_start, mrd = event_index
     dout = dout.contiguous()
     dm = weight.size(0)
-    ws = torch.empty(max(4, _nat.lib().bcm_restore_proj_bwd_workspace_bytes(n_ch, int(dim), int(seqlen), dm)) // 4,
-                     dtype=torch.float32, device=dout.device)
+    # the weight gradient's partials (d_model x dim per sequence segment) only
+    # when it is asked for; dy alone needs the fix-up arrays
+    nbytes = _nat.lib().bcm_restore_proj_bwd_workspace_bytes(n_ch, int(dim), int(seqlen), dm) if need_dw else \
+        _nat.lib().bcm_restore_bwd_workspace_bytes(n_ch, int(seqlen))
+    ws = torch.empty(max(4, nbytes) // 4, dtype=torch.float32, device=dout.device)
     dy = torch.empty(y_flat.numel(), dtype=torch.float32, device=dout.device) if need_dy else None
     dw = torch.empty_like(weight) if need_dw else None
     _nat.call("bcm_restore_proj_bwd", _nat.ptr(dout), _nat.ptr(y_flat), int(y_flat.numel()), _nat.ptr(bitmask),

@@ -164,10 +164,12 @@ def chunk_states_buffer(u_flat, cu_seqlens, max_seqlen, A):
     a.n_channels = int(cu_seqlens.size(0)) - 1
     a.dim, a.dstate = int(A.size(0)), int(A.size(1))
     a.max_seqlen = int(max_seqlen)
-    _, n_pass, needs = _nat.scan_chunking(a)
+    pass_len, n_pass, needs = _nat.scan_chunking(a)
     if not needs:
         return None
-    return torch.empty((a.n_channels, n_pass, a.dstate), dtype=torch.float32, device=u_flat.device)
+    buf = torch.empty((a.n_channels, n_pass, a.dstate), dtype=torch.float32, device=u_flat.device)
+    buf.bcm_pass_len = pass_len  # checked by the kernels against their own passes (chunk_g_pass)
+    return buf
 
 
 def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D, z):
@@ -224,8 +226,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.out, a.x = out.data_ptr(), x.data_ptr()
         a.out_z = out_z.data_ptr() if out_z is not None else None
         if mode == "depthwise":
-            if _chunk_g is not None:
-                a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
+            _nat.attach_chunk_g(a, _chunk_g)
             status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
             status.attach(a)
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
@@ -316,11 +317,10 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 scratch_out = torch.empty_like(u_flat)
                 f.out, f.x = scratch_out.data_ptr(), torch.empty_like(x).data_ptr()
                 f.out_z = torch.empty_like(u_flat).data_ptr() if has_z else None
-                f.chunk_g, f.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
+                _nat.attach_chunk_g(f, _chunk_g)
                 status.attach(f)
                 _nat.call("bcm_scan_fwd", f, s)
-            if _chunk_g is not None:
-                a.chunk_g, a.chunk_g_bytes = _chunk_g.data_ptr(), _chunk_g.numel() * 4
+            _nat.attach_chunk_g(a, _chunk_g)
             split_bytes = int(_nat.lib().bcm_scan_bwd_workspace_bytes(a))
             split_ws = torch.empty(split_bytes // 4, dtype=torch.float32, device=dev) if split_bytes else None
             a.split_ws = split_ws.data_ptr() if split_ws is not None else None

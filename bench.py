@@ -12,7 +12,13 @@ batch, inputs resident in HBM:
 All stages run in libbcm_event_scan.so on torch's current stream. Prints one
 JSON line (metric / value / roofline / cpu_baseline ...).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--cfg 1] [--no-cpu]
+Timing: `value` and `ms_per_step` come from the K timed steps, each run cold
+(L2 and the MALL flushed by reading 512 MiB first) with HIP events around
+the step, as their median; `warm_ms_per_step` is K back-to-back steps with
+inputs resident; `api_ms_per_step` times the drop-in Python API (autograd
+Functions over the same library) warm.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--cfg 1] [--no-cpu] [--no-api]
 """
 import argparse
 import json
@@ -29,8 +35,7 @@ METRIC = "fwd+bwd events/s & achieved HBM GB/s, B32 D256 L2048 N16 at 15% densit
 HBM_PEAK_GBS = 8000.0
 PROBE_STEPS = 5
 CAL_BYTES = 256 << 20  # device-to-device copy that calibrates the PMC byte counters
-FLUSH_BYTES = 512 << 20  # written before each cold step: more than L2 plus the 256 MB MALL
-COLD_REPS = 11
+FLUSH_BYTES = 512 << 20  # read before each timed step: more than the 8 L2s plus the 256 MB MALL
 
 # device kernels behind each stage of FusedStep.KERNELS (symbol substrings)
 STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
@@ -191,7 +196,7 @@ def main():
     ap.add_argument("--cfg", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-batches", type=int, default=4)
-    ap.add_argument("--api", action="store_true", help="also time the drop-in Python API path (autograd)")
+    ap.add_argument("--no-api", action="store_true", help="skip timing the drop-in Python API path (autograd)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure the dominant kernel's HBM bytes")
     ap.add_argument("--out-proj", choices=["gemm", "mfma", "off"], default="gemm",
@@ -234,21 +239,26 @@ def main():
     dominant = max(per_kernel, key=per_kernel.get)
     path.events.clear()
 
-    # timed region: no events inside (an event record makes the GPU write
-    # back its caches, several microseconds of idle device per record)
+    # timed region: `steps` cold steps (the measurement protocol's headline),
+    # each after a 512 MiB read has flushed L2 and the MALL, HIP events
+    # around the step alone; value is their median
+    cold = cold_steps_ms(path, dev, args.steps)
+    ms_per_step = cold["median"]
+    # warm figure beside it: back-to-back steps with inputs resident, no
+    # events inside (an event record makes the GPU write back its caches,
+    # several microseconds of idle device per record), host clock
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         path.step()
     torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    warm_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # the dominant kernel's launch duration: HIP events around it, on its
     # stream, over as many steps again right after the timed region
     for _ in range(args.steps):
         path.step(timed=(dominant,))
     torch.cuda.synchronize()
     dom_ms = path.kernel_ms(dominant)
-    cold_ms = cold_step_ms(path, dev, COLD_REPS)
 
     E, ms = path.E, path.ms
     su = torch.tensor([], dtype=w.dtype).element_size()
@@ -285,10 +295,15 @@ def main():
         "path_frac_own_bytes": own_total / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "path_frac_of_hbm_peak": total_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": per_kernel,
-        # one step after a 512 MiB write has flushed L2 and the 256 MB MALL
-        # (median of COLD_REPS, HIP events); ms_per_step is back-to-back steps
-        "cold_ms_per_step": cold_ms,
-        "cold_events_per_s": E / (cold_ms * 1e-3),
+        # ms_per_step / value: median over the timed steps, each after a
+        # 512 MiB read (L2 and the MALL flushed, no dirty lines left), HIP
+        # events around the step; warm: back-to-back steps, host clock
+        "timing": {"ms_per_step": "median of cold steps (L2 + MALL flushed by a 512 MiB read), HIP events",
+                   "reps": len(cold["all"]), "min_ms": min(cold["all"]), "max_ms": max(cold["all"]),
+                   "wall_s": cold["wall_s"]},
+        "warm_ms_per_step": warm_ms,
+        "warm_events_per_s": E / (warm_ms * 1e-3),
+        "warm_achieved_gbs": total_bytes / (warm_ms * 1e-3) / 1e9,
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": dom_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom_gbs / HBM_PEAK_GBS, "traffic": None, "launch_ms": dom_ms,
                      "bytes_per_launch": kernel_bytes[dominant]},
@@ -297,7 +312,9 @@ def main():
         traffic, detail = measure_traffic(args.cfg, dominant)
         result["roofline"]["traffic"] = traffic
         result["roofline"]["traffic_detail"] = detail
-    if args.api:
+    if not args.no_api:
+        # the drop-in Python API path (autograd Functions over the same
+        # library), warm: what a caller of the reference's interface sees
         result["api_ms_per_step"] = api_path_ms(w, dev, args.steps, args.warmup)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cfg, args.cpu_batches)
@@ -380,22 +397,30 @@ def peak_memory(model, step):
     return res
 
 
-def cold_step_ms(path, dev, reps):
-    """Median time of one step, each after writing a 512 MiB scratch buffer
-    (larger than L2 plus the 256 MB MALL), HIP events around the step only."""
+def cold_steps_ms(path, dev, reps):
+    """`reps` steps, each after reading a 512 MiB buffer (more than the
+    eight L2s and the 256 MB MALL together: the step's inputs are evicted,
+    and a read leaves no dirty lines whose write-back the step would pay
+    for), HIP events around the step only. Returns the median, every rep
+    and the wall time of the whole region (flushes included)."""
     import torch
-    scratch = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device=dev)
-    times = []
+    scratch = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    sink = torch.empty((), dtype=torch.float32, device=dev)
+    evs = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     for _ in range(reps):
-        scratch.fill_(1)
+        torch.sum(scratch, dim=0, out=sink)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         path.step()
         b.record()
-        torch.cuda.synchronize()
-        times.append(a.elapsed_time(b))
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    times = [a.elapsed_time(b) for a, b in evs]
     del scratch
-    return sorted(times)[len(times) // 2]
+    return {"median": sorted(times)[len(times) // 2], "all": times, "wall_s": wall}
 
 
 def api_path_ms(w, dev, steps, warmup):

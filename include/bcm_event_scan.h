@@ -12,7 +12,9 @@
  *   - every pointer is a device pointer unless stated otherwise; the caller
  *     allocates every input, output and workspace buffer; the library never
  *     allocates device memory and holds no state other than a thread-local
- *     error string, so calls on different streams may run concurrently;
+ *     error string, the process-wide scan-family setting
+ *     (bcm_set_scan_family) and the scratch of the allocation-free entry
+ *     point, so calls on different streams may run concurrently;
  *   - work is enqueued on `stream` (a hipStream_t; NULL = default stream) of
  *     the current device; no entry point synchronises the host;
  *   - the return value is BCM_OK or an error code; bcm_last_error() returns
@@ -39,7 +41,7 @@
 extern "C" {
 #endif
 
-#define BCM_ABI_VERSION 3
+#define BCM_ABI_VERSION 4
 
 typedef struct ihipStream_t* bcm_stream_t; /* == hipStream_t */
 
@@ -257,9 +259,30 @@ typedef struct bcm_scan_args {
    * later passes, and bcm_scan_bwd_rows' dense row) are incomplete. Every
    * write stays inside the buffers either way. */
   int32_t* status;
+  /* Events per pass that chunk_g is laid out for: the pass_len that
+   * bcm_scan_chunking returned when the caller sized chunk_g (the forward
+   * that fills it and the backward that reads it each check it against
+   * their own pass length: a mismatch, e.g. a forward and a backward run
+   * under different scan families, is BCM_EINVAL, as the reference refuses
+   * a stale chunk count, selective_scan.cpp:1009-1014). Ignored when chunk_g
+   * is NULL. */
+  int32_t chunk_g_pass;
 } bcm_scan_args;
 
 #define BCM_SCAN_SEQLEN_EXCEEDED 1
+
+/* Which kernel family runs a depthwise scan, for the whole process:
+ * BCM_SCAN_AUTO picks by shape (the state lanes of dstate 16 from one wave
+ * of four channels per SIMD up, the lane groups otherwise),
+ * BCM_SCAN_LANES / BCM_SCAN_ITEMS force the state lanes (dstate 16) / the
+ * lane groups. The initial value comes from the environment variable
+ * BCM_SCAN_KERNEL ("lanes", "items"; read once, at the first scan call),
+ * else BCM_SCAN_AUTO. The family fixes chunk_g's pass length, so a forward
+ * and its backward must run under the same setting (chunk_g_pass checks
+ * it). Returns the previous setting, or -1 for an unknown code. No
+ * counterpart in the reference (it has one kernel family). */
+enum bcm_scan_family { BCM_SCAN_AUTO = 0, BCM_SCAN_LANES = 1, BCM_SCAN_ITEMS = 2 };
+int bcm_set_scan_family(int family);
 
 /* Events per pass of a channel (pass_len) and passes of the longest channel
  * (n_pass) for these arguments (max_seqlen, n_events, n_channels, dstate):
@@ -444,7 +467,9 @@ int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitma
 
 /* Workspace of bcm_restore_proj_bwd: the restore backward's per-tile
  * arrays (3 * 4 * n_rows * tile_count(L)) and the weight gradient's
- * partials (4 * d_model * dim per (sequence, 1024-step segment)). */
+ * partials (4 * d_model * dim per (sequence, 1024-step segment)). A call
+ * with dweight == NULL needs only the per-tile arrays (the size of
+ * bcm_restore_bwd_workspace_bytes(n_rows, L)). */
 int64_t bcm_restore_proj_bwd_workspace_bytes(int64_t n_rows, int64_t dim, int64_t L,
                                              int64_t d_model);
 

@@ -42,9 +42,12 @@ def cuda_device():
 
 
 @pytest.fixture(params=["items", "lanes"])
-def scan_kernel(request, monkeypatch):
-    """Runs a test under each dstate-16 depthwise scan family: the lane
-    groups over items (scan.hip) and the lanes over states (scan_sl.hip),
-    forced with BCM_SCAN_KERNEL (the library reads it on every call)."""
-    monkeypatch.setenv("BCM_SCAN_KERNEL", request.param)
-    return request.param
+def scan_kernel(request):
+    """Runs a test under each depthwise scan family: the lane groups over
+    items (scan.hip) and the lanes over states (scan_sl.hip), forced with
+    the library's process-wide setting (bcm_set_scan_family) and restored
+    afterwards."""
+    import bc_mamba_amd._native as nat
+    prev = nat.set_scan_family(request.param)
+    yield request.param
+    nat.set_scan_family(prev)

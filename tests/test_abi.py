@@ -47,8 +47,9 @@ def test_library_exports_every_header_symbol(lib):
 
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
-    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 27 pointers + 2 int64 sizes
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 27 * 8 + 2 * 8
+    # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 27 pointers + 2 int64 sizes + int32 chunk_g_pass
+    # (padded to the struct's 8-byte alignment)
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 27 * 8 + 2 * 8 + 8
 
 
 def test_scan_bc_layout_matches_header():
@@ -115,7 +116,7 @@ def test_restore_proj_checks_before_launch(lib):
 
 
 def test_host_helpers(lib):
-    assert lib.bcm_abi_version() == nat.ABI_VERSION == 3
+    assert lib.bcm_abi_version() == nat.ABI_VERSION == 4
     assert lib.bcm_bitmask_words(2048) == nat.bitmask_words(2048) == 64
     assert lib.bcm_bitmask_words(1) == 32 and lib.bcm_bitmask_words(1025) == 64
     assert lib.bcm_tile_count(2048) == nat.tile_count(2048) == 32
@@ -164,8 +165,53 @@ def test_scan_chunk_states_size_is_checked(lib):
     a.out = a.x = 16
     pass_len, n_pass, needs = nat.scan_chunking(a)
     assert needs and n_pass > 1
-    a.chunk_g, a.chunk_g_bytes = 16, 4 * 8 * n_pass * 16 - 4
+    a.chunk_g, a.chunk_g_bytes, a.chunk_g_pass = 16, 4 * 8 * n_pass * 16 - 4, pass_len
     assert lib.bcm_scan_fwd(a, None) == 1 and "chunk_g needs" in lib.bcm_last_error().decode()
+
+
+def test_scan_refuses_chunk_states_of_another_family(lib):
+    """chunk_g records the pass length it was sized for (chunk_g_pass). A
+    forward run under one scan family and a backward under the other (which
+    walks passes of a different length) would read the pass states at the
+    wrong rows: both directions refuse a chunk_g whose pass length is not
+    their own, before any launch (pointers are never dereferenced)."""
+    a = nat.ScanArgs()
+    a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen, a.n_chunks, a.dtype = 8192 * 300, 8192, 256, 16, 367, 1, 0
+    a.cu_seqlens = a.dt_idle = a.dt_active = a.A = a.W_B = a.W_C = a.u = a.k = 16
+    a.out = a.x = 16
+    a.dA = a.dW_B = a.dW_C = a.ddt_idle = a.ddt_active = a.dout = a.du = 16
+    prev = nat.set_scan_family("lanes")
+    try:
+        lanes_pass, n_pass, needs = nat.scan_chunking(a)
+        assert needs and lanes_pass == 32
+        nat.set_scan_family("items")
+        items_pass, items_n, _ = nat.scan_chunking(a)
+        assert items_pass != lanes_pass
+        # a chunk_g laid out by a forward under the state lanes, large enough
+        # for either layout, refused by both directions of the lane groups
+        a.chunk_g, a.chunk_g_bytes = 16, 4 * 8192 * max(n_pass, items_n) * 16
+        a.chunk_g_pass = lanes_pass
+        for fn in (lib.bcm_scan_fwd, lib.bcm_scan_bwd):
+            assert fn(a, None) == 1
+            msg = lib.bcm_last_error().decode()
+            assert "passes of 32 events" in msg and f"passes of {items_pass}" in msg, msg
+        # no record at all (0) is refused too
+        nat.set_scan_family("lanes")
+        a.chunk_g_pass = 0
+        assert lib.bcm_scan_bwd(a, None) == 1 and "passes of 0 events" in lib.bcm_last_error().decode()
+    finally:
+        nat.set_scan_family(prev)
+
+
+def test_scan_family_setter_rejects_unknown_codes(lib):
+    prev = nat.set_scan_family("auto")
+    try:
+        assert lib.bcm_set_scan_family(7) == -1
+        assert lib.bcm_last_error().decode().startswith("bcm_set_scan_family")
+        assert nat.set_scan_family("items") == "auto"
+        assert nat.set_scan_family("lanes") == "items"
+    finally:
+        nat.set_scan_family(prev)
 
 
 def test_scan_backward_requires_chunk_states(lib):
@@ -197,23 +243,26 @@ def test_conv_events_backward_rejects_overlapping_rows(lib):
     assert call(64, 64) == 1 and "overlap" in lib.bcm_last_error().decode()
 
 
-def test_scan_family_choice_and_passes(monkeypatch):
+def test_scan_family_choice_and_passes():
     """The dstate-16 scan family: the state lanes (32-event passes kept in
     chunk_g) from 4096 channels on a 256-CU part (a wave of four channels
     per SIMD), the lane groups below that, other dstates always the lane
-    groups; BCM_SCAN_KERNEL overrides the choice on every call. Without a
+    groups; bcm_set_scan_family forces either for the process. Without a
     device the library assumes 256 CUs."""
     def chunking(nc, dstate, ms):
         a = nat.ScanArgs()
         a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen = nc * 100, nc, 256, dstate, ms
         return nat.scan_chunking(a)
-    monkeypatch.delenv("BCM_SCAN_KERNEL", raising=False)
-    assert chunking(8192, 16, 367) == (32, 12, 1)      # config 1: lanes, chunk_g rows every 32 events
-    assert chunking(4096, 16, 482) == (32, 16, 1)      # config 2: lanes
-    assert chunking(2048, 16, 482)[0] > 32             # half the SIMDs: lane groups
-    assert chunking(8192, 64, 367)[0] > 32             # dstate 64: lane groups
-    assert chunking(8192, 16, 20) == (32, 1, 0)        # one pass: no chunk_g
-    monkeypatch.setenv("BCM_SCAN_KERNEL", "lanes")
-    assert chunking(2048, 16, 482) == (32, 16, 1)
-    monkeypatch.setenv("BCM_SCAN_KERNEL", "items")
-    assert chunking(8192, 16, 367)[0] > 32
+    prev = nat.set_scan_family("auto")
+    try:
+        assert chunking(8192, 16, 367) == (32, 12, 1)      # config 1: lanes, chunk_g rows every 32 events
+        assert chunking(4096, 16, 482) == (32, 16, 1)      # config 2: lanes
+        assert chunking(2048, 16, 482)[0] > 32             # half the SIMDs: lane groups
+        assert chunking(8192, 64, 367)[0] > 32             # dstate 64: lane groups
+        assert chunking(8192, 16, 20) == (32, 1, 0)        # one pass: no chunk_g
+        nat.set_scan_family("lanes")
+        assert chunking(2048, 16, 482) == (32, 16, 1)
+        nat.set_scan_family("items")
+        assert chunking(8192, 16, 367)[0] > 32
+    finally:
+        nat.set_scan_family(prev)

@@ -102,8 +102,10 @@ def scan_oracle(w, st, ocu, oms, c0, c1):
     return (e0, e1), y, x, g
 
 
-def check_scan_channels(w, st, ocu, oms, och, ot, c0, c1, rtol_out):
-    (e0, e1), y, x, g = scan_oracle(w, st, ocu, oms, c0, c1)
+def check_scan_channels(w, st, ocu, oms, och, ot, c0, c1, rtol_out, ref=None):
+    """Scan out, x, du and the dense dx rows of channels [c0, c1) against
+    the oracle (`ref`: scan_oracle's result for them, if already run)."""
+    (e0, e1), y, x, g = ref if ref is not None else scan_oracle(w, st, ocu, oms, c0, c1)
     assert_close(n(st.y)[e0:e1], y, rtol_out, FLOOR, f"scan out [{c0},{c1})")
     assert_close(n(st.xs)[c0:c1], x, 1e-4, FLOOR, f"scan x [{c0},{c1})")
     assert_close(n(st.du)[e0:e1], g[0], rtol_out, FLOOR, f"du [{c0},{c1})")
@@ -144,20 +146,20 @@ def test_config_full_size_bench_kernels(cuda_device, cfg, scan_kernel):
 def test_config3_full_size_bench_kernels(cuda_device):
     """Config 3 (B64 D128 L4000 N64, bursty Markov events with half the
     channels below 2 %): multi-pass channels with chunk_g, model channels
-    split over workgroups. Indices on the full membrane; restore, scan out,
-    x, du and dx on every channel of two sampled batches; the six parameter
-    gradients over all 64 batches (the oracle run in batch slices, summed)."""
+    split over workgroups. Everything on every channel of all 64 batches:
+    indices on the full membrane, restore out and dy, and the oracle run in
+    8-batch slices for scan out, x, du, the dense dx rows and the six
+    parameter gradients (the slices' partial sums added)."""
     w, st = run_step(3, cuda_device)
     assert st.chunk_g is not None and st.split_ws is not None  # the multi-pass and split forms run
     och, ot, ok, ocu, oms = check_indices(w, st)
     B, D = w.B, w.D
-    sampled = (5, 42)
-    check_restore(w, st, och, ot, ocu, sel=sampled)
-    for b in sampled:
-        check_scan_channels(w, st, ocu, oms, och, ot, b * D, (b + 1) * D, 1e-4)
+    check_restore(w, st, och, ot, ocu)
     acc = None
     for b0 in range(0, B, 8):
-        _, _, _, g = scan_oracle(w, st, ocu, oms, b0 * D, (b0 + 8) * D)
+        c0, c1 = b0 * D, (b0 + 8) * D
+        print(f"config 3: batches {b0}..{b0 + 7}", flush=True)
+        g = check_scan_channels(w, st, ocu, oms, och, ot, c0, c1, 1e-4, ref=scan_oracle(w, st, ocu, oms, c0, c1))
         part = g[1:7]
         acc = list(part) if acc is None else [a + p for a, p in zip(acc, part)]
     check_param_grads(st, acc)

@@ -64,6 +64,8 @@ CASES = [  # B, D, L, d_model, density, mask_row_div
     (1, 32, 64, 16, 1.0, 1),       # every step an event
     (2, 64, 128, 64, 0.0, 1),      # no events: out = bias, dy empty
     (4, 512, 1024, 256, 0.07, 1),  # config-4 layer slice
+    (3, 64, 300, 64, 0.3, 1),      # LDS-DMA forward with an odd tile count (5 tiles: a half item pair)
+    (1, 4096, 128, 64, 0.1, 1),    # dim past the DMA forward's LDS: the register-staged form runs
 ]
 
 
