@@ -1032,7 +1032,7 @@ static ShapeId pick_shape(const bcm_scan_args& a) {
 
 static void chunking(const bcm_scan_args& a, int* pass_len, int* n_pass, int* needs_chunk_g) {
   const ShapeId id = pick_shape(a);
-  const int C = sl_applies(a) ? kSLPass : kShapeG[id] * kShapeR[id];
+  const int C = sl_applies(a) ? sl_pass_len(a.dstate) : kShapeG[id] * kShapeR[id];
   *pass_len = C;
   *n_pass = a.max_seqlen > 0 ? (a.max_seqlen + C - 1) / C : 1;
   *needs_chunk_g = (*n_pass > 1 && C < kXChunk) ? 1 : 0;

@@ -107,7 +107,9 @@ struct ScanRows {
 
 // ---- state-lane kernels (scan_sl.hip) for dstate 16: lane = (channel, state)
 constexpr int kSLN = 16;     // dstate they serve
-constexpr int kSLPass = 32;  // events per pass: chunk_g rows, the backward's unit of work
+constexpr int kSLPass = 32;  // events per pass (one state per lane): chunk_g rows, the backward's unit of work
+// Events per pass of the state-lane kernels for a dstate they serve.
+int sl_pass_len(int dstate);
 // True when the state-lane kernels run this scan (forward and backward
 // alike, so that chunk_g has the passes the backward expects).
 bool sl_applies(const bcm_scan_args& a);

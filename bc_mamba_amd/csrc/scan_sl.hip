@@ -1,32 +1,41 @@
-// Stage 2, dstate 16: the depthwise flat selective scan with one lane per
-// (channel, state), forward and backward.
+// Stage 2, dstate 16 / 32 / 64: the depthwise flat selective scan with one
+// lane per (channel, group of states), forward and backward.
 //
 // Reference behaviour: as scan.hip (selective_scan_fwd_kernel.cuh:403-728,
 // selective_scan_bwd_kernel.cuh:635-1169, the exponent clamp of
 // selective_scan_common.h:43-52).
 //
 // MI355X design
-//   * The 16 lanes of a DPP row own one channel, one state each; a wave holds
-//     four channels of one model channel d (one workgroup per d, as in
-//     scan.hip, so the per-d decay table and the parameter-gradient sums stay
-//     in the workgroup). Each lane walks its channel's events in order: the
-//     recurrence costs one table read and one fma per event and state, with
-//     no lane scans and no padding beyond a block's tail.
+//   * The 16 lanes of a DPP row own one channel; lane s holds states
+//     s + 16j, j < NL (NL = dstate / 16: one, two or four independent
+//     recurrences per lane). A wave holds four channels of one model channel
+//     d (one workgroup per d, as in scan.hip, so the per-d decay table and
+//     the parameter-gradient sums stay in the workgroup). Each lane walks its
+//     channel's events in order: the recurrence costs one table read and one
+//     fma per event and state, with no lane scans and no padding beyond a
+//     block's tail.
 //   * Events come in blocks of 16, one per lane of the row: lane j loads
 //     event 16·blk + j (coalesced), forms Δ, Δu², its table offset (and the
 //     backward's dout·u, k-1), and DPP row_newbcast:q hands event q's values
-//     to the whole row. The next blocks' loads are in flight while a block
-//     computes (a ring of registers), so memory latency overlaps the VALU.
+//     to the whole row, once for all NL states of a lane. The next blocks'
+//     loads are in flight while a block computes (a ring of registers), so
+//     memory latency overlaps the VALU.
 //   * Sums over the states of one event (y, and the backward's Σ_s W_B W_C e
 //     and Σ_s W_B W_C g) go through a padded LDS tile per row: state lane s
 //     writes its 16 values of the block at (q·17 + s), event lane j reads its
-//     16 states at (j·17 + m): conflict-free both ways, one fma per value
-//     with the per-state weight.
+//     16 states at (j·17 + m): conflict-free both ways. With one state per
+//     lane the reader applies the per-state weight; with several, each lane
+//     first forms its states' weighted sum, so the tile traffic per event
+//     stays one write and one read per lane.
 //   * The forward saves the state h at the start of every 32-event pass in
 //     chunk_g; the backward walks a channel's passes last to first, rebuilds
-//     the pass's states and decays in registers from that row, then runs the
-//     adjoint recurrence e_i = a_{i+1} e_{i+1} + dout_i u_i backward through
-//     them.
+//     the pass's states (and, up to two states per lane, decays) in registers
+//     from that row, then runs the adjoint recurrence
+//     e_i = a_{i+1} e_{i+1} + dout_i u_i backward through them.
+//   * Bursty streams (a longest channel of more than twice the mean): the
+//     workgroup first ranks its model channel's channels by length, and the
+//     four rows of a wave take neighbouring ranks, so a wave's rows end
+//     together; the two waves that share a SIMD pair long ranks with short.
 //   * Scaled recurrences as in scan.hip: g = h / W_B (g = a·g + Δu²) and
 //     e = dh / W_C.
 
@@ -43,8 +52,31 @@ namespace bcm {
 constexpr int kSLB = 16;                   // events per block (one per lane of a row)
 constexpr int kSLRows = kWave / kSLN;      // channels per wave
 constexpr int kSLTileSz = kSLN * (kSLN + 1);  // floats of one row's transpose tile (stride 17)
-constexpr int kSLTab = tab_gaps(kSLN);     // longest gap in the decay table (256)
 constexpr int kSLPF = 4;                   // blocks per load round (a round ahead in flight)
+
+// Shape of the state-lane kernels with NL states per lane (dstate 16·NL).
+// The decay table holds two copies interleaved, T[k][m][parity]: lane
+// (row g, state m) reads word 2(N k + m) + (g & 1), so the two rows
+// (channels) of a half-wave read disjoint banks whatever their gaps k (one
+// bank per lane: conflict-free); state m + 16j sits 128 bytes after m.
+template <int NL> struct SLShape {
+  static constexpr int N = kSLN * NL;            // dstate
+  static constexpr int Tab = tab_gaps(N);        // longest gap in the decay table
+  static constexpr uint32_t Gap = 2u * N * 4u;   // bytes per gap row of the table
+  static constexpr int TabSz = 2 * N * (Tab + 1);  // floats of the table
+  static constexpr int NA = 3 * N + 3;           // gradient accumulators per slot
+  // the backward keeps a pass's decays in registers beside its states up to
+  // two states per lane; with four it reads them from the table again
+  static constexpr bool KeepA = NL <= 2;
+  // events per table round of the backward: four states per lane read a
+  // half block at a time, so fewer decays are live beside the pass's states
+  static constexpr int H = NL == 4 ? 8 : 16;
+  // events per pass (chunk_g rows, the backward's unit of work): the pass's
+  // states stay in registers, four states per lane hold 16 events' worth
+  static constexpr int Pass = NL == 4 ? 16 : 32;
+};
+static_assert(SLShape<1>::Pass == kSLPass, "one state per lane: the scan_common pass length");
+__device__ __forceinline__ uint32_t sl_tab_lane(int s, int grp) { return (uint32_t)(2 * s + (grp & 1)) * 4; }
 
 // Value of lane Q of this lane's DPP row.
 template <int Q> __device__ __forceinline__ int bcast_i(int v) {
@@ -54,12 +86,14 @@ template <int Q> __device__ __forceinline__ float bcast_f(float v) {
   return __int_as_float(bcast_i<Q>(__float_as_int(v)));
 }
 
-// Decays of the 16 events of a block for this lane's state: each event's
+// Decays of the 16 events of a block for this lane's states: each event's
 // byte offset in a table row (lane q's tb) plus the lane's row base, one DPP
-// add per event. One s_nop 1 first: a DPP read needs two wait states after
-// the VALU write of its source, whichever instruction the compiler placed
-// just before; the adds themselves write no source of a later one.
-__device__ __forceinline__ void tab16(float (&av)[16], const float* sT, uint32_t rowb, uint32_t tb) {
+// add per event, then one read per state (states 16 apart are 128 bytes
+// apart). One s_nop 1 first: a DPP read needs two wait states after the VALU
+// write of its source, whichever instruction the compiler placed just
+// before; the adds themselves write no source of a later one.
+template <int NL>
+__device__ __forceinline__ void tab16(float (&av)[NL][16], const float* sT, uint32_t rowb, uint32_t tb) {
   uint32_t o[16];
   asm("s_nop 1\n\t"
       "v_add_u32_dpp %0, %16, %17 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
@@ -82,7 +116,39 @@ __device__ __forceinline__ void tab16(float (&av)[16], const float* sT, uint32_t
         "=&v"(o[8]), "=&v"(o[9]), "=&v"(o[10]), "=&v"(o[11]), "=&v"(o[12]), "=&v"(o[13]), "=&v"(o[14]), "=&v"(o[15])
       : "v"(tb), "v"(rowb));
 #pragma unroll
-  for (int q = 0; q < 16; ++q) av[q] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + o[q]);
+  for (int q = 0; q < 16; ++q)
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      av[j][q] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + o[q] + 128u * (uint32_t)j);
+}
+
+// Decays of events Q0..Q0+NQ-1 of a block, as tab16 (a shorter range keeps
+// fewer decays live: the four-state backward works in half blocks). The
+// s_nop 1 of the first add covers the source's last write; the hazard check
+// over the built assembly (tests/test_dpp_hazards.py) keeps it honest.
+// One event's table address: tb of lane Q of the row plus the lane's row base.
+template <int Q, bool NOP> __device__ __forceinline__ uint32_t tab_addr(uint32_t tb, uint32_t rowb) {
+  uint32_t o;
+  if constexpr (NOP)
+    asm("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+        : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
+  else
+    asm("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
+  return o;
+}
+template <int NL, int Q0, int NQ, int... Q>
+__device__ __forceinline__ void tabq_impl(float (&av)[NL][16], const float* sT, uint32_t rowb, uint32_t tb,
+                                          std::integer_sequence<int, Q...>) {
+  const uint32_t o[NQ] = {tab_addr<Q0 + Q, Q == 0>(tb, rowb)...};
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      av[j][Q0 + q] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(sT) + o[q] + 128u * (uint32_t)j);
+}
+template <int NL, int Q0, int NQ>
+__device__ __forceinline__ void tabq(float (&av)[NL][16], const float* sT, uint32_t rowb, uint32_t tb) {
+  tabq_impl<NL, Q0, NQ>(av, sT, rowb, tb, std::make_integer_sequence<int, NQ>{});
 }
 
 // acc += (value of lane Q of the row's src) * v as one v_fmac_f32_dpp (the
@@ -110,6 +176,21 @@ template <typename F, int... Q> __device__ __forceinline__ void rfor16_impl(F&& 
 template <typename F> __device__ __forceinline__ void rfor16(F&& f) {  // q = 15..0
   rfor16_impl(f, std::make_integer_sequence<int, 16>{});
 }
+// Calls f(std::integral_constant<int, q>) for q = Q0..Q0+NQ-1 (forr) or
+// q = Q0+NQ-1..Q0 (rforr).
+template <int Q0, typename F, int... Q> __device__ __forceinline__ void forr_impl(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q0 + Q>{}), ...);
+}
+template <int Q0, int NQ, typename F> __device__ __forceinline__ void forr(F&& f) {
+  forr_impl<Q0>(f, std::make_integer_sequence<int, NQ>{});
+}
+template <int Q0, int NQ, typename F, int... Q>
+__device__ __forceinline__ void rforr_impl(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q0 + NQ - 1 - Q>{}), ...);
+}
+template <int Q0, int NQ, typename F> __device__ __forceinline__ void rforr(F&& f) {
+  rforr_impl<Q0, NQ>(f, std::make_integer_sequence<int, NQ>{});
+}
 
 // Sum over the 16 lanes of a row, in every lane of it.
 __device__ __forceinline__ float row_sum(float v) {
@@ -120,47 +201,53 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
-// The decay table holds two copies interleaved, T[k][m][parity]: lane
-// (row g, state m) reads word 32k + 2m + (g & 1), so the two rows (channels)
-// of a half-wave read disjoint banks whatever their gaps k (one bank per
-// lane: conflict-free). Byte offset of gap k in it, and a lane's base.
-constexpr uint32_t kSLTabGap = 2 * kSLN * 4;
-constexpr int kSLTabSz = 2 * kSLN * (kSLTab + 1);  // floats
-__device__ __forceinline__ uint32_t sl_tab_lane(int s, int grp) { return (uint32_t)(2 * s + (grp & 1)) * 4u; }
-
 // Decay table of model channel d: T[m][0] = 1 (padding), T[m][k] = the
 // decay of gap k, the same expression as the per-event path. Thread t
-// builds the entries of state t % 16 (consecutive threads: consecutive
+// builds the entries of state t % N (consecutive threads: consecutive
 // words); its A value is loaded at the kernel's start (al), before the
 // first events' loads, so the build waits on no data load.
-__device__ __forceinline__ float sl_table_al(const bcm_scan_args& a, int d) {
-  return a.A[(int64_t)d * kSLN + threadIdx.x % kSLN] * kLog2e;
+template <int NL> __device__ __forceinline__ float sl_table_al(const bcm_scan_args& a, int d) {
+  constexpr int N = SLShape<NL>::N;
+  return a.A[(int64_t)d * N + threadIdx.x % N] * kLog2e;
 }
-__device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, float dta, int nw) {
-  const int m = threadIdx.x % kSLN;
-  for (int q = threadIdx.x / kSLN; q <= kSLTab; q += nw * (kWave / kSLN)) {
+template <int NL> __device__ __forceinline__ void sl_build_table(float* sT, float al, float dti, float dta, int nw) {
+  constexpr int N = SLShape<NL>::N;
+  const int m = threadIdx.x % N;
+  for (int q = threadIdx.x / N; q <= SLShape<NL>::Tab; q += nw * (kWave / N)) {
     const float v = q == 0 ? 1.0f : decay(fmaf(dti, (float)(q - 1), dta) * al);
-    reinterpret_cast<float2*>(sT)[q * kSLN + m] = make_float2(v, v);
+    reinterpret_cast<float2*>(sT)[q * N + m] = make_float2(v, v);
   }
 }
 
+// Where a slot stands in the length order of a ranked workgroup: the four
+// rows of a wave take neighbouring places, and of the two waves that share
+// a SIMD (w and w + 4 of 8) one takes a long place and the other a short one.
+__device__ __forceinline__ int sl_slot_order(int wave, int grp, int nw) {
+  const int k = (nw == 8 && wave >= 4) ? 11 - wave : wave;
+  return k * kSLRows + grp;
+}
+
 // ------------------------------------------------------------------ forward
-template <typename T, bool HAS_Z>
-__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int nw, int S) {
+// rank: rank the model channel's channels by length first (sord: [kSortMax]
+// ints of LDS, keys: kSortMax ints of scratch LDS, dead after the ranking).
+template <typename T, bool HAS_Z, int NL>
+__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int* sord, int* keys,
+                                            int nw, int S, int rank) {
 #pragma clang fp contract(off)  // fmas are written out where they are meant
+  using Sh = SLShape<NL>;
   constexpr uint32_t SZ = sizeof(T);
-  constexpr int N = kSLN;
+  constexpr int N = Sh::N;
   // the kernel arguments that the first loads need arrive with the first
   // batch of argument loads (one wait), not on demand one batch later
   asm volatile("" ::"s"(a.u), "s"(a.k), "s"(a.cu_seqlens), "s"(a.n_events), "s"(nw), "s"(S), "s"(a.D));
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim;
   const int wave = threadIdx.x / kWave, lane = lane_id();
-  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
+  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's first state, and its event slot in a block
   const int nslots = nw * kSLRows;
   const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
-  const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
+  const int g_rows = (a.max_seqlen + Sh::Pass - 1) / Sh::Pass;
 
   const int64_t E = a.n_events;
   const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
@@ -169,11 +256,13 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
 
   // The slot's first channel leads the kernel's loads: the first events'
   // loads wait for its bounds alone, and their latency overlaps the rest of
-  // the set-up (parameters, decay table).
+  // the set-up (parameters, decay table). A ranked workgroup ranks first.
   const int slot = wave * kSLRows + grp;
+  const int sorder = rank ? sl_slot_order(wave, grp, nw) : slot;
+  if (rank) rank_channels(a, d, n_per_d, keys, sord, nw * kWave);
   auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
-    const int v = r0 + slot * S + sp;
-    return v < n_per_d ? v : n_per_d;
+    const int v = r0 + sorder * S + sp;
+    return v < n_per_d ? (rank ? sord[v] : v) : n_per_d;
   };
   auto channel = [&](int r0, int& e0, int& n) {  // unconditional loads (a clamped row), then selected
     const int b = chan_at(r0);
@@ -187,16 +276,26 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   int e0, n;
   channel(0, e0, n);
 
-  const float al = sl_table_al(a, d);  // the table build waits for this load alone
+  const float al = sl_table_al<NL>(a, d);  // the table build waits for this load alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  const float Al = a.A[(int64_t)d * N + s] * kLog2e;
-  const float wb = a.W_B[(int64_t)d * N + s];
-  float wbc[N];  // W_B·W_C of every state (the event lanes' weights; wave-uniform, scalar registers)
+  float Al[NL], wb[NL], cw[NL];  // the lane's states s + 16j
 #pragma unroll
-  for (int m = 0; m < N; ++m)
-    wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
-        __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  for (int j = 0; j < NL; ++j) {
+    const int64_t ix = (int64_t)d * N + s + kSLN * j;
+    Al[j] = a.A[ix] * kLog2e;
+    wb[j] = a.W_B[ix];
+    cw[j] = NL > 1 ? wb[j] * a.W_C[ix] : 0.0f;
+  }
+  // one state per lane: W_B·W_C of every state, the event lanes' weights
+  // (wave-uniform, scalar registers); several: each lane weights its own
+  float wbc[NL == 1 ? kSLN : 1];
+  if constexpr (NL == 1) {
+#pragma unroll
+    for (int m = 0; m < kSLN; ++m)
+      wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
+          __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  }
   const uint32_t rowb = sl_tab_lane(s, grp);
 
   // the loads of a channel's block round r
@@ -213,10 +312,10 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   };
   issue(e0, 0);
   // a decay exponent that can be positive (A > 0 or Δ < 0): lane products
-  // of decays are multiplied out instead of taken as exp2 of a Δ sum (the
-  // rows' 16 lanes hold all of A[d]; uniform over the workgroup)
+  // of decays are multiplied out instead of taken as exp2 of a Δ sum (a
+  // wave's lanes hold all of A[d]; uniform over the workgroup)
   const bool exact = __any(al > 0.0f) || dti < 0.0f || dta < 0.0f;
-  sl_build_table(sT, al, dti, dta, nw);
+  sl_build_table<NL>(sT, al, dti, dta, nw);
   __syncthreads();
 
   auto run = [&](auto exact_tag) {
@@ -235,33 +334,56 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
       // channel's end: the loads read the next channel's values or 0, unused).
       // Blocks go in rounds of kSLPF: a round's loads are issued when the round
       // before it starts, so each has a round of compute to arrive in.
-      float g = 0.0f, P = 1.0f, sdl = 0.0f;
+      float g[NL], P[NL];
+#pragma unroll
+      for (int j = 0; j < NL; ++j) g[j] = 0.0f, P[j] = 1.0f;
+      float sdl = 0.0f;
       auto block = [&](const int bk, const float uv, const int kk, const float zv) {
         const int i = bk * kSLB + s;
         const bool valid = i < n;
         // padding events are identities: Δ = 0 -> a = 1 (table entry 0), Δu² = 0
         const float dl = valid ? fmaf(dti, (float)(kk - 1), dta) : 0.0f;
         const float du2 = dl * uv * uv;
-        const int big = valid && kk > kSLTab;
+        const int big = valid && kk > Sh::Tab;
         sdl += dl;
-        float av[kSLB];
-        tab16(av, sT, rowb, valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u);
+        float av[NL][kSLB];
+        tab16<NL>(av, sT, rowb, valid ? (uint32_t)min(kk, Sh::Tab) * Sh::Gap : 0u);
         if (__builtin_expect(__any(big), 0)) {  // gaps past the table: computed decays
           for16([&](auto q) {
             constexpr int Q = decltype(q)::value;
             const float dq = bcast_f<Q>(dl);  // row-uniform condition: lane Q of the row is active
-            if (bcast_i<Q>(big)) av[Q] = decay(dq * Al);
+            if (bcast_i<Q>(big)) {
+#pragma unroll
+              for (int j = 0; j < NL; ++j) av[j][Q] = decay(dq * Al[j]);
+            }
           });
         }
         for16([&](auto q) {
-          g = fmaf(av[q], g, bcast_f<decltype(q)::value>(du2));
-          if (EXACT) P *= av[q];
-          xt[q * (kSLN + 1) + s] = g;
+          constexpr int Q = decltype(q)::value;
+          if constexpr (NL == 1) {
+            g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2));
+            if (EXACT) P[0] *= av[0][Q];
+            xt[Q * (kSLN + 1) + s] = g[0];
+          } else {
+            const float x = bcast_f<Q>(du2);
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+              g[j] = fmaf(av[j][Q], g[j], x);
+              if (EXACT) P[j] *= av[j][Q];
+            }
+            float w = cw[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
+#pragma unroll
+            for (int j = 1; j < NL; ++j) w = fmaf(cw[j], g[j], w);
+            xt[Q * (kSLN + 1) + s] = w;
+          }
         });
         wave_sync();
         float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
 #pragma unroll
-        for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+        for (int m = 0; m < kSLN; ++m) {
+          if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+          else acc += xt[s * (kSLN + 1) + m];
+        }
         wave_sync();  // the tile is rewritten by the next block
         const float y = fmaf(Dv, uv, uv * acc);
         const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
@@ -275,13 +397,18 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
         if (__any(xsave)) {
           const float sd = row_sum(sdl);
           if (xsave) {
-            const float Pn = EXACT ? P : decay(sd * Al);
-            reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s] = make_float2(Pn, g * wb);
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+              const float Pn = EXACT ? P[j] : decay(sd * Al[j]);
+              reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s + kSLN * j] = make_float2(Pn, g[j] * wb[j]);
+            }
           }
         }
         const int pend = (bk + 1) * kSLB;  // events before the next pass start, when it is one
-        if (a.chunk_g && pend % kSLPass == 0 && pend < n && pend / kSLPass < g_rows)
-          a.chunk_g[(ch * g_rows + pend / kSLPass) * N + s] = g * wb;
+        if (a.chunk_g && pend % Sh::Pass == 0 && pend < n && pend / Sh::Pass < g_rows) {
+#pragma unroll
+          for (int j = 0; j < NL; ++j) a.chunk_g[(ch * g_rows + pend / Sh::Pass) * N + s + kSLN * j] = g[j] * wb[j];
+        }
       };
       for (int r = 0; r * kSLPF < wblk; ++r) {
         float U[kSLPF], Z[kSLPF];
@@ -300,8 +427,8 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
       // chunks past the channel's end keep the reference's zero state
       if (act) {
         for (int c = (n + kXChunk - 1) / kXChunk; c < nck; ++c) {
-          a.x[(ch * nck + c) * 2 * N + s] = 0.0f;
-          a.x[(ch * nck + c) * 2 * N + N + s] = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 2 * NL; ++j) a.x[(ch * nck + c) * 2 * N + s + kSLN * j] = 0.0f;
         }
       }
     }
@@ -312,64 +439,88 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
 
 // nw: waves per workgroup, S: workgroups per model channel (the launch's
 // shape, passed rather than read from blockDim / gridDim, whose loads would
-// come before any other work)
-template <typename T, bool HAS_Z>
-__global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a, int nw, int S) {
-  __shared__ float sT[kSLTabSz];
+// come before any other work); rank: rank the channels by length first
+template <typename T, bool HAS_Z, int NL>
+__global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a, int nw, int S, int rank) {
+  __shared__ float sT[SLShape<NL>::TabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
+  __shared__ int sord[kSortMax];
+  static_assert(sizeof(sX) >= kSortMax * sizeof(int), "the transpose tiles hold the ranking keys");
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
   float* xt = &sX[wave][grp * kSLTileSz];
-  sl_fwd_body<T, HAS_Z>(a, sT, xt, nw, S);
+  sl_fwd_body<T, HAS_Z, NL>(a, sT, xt, sord, reinterpret_cast<int*>(&sX[0][0]), nw, S, rank);
 }
 
 // ----------------------------------------------------------------- backward
 // A channel's passes of kSLPass events, last to first. Each pass rebuilds its
-// states g and decays a in registers from the pass-start state the forward
-// saved (phase A, blocks 0..3), then runs the adjoint backward through them
-// (phase B, blocks 3..0): e_i = doutu_i + f, f = a_i e_i carried to the
-// event before (and across passes). Per state lane: T0 = Σ tg, T1 = Σ tg·(k-1)
+// states g (and decays a) in registers from the pass-start state the forward
+// saved (phase A, blocks 0..1), then runs the adjoint backward through them
+// (phase B, blocks 1..0): e_i = doutu_i + f, f = a_i e_i carried to the
+// event before (and across passes). Per state: T0 = Σ tg, T1 = Σ tg·(k-1)
 // with tg = f·g_{i-1}, and Σ e·Δu² (dW_B; dW_C is the same sum, since
 // Σ_i dout_i u_i g_i = Σ_i e_i Δ_i u_i² over a channel). Per event lane:
 // Σ_s W_B W_C g_s (phase A) and Σ_s W_B W_C e_s (phase B) through the
 // transpose tile, then du, the Δ terms of ddt and dD.
 constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its dense row
 
-template <typename T, bool HAS_Z, bool DXR>
+// Calls f(std::integral_constant<int, j>) for j = 0..NL-1.
+template <int NL, typename F, int... J> __device__ __forceinline__ void forj_impl(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <int NL, typename F> __device__ __forceinline__ void forj(F&& f) {
+  forj_impl<NL>(f, std::make_integer_sequence<int, NL>{});
+}
+
+template <typename T, bool HAS_Z, bool DXR, int NL>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
-                                            float* sacc, float* sdu, int nw, int S) {
+                                            float* sacc, float* sdu, int* sord, int* keys, int nw, int S, int rank) {
   // no implicit fma contraction: the instantiations (with and without the
   // dense rows) round alike, so their gradients are bit-equal; fmas are
   // written out where they are meant
 #pragma clang fp contract(off)
+  static_assert(!DXR || NL == 1, "the dense rows are written by the one-state-per-lane kernel");
+  using Sh = SLShape<NL>;
+  constexpr bool KEEPA = Sh::KeepA;
   constexpr uint32_t SZ = sizeof(T);
-  constexpr int N = kSLN;
-  constexpr int NA = 3 * N + 3;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
+  constexpr int N = Sh::N;
+  constexpr int NA = Sh::NA;  // accumulators per slot: dA, dW_B, dW_C, ddt_idle, ddt_active, dD
   // the arguments of the channel bounds' loads come in the first batch of
   // argument loads (more operands here cost scalar-register spills)
   asm volatile("" ::"s"(a.cu_seqlens), "s"(nw), "s"(S));
-  constexpr int NB = kSLPass / kSLB;  // blocks per pass
+  constexpr int NB = Sh::Pass / kSLB;  // blocks per pass
   const int d = blockIdx.x % a.dim;
   const int sp = blockIdx.x / a.dim;
   const int nthr = nw * kWave;
   const int wave = threadIdx.x / kWave, lane = lane_id();
-  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's state, and its event slot in a block
+  const int grp = lane / kSLN, s = lane % kSLN;  // s: the lane's first state, and its event slot in a block
   const int slot = wave * kSLRows + grp, nslots = nw * kSLRows;
   const int NC = a.n_channels, dim = a.dim;
   const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
-  const int g_rows = (a.max_seqlen + kSLPass - 1) / kSLPass;
+  const int g_rows = (a.max_seqlen + Sh::Pass - 1) / Sh::Pass;
 
-  const float al = sl_table_al(a, d);  // first load of the kernel: the table build waits for it alone
+  const float al = sl_table_al<NL>(a, d);  // first load of the kernel: the table build waits for it alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  const float Av = a.A[(int64_t)d * N + s];
-  const float Al = Av * kLog2e;
-  const float wb = a.W_B[(int64_t)d * N + s], wc = a.W_C[(int64_t)d * N + s];
-  const float wbc_s = wb * wc, wbca = wbc_s * Av;
-  float wbc[N];  // W_B·W_C of every state (the event lanes' weights; wave-uniform, scalar registers)
+  float Al[NL], wb[NL], wc[NL], wbcs[NL], wbca[NL];  // the lane's states s + 16j
 #pragma unroll
-  for (int m = 0; m < N; ++m)
-    wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
-        __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  for (int j = 0; j < NL; ++j) {
+    const int64_t ix = (int64_t)d * N + s + kSLN * j;
+    const float Av = a.A[ix];
+    Al[j] = Av * kLog2e;
+    wb[j] = a.W_B[ix];
+    wc[j] = a.W_C[ix];
+    wbcs[j] = wb[j] * wc[j];
+    wbca[j] = wbcs[j] * Av;
+  }
+  // one state per lane: W_B·W_C of every state, the event lanes' weights
+  // (wave-uniform, scalar registers); several: each lane weights its own
+  float wbc[NL == 1 ? kSLN : 1];
+  if constexpr (NL == 1) {
+#pragma unroll
+    for (int m = 0; m < kSLN; ++m)
+      wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
+          __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+  }
   const uint32_t rowb = sl_tab_lane(s, grp);
 
   for (int i = threadIdx.x; i < nslots * NA; i += nthr) sacc[i] = 0.0f;
@@ -382,16 +533,16 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.chunk_g, a.chunk_g ? a.chunk_g_bytes : 0);
 
-  // The lane's events of pass p: e0 + 32p + 16t + s (t = 0, 1); loads past
+  // The lane's events of pass p: e0 + Pass·p + 16t + s (t < NB); loads past
   // the channel's end read the next channel's values or 0 and are unused.
   // A pass's loads are issued when the pass after it (in the walk: before
   // it) starts; unconditional, so the registers never merge with old values.
-  float Un[NB], Dn[NB], Zn[NB], On[NB], Gn;
+  float Un[NB], Dn[NB], Zn[NB], On[NB], Gn[NL];
   int Kn[NB];
   auto issue = [&](int e0, int64_t ch, int p) {
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      const uint32_t o = (uint32_t)(e0 + p * kSLPass + t * kSLB + s);
+      const uint32_t o = (uint32_t)(e0 + p * Sh::Pass + t * kSLB + s);
       Un[t] = buf_load<T>(ru, o * SZ);
       Kn[t] = buf_load_i32(rk, o * 4u);
       Dn[t] = buf_load<T>(rdo, o * SZ);
@@ -399,12 +550,18 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
       On[t] = HAS_Z ? buf_load<T>(ros, o * SZ) : 0.0f;
     }
     // pass-start state h of pass p (chunk_g row p, written by the forward)
-    Gn = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-        rg, (uint32_t)(((ch * g_rows + p) * N + s) * 4), 0, 0));
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      Gn[j] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+          rg, (uint32_t)(((ch * g_rows + p) * N + s + kSLN * j) * 4), 0, 0));
   };
+  // a ranked workgroup ranks its channels first; the keys live in the
+  // transpose tiles, which the zeroing above does not touch
+  const int sorder = rank ? sl_slot_order(wave, grp, nw) : slot;
+  if (rank) rank_channels(a, d, n_per_d, keys, sord, nthr);
   auto chan_at = [&](int r0) {  // channel b of the slot in round r0 (n_per_d: none)
-    const int v = r0 + slot * S + sp;
-    return v < n_per_d ? v : n_per_d;
+    const int v = r0 + sorder * S + sp;
+    return v < n_per_d ? (rank ? sord[v] : v) : n_per_d;
   };
   auto channel = [&](int r0, int& e0, int& n, int64_t& ch) {  // unconditional loads (a clamped row), then selected
     const int b = chan_at(r0);
@@ -419,21 +576,24 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   int64_t ch;
   channel(0, e0, n, ch);
   // at least one pass: the dense rows of empty channels are written by it
-  int wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
+  int wp = max(1, wave_max_dpp((n + Sh::Pass - 1) / Sh::Pass));
   issue(e0, ch, wp - 1);
-  sl_build_table(sT, al, dti, dta, nw);
+  sl_build_table<NL>(sT, al, dti, dta, nw);
   __syncthreads();
 
   for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
     if (r0 > 0) {
       channel(r0, e0, n, ch);
-      wp = max(1, wave_max_dpp((n + kSLPass - 1) / kSLPass));
+      wp = max(1, wave_max_dpp((n + Sh::Pass - 1) / Sh::Pass));
       issue(e0, ch, wp - 1);
     }
     const bool act = chan_at(r0) < n_per_d;
-    const int np = (n + kSLPass - 1) / kSLPass;
-    float f = 0.0f;  // a·e of the event after the current one
-    float T0 = 0.0f, T1 = 0.0f, dWB = 0.0f, ddti_l = 0.0f, ddta_l = 0.0f, dD_l = 0.0f;
+    const int np = (n + Sh::Pass - 1) / Sh::Pass;
+    float f[NL];  // a·e of the event after the current one
+    float T0[NL], T1[NL], dWB[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) f[j] = T0[j] = T1[j] = dWB[j] = 0.0f;
+    float ddti_l = 0.0f, ddta_l = 0.0f, dD_l = 0.0f;
     for (int p = wp - 1; p >= 0; --p) {
       float uv[NB], gg[NB], dl[NB], km[NB], du2[NB], doutu[NB], acc2[NB];
       uint32_t tb[NB];
@@ -441,7 +601,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
       // the lane's own events of the pass: Δ, Δu², the gated dout (and dz)
 #pragma unroll
       for (int t = 0; t < NB; ++t) {
-        const int i = p * kSLPass + t * kSLB + s;
+        const int i = p * Sh::Pass + t * kSLB + s;
         const bool valid = i < n;
         const int kk = Kn[t];
         uv[t] = Un[t];
@@ -457,37 +617,70 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         km[t] = valid ? (float)(kk - 1) : 0.0f;
         du2[t] = dl[t] * uv[t] * uv[t];
         doutu[t] = valid ? dv * uv[t] : 0.0f;
-        tb[t] = valid ? (uint32_t)min(kk, kSLTab) * kSLTabGap : 0u;
-        big[t] = valid && kk > kSLTab;
+        tb[t] = valid ? (uint32_t)min(kk, Sh::Tab) * Sh::Gap : 0u;
+        big[t] = valid && kk > Sh::Tab;
       }
-      const float h0 = Gn;
-      const float g_in = (p >= 1 && p < np && p < g_rows && wb != 0.0f) ? h0 / wb : 0.0f;
-      issue(e0, ch, p - 1);  // the next pass of the walk (past the start: unused)
-      // ---- phase A: states and decays of the pass, Σ_s W_B W_C g_s per event
-      float gb[kSLPass], ab[kSLPass];
-      float g = g_in;
+      float g_in[NL];
 #pragma unroll
-      for (int t = 0; t < NB; ++t) {
-        float av[kSLB];
-        tab16(av, sT, rowb, tb[t]);
+      for (int j = 0; j < NL; ++j) g_in[j] = (p >= 1 && p < np && p < g_rows && wb[j] != 0.0f) ? Gn[j] / wb[j] : 0.0f;
+      issue(e0, ch, p - 1);  // the next pass of the walk (past the start: unused)
+      // decays of events Q0..Q0+H-1 of block t for the lane's states, from the
+      // table or computed
+      constexpr int H = Sh::H;
+      auto decays = [&](float (&av)[NL][kSLB], int t, auto q0c) {
+        constexpr int Q0 = decltype(q0c)::value;
+        tabq<NL, Q0, H>(av, sT, rowb, tb[t]);
         if (__builtin_expect(__any(big[t]), 0)) {  // gaps past the table: computed decays
-          for16([&](auto q) {
+          forr<Q0, H>([&](auto q) {
             constexpr int Q = decltype(q)::value;
             const float dq = bcast_f<Q>(dl[t]);  // row-uniform condition: lane Q of the row is active
-            if (bcast_i<Q>(big[t])) av[Q] = decay(dq * Al);
+            if (bcast_i<Q>(big[t])) {
+#pragma unroll
+              for (int j = 0; j < NL; ++j) av[j][Q] = decay(dq * Al[j]);
+            }
           });
         }
-        for16([&](auto q) {
+      };
+      // ---- phase A: states (and decays) of the pass, Σ_s W_B W_C g_s per event
+      float gb[Sh::Pass][NL], ab[KEEPA ? Sh::Pass : 1][NL];
+      float g[NL];
+#pragma unroll
+      for (int j = 0; j < NL; ++j) g[j] = g_in[j];
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        forr<0, kSLB / H>([&](auto hc) {
+        constexpr int Q0 = decltype(hc)::value * H;
+        float av[NL][kSLB];
+        decays(av, t, std::integral_constant<int, Q0>{});
+        forr<Q0, H>([&](auto q) {
           constexpr int Q = decltype(q)::value;
-          g = fmaf(av[Q], g, bcast_f<Q>(du2[t]));
-          gb[t * kSLB + Q] = g;
-          ab[t * kSLB + Q] = av[Q];
-          xt[Q * (kSLN + 1) + s] = g;
+          if constexpr (NL == 1) {
+            g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2[t]));
+            gb[t * kSLB + Q][0] = g[0];
+            ab[t * kSLB + Q][0] = av[0][Q];
+            xt[Q * (kSLN + 1) + s] = g[0];
+          } else {
+            const float x = bcast_f<Q>(du2[t]);
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+              g[j] = fmaf(av[j][Q], g[j], x);
+              gb[t * kSLB + Q][j] = g[j];
+              if constexpr (KEEPA) ab[t * kSLB + Q][j] = av[j][Q];
+            }
+            float w = wbcs[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
+#pragma unroll
+            for (int j = 1; j < NL; ++j) w = fmaf(wbcs[j], g[j], w);
+            xt[Q * (kSLN + 1) + s] = w;
+          }
+        });
         });
         wave_sync();
         float acc = 0.0f;
 #pragma unroll
-        for (int m = 0; m < N; ++m) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+        for (int m = 0; m < kSLN; ++m) {
+          if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+          else acc += xt[s * (kSLN + 1) + m];
+        }
         acc2[t] = acc;
         wave_sync();
       }
@@ -495,24 +688,51 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
 #pragma unroll
       for (int tt = 0; tt < NB; ++tt) {
         const int t = NB - 1 - tt;
-        rfor16([&](auto q) {
+        rforr<0, kSLB / H>([&](auto hc) {
+        constexpr int Q0 = decltype(hc)::value * H;
+        float av[KEEPA ? 1 : NL][kSLB];  // four states per lane: the block's decays read again
+        if constexpr (!KEEPA) decays(av, t, std::integral_constant<int, Q0>{});
+        rforr<Q0, H>([&](auto q) {
           constexpr int Q = decltype(q)::value;
           const int I = t * kSLB + Q;
-          const float e = f + bcast_f<Q>(doutu[t]);
-          f = ab[I] * e;
-          const float tg = f * (I > 0 ? gb[I > 0 ? I - 1 : 0] : g_in);
-          T0 += tg;
-          fmac_bcast<Q, Q == kSLB - 1>(T1, km[t], tg);   // T1 += (k-1)·tg
-          fmac_bcast<Q, Q == kSLB - 1>(dWB, du2[t], e);  // dWB += Δu²·e
-          xt[Q * (kSLN + 1) + s] = e;
+          if constexpr (NL == 1) {
+            const float e = f[0] + bcast_f<Q>(doutu[t]);
+            f[0] = ab[I][0] * e;
+            const float tg = f[0] * (I > 0 ? gb[I > 0 ? I - 1 : 0][0] : g_in[0]);
+            T0[0] += tg;
+            fmac_bcast<Q, Q == kSLB - 1>(T1[0], km[t], tg);   // T1 += (k-1)·tg
+            fmac_bcast<Q, Q == kSLB - 1>(dWB[0], du2[t], e);  // dWB += Δu²·e
+            xt[Q * (kSLN + 1) + s] = e;
+          } else {
+            const float dq = bcast_f<Q>(doutu[t]);
+            float w = 0.0f;
+            forj<NL>([&](auto jc) {
+              constexpr int J = decltype(jc)::value;
+              const float e = f[J] + dq;
+              float aj;
+              if constexpr (KEEPA) aj = ab[I][J];
+              else aj = av[J][Q];
+              f[J] = aj * e;
+              const float tg = f[J] * (I > 0 ? gb[I > 0 ? I - 1 : 0][J] : g_in[J]);
+              T0[J] += tg;
+              fmac_bcast<Q, Q == kSLB - 1 && J == 0>(T1[J], km[t], tg);   // T1 += (k-1)·tg
+              fmac_bcast<Q, Q == kSLB - 1 && J == 0>(dWB[J], du2[t], e);  // dWB += Δu²·e
+              w = J == 0 ? wbcs[0] * e : fmaf(wbcs[J], e, w);
+            });
+            xt[Q * (kSLN + 1) + s] = w;
+          }
+        });
         });
         wave_sync();
         float acc1 = 0.0f;
 #pragma unroll
-        for (int m = 0; m < N; ++m) acc1 = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc1);
+        for (int m = 0; m < kSLN; ++m) {
+          if constexpr (NL == 1) acc1 = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc1);
+          else acc1 += xt[s * (kSLN + 1) + m];
+        }
         wave_sync();
         // the lane's own event of block t: du, the Δu² terms of ddt, dD
-        const int i = p * kSLPass + t * kSLB + s;
+        const int i = p * Sh::Pass + t * kSLB + s;
         const float duv = fmaf(gg[t], Dv + acc2[t], 2.0f * dl[t] * uv[t] * acc1);
         const float dd = uv[t] * uv[t] * acc1;  // the A-term of dΔ goes into ddt through T0, T1
         ddti_l = fmaf(dd, km[t], ddti_l);
@@ -527,15 +747,22 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
       }
     }
     // the channel's parameter-gradient terms into the slot's accumulators
-    ddti_l = fmaf(wbca, T1, ddti_l);
-    ddta_l = fmaf(wbca, T0, ddta_l);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      ddti_l = fmaf(wbca[j], T1[j], ddti_l);
+      ddta_l = fmaf(wbca[j], T0[j], ddta_l);
+    }
     ddti_l = row_sum(ddti_l);
     ddta_l = row_sum(ddta_l);
     dD_l = row_sum(dD_l);
     if (act) {
-      cacc[s] = fmaf(wbc_s, fmaf(dti, T1, dta * T0), cacc[s]);
-      cacc[N + s] = fmaf(dWB, wc, cacc[N + s]);
-      cacc[2 * N + s] = fmaf(dWB, wb, cacc[2 * N + s]);
+#pragma unroll
+      for (int j = 0; j < NL; ++j) {
+        const int m = s + kSLN * j;
+        cacc[m] = fmaf(wbcs[j], fmaf(dti, T1[j], dta * T0[j]), cacc[m]);
+        cacc[N + m] = fmaf(dWB[j], wc[j], cacc[N + m]);
+        cacc[2 * N + m] = fmaf(dWB[j], wb[j], cacc[2 * N + m]);
+      }
       if (s == 0) {
         cacc[3 * N] += ddti_l;
         cacc[3 * N + 1] += ddta_l;
@@ -609,16 +836,19 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   }
 }
 
-template <typename T, bool HAS_Z, bool DXR>
+template <typename T, bool HAS_Z, bool DXR, int NL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw, int nw,
-                                                               int S) {
-  __shared__ float sT[kSLTabSz];
+                                                               int S, int rank) {
+  __shared__ float sT[SLShape<NL>::TabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
-  __shared__ float sacc[kScanThreads / kWave * kSLRows * (3 * kSLN + 3)];
+  __shared__ float sacc[kScanThreads / kWave * kSLRows * SLShape<NL>::NA];
+  __shared__ int sord[kSortMax];
+  static_assert(sizeof(sX) >= kSortMax * sizeof(int), "the transpose tiles hold the ranking keys");
   extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
-  sl_bwd_body<T, HAS_Z, DXR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc, sdu + (wave * kSLRows + grp) * kSLRowCap,
-                             nw, S);
+  sl_bwd_body<T, HAS_Z, DXR, NL>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
+                                 sdu + (wave * kSLRows + grp) * kSLRowCap, sord, reinterpret_cast<int*>(&sX[0][0]), nw,
+                                 S, rank);
 }
 
 // ------------------------------------------------------------------- host
@@ -640,20 +870,32 @@ int scan_family() {
   return f;
 }
 
-// Which family runs a dstate-16 scan. The state lanes give one wave per four
-// channels, so they pay when the channels fill every SIMD with at least one
-// wave (config 2, 4096 channels on 256 CUs: 125-127 against 130-131 µs per
-// step; the forward is 2-3 µs slower there, the backward 5-7 µs faster);
-// below that the lane groups of scan.hip, which split a channel over 16
-// lanes, keep more of the chip busy. bcm_set_scan_family forces either
-// family (the tests run both on the same shapes).
+// Which family runs a depthwise scan of dstate 16, 32 or 64. The state lanes
+// give one wave per four channels, so they pay when the channels fill every
+// SIMD with at least one wave (config 2, 4096 channels on 256 CUs: 125-127
+// against 130-131 µs per step; the forward is 2-3 µs slower there, the
+// backward 5-7 µs faster); below that the lane groups of scan.hip, which
+// split a channel over 16 lanes, keep more of the chip busy.
+// bcm_set_scan_family forces either family (the tests run both on the same
+// shapes); other dstates always take the lane groups.
 bool sl_applies(const bcm_scan_args& a) {
-  if (a.dstate != kSLN) return false;
+  if (a.dstate != kSLN && a.dstate != 2 * kSLN && a.dstate != 4 * kSLN) return false;
   const int f = scan_family();
   if (f == BCM_SCAN_LANES) return true;
   if (f == BCM_SCAN_ITEMS) return false;
   return (int64_t)a.n_channels >= (int64_t)kSLRows * 4 * device_cus();
 }
+
+// Rank the channels by length when the stream is bursty (the longest
+// channel more than twice the mean) and a model channel's channels fill
+// more than one wave: the rows of a wave then end together.
+static int sl_rank(const bcm_scan_args& a) {
+  const int64_t per_d = (a.n_channels + a.dim - 1) / a.dim;
+  if (per_d <= kSLRows || per_d > kSortMax || a.n_channels < 1) return 0;
+  return 2 * a.n_events < (int64_t)a.max_seqlen * a.n_channels ? 1 : 0;
+}
+
+int sl_pass_len(int dstate) { return dstate == 4 * kSLN ? SLShape<4>::Pass : kSLPass; }
 
 int sl_split(const bcm_scan_args& a) {
   const int per_d = (a.n_channels + a.dim - 1) / a.dim;
@@ -670,32 +912,51 @@ static int sl_waves(const bcm_scan_args& a) {
   return std::max(1, std::min(kScanThreads / kWave, nw));
 }
 
-int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
-  const int S = sl_split(a), nw = sl_waves(a);
-  const dim3 grid((unsigned)((int64_t)a.dim * S)), block((unsigned)(nw * kWave));
+template <int NL> static void sl_fwd_nl(const bcm_scan_args& a, hipStream_t st, dim3 grid, dim3 block, int nw, int S,
+                                        int rank) {
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
-    if (a.z) hipLaunchKernelGGL((k_scan_fwd_sl<T, true>), grid, block, 0, st, a, nw, S);
-    else hipLaunchKernelGGL((k_scan_fwd_sl<T, false>), grid, block, 0, st, a, nw, S);
+    if (a.z) hipLaunchKernelGGL((k_scan_fwd_sl<T, true, NL>), grid, block, 0, st, a, nw, S, rank);
+    else hipLaunchKernelGGL((k_scan_fwd_sl<T, false, NL>), grid, block, 0, st, a, nw, S, rank);
   });
+}
+
+int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
+  const int S = sl_split(a), nw = sl_waves(a), rank = sl_rank(a);
+  const dim3 grid((unsigned)((int64_t)a.dim * S)), block((unsigned)(nw * kWave));
+  if (a.dstate == kSLN) sl_fwd_nl<1>(a, st, grid, block, nw, S, rank);
+  else if (a.dstate == 2 * kSLN) sl_fwd_nl<2>(a, st, grid, block, nw, S, rank);
+  else sl_fwd_nl<4>(a, st, grid, block, nw, S, rank);
   return check_launch(fn);
+}
+
+template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, dim3 grid, dim3 block, int nw, int S,
+                                        int rank, const ScanRows* rw) {
+  const ScanRows rows = rw ? *rw : ScanRows{};
+  dispatch_dtype(a.dtype, [&](auto tag) {
+    using T = decltype(tag);
+    if constexpr (NL == 1) {
+      if (rw) {
+        hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st,
+                           a, rows, nw, S, rank);
+        return;
+      }
+    }
+    if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
+    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
+  });
 }
 
 int sl_launch_bwd(const bcm_scan_args& a, hipStream_t st, const char* fn, const ScanRows* rw) {
   int S = sl_split(a);
   // no (or too small a) workspace for the partials: one workgroup per model channel
   if (!a.split_ws || a.split_ws_bytes < 4 * (int64_t)S * a.dim * (3 * a.dstate + 3)) S = 1;
-  const int nw = sl_waves(a);
+  const int nw = sl_waves(a), rank = sl_rank(a);
   const dim3 grid((unsigned)((int64_t)a.dim * S)), block((unsigned)(nw * kWave));
-  const ScanRows rows = rw ? *rw : ScanRows{};
-  dispatch_dtype(a.dtype, [&](auto tag) {
-    using T = decltype(tag);
-    if (rw)
-      hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st, a,
-                         rows, nw, S);
-    else if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false>), grid, block, 0, st, a, rows, nw, S);
-    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false>), grid, block, 0, st, a, rows, nw, S);
-  });
+  if (rw && a.dstate != kSLN) return set_error(BCM_EINVAL, "%s: no fused dense rows for dstate %d", fn, a.dstate);
+  if (a.dstate == kSLN) sl_bwd_nl<1>(a, st, grid, block, nw, S, rank, rw);
+  else if (a.dstate == 2 * kSLN) sl_bwd_nl<2>(a, st, grid, block, nw, S, rank, rw);
+  else sl_bwd_nl<4>(a, st, grid, block, nw, S, rank, rw);
   int rc = check_launch(fn);
   if (rc || S == 1) return rc;
   return sl_param_reduce(a, S, st, fn);
@@ -705,7 +966,8 @@ int sl_launch_bwd(const bcm_scan_args& a, hipStream_t st, const char* fn, const 
 // LDS row (max_seqlen <= kSLRowCap), no z, 4-step aligned rows.
 bool sl_rows_fusable(const bcm_scan_args& a, const bcm_scan_rows& r) {
   const uintptr_t p = reinterpret_cast<uintptr_t>(r.dx);
-  return !a.z && a.max_seqlen <= kSLRowCap && r.seqlen % 4 == 0 && p % (4 * dtype_size(a.dtype)) == 0;
+  return a.dstate == kSLN && !a.z && a.max_seqlen <= kSLRowCap && r.seqlen % 4 == 0 &&
+         p % (4 * dtype_size(a.dtype)) == 0;
 }
 
 }  // namespace bcm

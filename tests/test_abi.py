@@ -244,11 +244,12 @@ def test_conv_events_backward_rejects_overlapping_rows(lib):
 
 
 def test_scan_family_choice_and_passes():
-    """The dstate-16 scan family: the state lanes (32-event passes kept in
-    chunk_g) from 4096 channels on a 256-CU part (a wave of four channels
-    per SIMD), the lane groups below that, other dstates always the lane
-    groups; bcm_set_scan_family forces either for the process. Without a
-    device the library assumes 256 CUs."""
+    """The scan family: the state lanes (32-event passes kept in chunk_g; 16
+    with four states per lane) for dstate 16, 32 and 64 from 4096 channels
+    on a 256-CU part (a wave of four channels per SIMD), the lane groups
+    below that, other dstates always the lane groups; bcm_set_scan_family
+    forces either for the process. Without a device the library assumes 256
+    CUs."""
     def chunking(nc, dstate, ms):
         a = nat.ScanArgs()
         a.n_events, a.n_channels, a.dim, a.dstate, a.max_seqlen = nc * 100, nc, 256, dstate, ms
@@ -258,7 +259,10 @@ def test_scan_family_choice_and_passes():
         assert chunking(8192, 16, 367) == (32, 12, 1)      # config 1: lanes, chunk_g rows every 32 events
         assert chunking(4096, 16, 482) == (32, 16, 1)      # config 2: lanes
         assert chunking(2048, 16, 482)[0] > 32             # half the SIMDs: lane groups
-        assert chunking(8192, 64, 367)[0] > 32             # dstate 64: lane groups
+        assert chunking(8192, 64, 1111) == (16, 70, 1)     # config 3: four states per lane, 16-event passes
+        assert chunking(8192, 32, 367) == (32, 12, 1)      # two states per lane
+        assert chunking(2048, 64, 367)[0] > 32             # half the SIMDs: lane groups
+        assert chunking(8192, 48, 367)[0] > 32             # dstate 48: lane groups
         assert chunking(8192, 16, 20) == (32, 1, 0)        # one pass: no chunk_g
         nat.set_scan_family("lanes")
         assert chunking(2048, 16, 482) == (32, 16, 1)

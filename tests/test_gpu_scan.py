@@ -12,7 +12,8 @@ from bc_mamba_amd import selective_scan_interface as ssi
 from conftest import assert_close
 from oracle import event_path as orc
 
-# every case under both dstate-16 kernel families (other dstates: the same kernel twice)
+# every case under both kernel families (dstate 16, 32 and 64: the lane groups
+# and the state lanes; other dstates: the lane groups twice)
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("scan_kernel")]
 
 TOL = {torch.float32: (1e-4, 1e-6), torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3)}
@@ -97,6 +98,9 @@ SHAPES = [  # B, D, L, density, N  (max_seqlen lands in each kernel-shape bucket
     # no decay table and ~3000-event channels: 2048-event passes that re-seed
     # from the saved x (no chunk_g), as the reference does
     (1, 2, 6000, 0.5, 80),
+    # two states per lane (dstate 32): single and multi-pass, two x chunks
+    (2, 4, 700, 0.4, 32),
+    (4, 2, 3000, 0.8, 32),
 ]
 
 
@@ -140,12 +144,23 @@ def test_scan_clamped_decays(cuda_device):
     _run_and_check(c, torch.float32, cuda_device)
 
 
+@pytest.mark.parametrize("N", [16, 32, 64])
+@pytest.mark.parametrize("with_z", [False, True])
+def test_scan_states_per_lane(cuda_device, N, with_z):
+    """One, two and four states per lane of the state-lane kernels (dstate
+    16, 32, 64; the lane groups under the other family): z gate, clamped
+    long-gap decays past the table (sparse channels) and gaps within it."""
+    c = _case(2, 8, 1500, 0.15, N, torch.float32, seed=40 + N, with_z=with_z, p_short=0.01, long_every=3)
+    _run_and_check(c, torch.float32, cuda_device)
+
+
+@pytest.mark.parametrize("N", [16, 32, 64])
 @pytest.mark.parametrize("kind", ["A_positive", "dt_negative"])
-def test_scan_exact_products(cuda_device, kind):
+def test_scan_exact_products(cuda_device, kind, N):
     """Decay exponents that can be positive (A > 0 for some states, or a
     negative Δ): the saved x then carries the multiplied-out decay products
     instead of exp2 of a Δ sum (the kernels' exact path)."""
-    c = _case(2, 4, 300, 0.3, 16, torch.float32, seed=31)
+    c = _case(2, 4, 300, 0.3, N, torch.float32, seed=31)
     g = torch.Generator().manual_seed(32)
     if kind == "A_positive":  # small growth rates on a third of the states
         grow = torch.rand(c["A"].shape, generator=g) < 0.33
@@ -223,7 +238,9 @@ def test_scan_multipass_chunk_states(cuda_device, B, D, L, p, ps, le, N):
 
 @pytest.mark.parametrize("B,D,L,p,ps,N", [
     (96, 2, 300, 0.5, None, 16),    # 96 channels per model channel: three rounds of 32
-    (64, 2, 1200, 0.6, 0.02, 16),   # bursty multi-pass, two rounds
+    (64, 2, 1200, 0.6, 0.02, 16),   # bursty multi-pass, two rounds (state lanes: length-ranked)
+    (64, 2, 1200, 0.6, 0.02, 64),   # the same with four states per lane (config-3 form)
+    (40, 3, 900, 0.5, 0.02, 32),    # two states per lane, ranked, rounds not filled
 ])
 def test_scan_split_workgroups(cuda_device, B, D, L, p, ps, N):
     """Few model channels with many channels each: the backward splits every
@@ -240,13 +257,14 @@ def test_scan_split_workgroups(cuda_device, B, D, L, p, ps, N):
     assert all(torch.equal(x, y) for x, y in zip(g1, g2))  # deterministic
 
 
+@pytest.mark.parametrize("N", [16, 64])
 @pytest.mark.parametrize("true_ms_scale", [3, 1])
-def test_scan_reports_understated_max_seqlen(cuda_device, true_ms_scale):
+def test_scan_reports_understated_max_seqlen(cuda_device, true_ms_scale, N):
     """A max_seqlen below the longest channel: the kernels keep every write
     inside the buffers sized from it and flag the channel in the status word;
     the Python entry points raise. With the true max_seqlen the status stays
     0 (regression test of the chunk_g bound and the status report)."""
-    c = _case(2, 8, 1200, 0.4, 16, torch.float32, seed=11, p_short=0.05)
+    c = _case(2, 8, 1200, 0.4, N, torch.float32, seed=11, p_short=0.05)
     true_ms = int(c["ms"])
     ms = true_ms // true_ms_scale
     print(f"seqlen status case: max_seqlen {ms} for channels of up to {true_ms} events", flush=True)
@@ -257,7 +275,7 @@ def test_scan_reports_understated_max_seqlen(cuda_device, true_ms_scale):
     if ms < true_ms:
         with pytest.raises(RuntimeError, match="more than max_seqlen"):
             ssc.fwd_flat_ch(*args, D=cud(c["D"]), is_depthwise_bc=True)
-        x = torch.zeros((16, ssc.n_chunks_for(ms), 32), device=dev)
+        x = torch.zeros((16, ssc.n_chunks_for(ms), 2 * N), device=dev)
         with pytest.raises(RuntimeError, match="more than max_seqlen"):
             ssc.bwd_flat_ch(*args, cud(c["dout"]), x, D=cud(c["D"]), is_depthwise_bc=True)
     else:
