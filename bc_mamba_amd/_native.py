@@ -38,6 +38,7 @@ class ScanArgs(ctypes.Structure):
 
 
 SCAN_SEQLEN_EXCEEDED = 1  # bcm_scan_args.status: a channel holds more than max_seqlen events
+SCAN_ROWS_INCOMPLETE = 2  # bcm_scan_args.status: bcm_scan_bwd_rows left the dense rows incomplete
 
 
 class ScanRows(ctypes.Structure):

@@ -463,6 +463,36 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_arg
 // transpose tile, then du, the Δ terms of ddt and dD.
 constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its dense row
 
+// Four steps t0..t0+3 of a channel's dense gradient row (the gather
+// backward) from its du in LDS, in event order: each value is the next
+// event's du masked by the step's bit (0 / -1), the LDS index advancing one
+// slot per set bit. m: the tile's event mask, tv: the index of its first
+// event, off = t0 % 64 (the lane's first step in the tile).
+template <typename T>
+__device__ __forceinline__ void dense_seg(T* dr, const float* sdu, int e0, uint64_t m, int32_t tv, int off, int t0) {
+  const uint32_t lo_keep = off >= 32 ? 0xFFFFFFFFu : (1u << off) - 1u;
+  const uint32_t hi_keep = off > 32 ? (1u << (off - 32)) - 1u : 0u;
+  const uint32_t sh = (uint32_t)off & 31u;
+  const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+  int e = tv - e0 + (int)(__builtin_popcount(mlo & lo_keep) + __builtin_popcount(mhi & hi_keep));
+  const uint32_t w = off >= 32 ? mhi : mlo;
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int32_t mk = __builtin_amdgcn_sbfe((int32_t)w, sh + (uint32_t)k, 1u);
+    o[k] = __float_as_uint(sdu[min(max(e, 0), kSLRowCap - 1)]) & (uint32_t)mk;
+    e -= mk;
+  }
+  if constexpr (sizeof(T) == 4) {
+    st_stream(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(dr + t0));
+  } else {
+    T h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h[k] = from_f<T>(__uint_as_float(o[k]));
+    st_stream(*reinterpret_cast<u32x2*>(h), reinterpret_cast<u32x2*>(dr + t0));
+  }
+}
+
 // Calls f(std::integral_constant<int, j>) for j = 0..NL-1.
 template <int NL, typename F, int... J> __device__ __forceinline__ void forj_impl(F&& f, std::integer_sequence<int, J...>) {
   (f(std::integral_constant<int, J>{}), ...);
@@ -471,14 +501,19 @@ template <int NL, typename F> __device__ __forceinline__ void forj(F&& f) {
   forj_impl<NL>(f, std::make_integer_sequence<int, NL>{});
 }
 
-template <typename T, bool HAS_Z, bool DXR, int NL>
+// WR: the dense rows are written by the workgroup's row writers
+// (sl_row_writer) as the passes finish; the waves here publish, per slot,
+// the first event whose du is final in prog.
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
-                                            float* sacc, float* sdu, int* sord, int* keys, int nw, int S, int rank) {
+                                            float* sacc, float* sdu, int* sord, int* keys, int* prog, int nw, int S,
+                                            int rank) {
   // no implicit fma contraction: the instantiations (with and without the
   // dense rows) round alike, so their gradients are bit-equal; fmas are
   // written out where they are meant
 #pragma clang fp contract(off)
   static_assert(!DXR || NL == 1, "the dense rows are written by the one-state-per-lane kernel");
+  static_assert(!WR || DXR, "row writers write dense rows");
   using Sh = SLShape<NL>;
   constexpr bool KEEPA = Sh::KeepA;
   constexpr uint32_t SZ = sizeof(T);
@@ -575,6 +610,11 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   int e0, n;
   int64_t ch;
   channel(0, e0, n, ch);
+  // a single round with row writers: nothing final yet but the (vacuous)
+  // events from n on; an idle slot has nothing to write
+  if constexpr (WR) {
+    if ((lane & (kSLN - 1)) == 0) prog[slot] = chan_at(0) < n_per_d ? n : 0;
+  }
   // at least one pass: the dense rows of empty channels are written by it
   int wp = max(1, wave_max_dpp((n + Sh::Pass - 1) / Sh::Pass));
   issue(e0, ch, wp - 1);
@@ -745,6 +785,13 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         // neighbouring slots' rows)
         if (DXR && valid && i < kSLRowCap) sdu[i] = duv;
       }
+      if constexpr (WR) {
+        // every du from event p·Pass on is in LDS: the writer may take the
+        // tiles whose first event is there (the release orders the du
+        // stores before the flag)
+        if ((lane & (kSLN - 1)) == 0)
+          __hip_atomic_store(&prog[slot], p * Sh::Pass, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
     // the channel's parameter-gradient terms into the slot's accumulators
 #pragma unroll
@@ -769,7 +816,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         cacc[3 * N + 2] += dD_l;
       }
     }
-    if constexpr (DXR) {
+    if constexpr (DXR && !WR) {
       // dense gradient row of the channel from its du in LDS (event order):
       // the row's 16 lanes take one 64-step tile per store, lane j writing
       // steps 4j..4j+3, each value the next event's du masked by the step's
@@ -781,29 +828,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         T* dr = static_cast<T*>(rw.dx) + ch * rw.L;
         const int L = (int)rw.L;
         const int off = 4 * s;  // the lane's first step in a tile
-        const uint32_t lo_keep = off >= 32 ? 0xFFFFFFFFu : (1u << off) - 1u;
-        const uint32_t hi_keep = off > 32 ? (1u << (off - 32)) - 1u : 0u;
-        const uint32_t sh = (uint32_t)off & 31u;
-        auto seg = [&](uint64_t m, int32_t tv, int t0) {
-          const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
-          int e = tv - e0 + (int)(__builtin_popcount(mlo & lo_keep) + __builtin_popcount(mhi & hi_keep));
-          const uint32_t w = off >= 32 ? mhi : mlo;
-          uint32_t o[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int32_t mk = __builtin_amdgcn_sbfe((int32_t)w, sh + (uint32_t)k, 1u);
-            o[k] = __float_as_uint(sdu[min(max(e, 0), kSLRowCap - 1)]) & (uint32_t)mk;
-            e -= mk;
-          }
-          if constexpr (sizeof(T) == 4) {
-            st_stream(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(dr + t0));
-          } else {
-            T h[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) h[k] = from_f<T>(__uint_as_float(o[k]));
-            st_stream(*reinterpret_cast<u32x2*>(h), reinterpret_cast<u32x2*>(dr + t0));
-          }
-        };
+        auto seg = [&](uint64_t m, int32_t tv, int t0) { dense_seg<T>(dr, sdu, e0, m, tv, off, t0); };
         const int nfull = L / kTile;  // tiles whose 64 steps are all < L
         constexpr int BAT = 8;
         int q0 = 0;
@@ -836,19 +861,119 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   }
 }
 
-template <typename T, bool HAS_Z, bool DXR, int NL>
-__global__ __launch_bounds__(kScanThreads) void k_scan_bwd_sl(const bcm_scan_args a, const ScanRows rw, int nw,
-                                                               int S, int rank) {
+// Dense-row writer of a single-round workgroup (one wave per SIMD beside
+// the compute waves): writer k writes the rows of compute waves k and k + 4
+// (the waves on its SIMD; the host uses writers with at most four compute
+// waves, so only wave k), each tile as soon as the du of its events are in
+// LDS, so the rows' 4 bytes per step leave during the adjoint loops instead
+// of in a burst after them. A tile is ready when its first event is at or
+// after the slot's published progress (every published value is a valid
+// bound: each event from it on has its final du). Lane l writes steps
+// 4(l % 16)..+3 of tile j0 + 4i + l / 16. The wait is bounded: after
+// kRowWriterPolls empty polls the writer stops and flags the status word
+// (BCM_SCAN_ROWS_INCOMPLETE), so every wave reaches the final barrier.
+constexpr int kRowWriterPolls = 1 << 20;
+constexpr int kRowWriterTiles = 64;  // most tiles per row (the lane of each tile's table entry)
+
+template <typename T>
+__device__ void sl_row_writer(const bcm_scan_args& a, const ScanRows& rw, const float* sdu_all, const int* prog,
+                              int nw, int S) {
+  constexpr int kC = 2 * kSLRows;  // the rows of two compute waves
+  const int d = blockIdx.x % a.dim, sp = blockIdx.x / a.dim;
+  const int wk = threadIdx.x / kWave - nw;
+  const int lane = lane_id();
+  const int NC = a.n_channels, dim = a.dim;
+  const int n_per_d = d < NC ? (NC - d + dim - 1) / dim : 0;
+  const int L = (int)rw.L;
+  const int nfull = L / kTile;
+  const int ntile = nfull + (nfull * kTile < L ? 1 : 0);  // at most kRowWriterTiles (the host's condition)
+  int hi[kC], e0c[kC];
+  int32_t tsv[kC];  // lane j: the tile table entry j of the channel
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const int w = wk + 4 * (c / kSLRows);
+    const int v = (w * kSLRows + c % kSLRows) * S + sp;  // the slot's only channel
+    const bool act = w < nw && v < n_per_d;
+    const int64_t ch = (int64_t)d + (int64_t)(act ? v : 0) * dim;
+    e0c[c] = act ? a.cu_seqlens[ch] : 0;
+    hi[c] = act ? ntile : 0;  // tiles [0, hi) still to write
+    tsv[c] = act && lane < ntile ? rw.ts[ch * (rw.nT + 1) + lane] : INT_MAX;
+  }
+  __syncthreads();  // the compute waves' set-up: decay table, progress initialised
+
+  auto write_tiles = [&](int c, int j0, int j1) {
+    const int w = wk + 4 * (c / kSLRows), slot = w * kSLRows + c % kSLRows;
+    const int64_t ch = (int64_t)d + (int64_t)(slot * S + sp) * dim;
+    const uint32_t* mrow = rw.bitmask + (ch / rw.mrd) * rw.W;
+    const int32_t* tsr = rw.ts + ch * (rw.nT + 1);
+    T* dr = static_cast<T*>(rw.dx) + ch * rw.L;
+    const float* sdu = sdu_all + slot * kSLRowCap;
+    const int sub = lane >> 4, off = 4 * (lane & 15);
+    constexpr int BAT = 8;
+    for (int jb = j0; jb < j1; jb += 4 * BAT) {
+      uint64_t m[BAT];
+      int32_t tv[BAT];
+#pragma unroll
+      for (int i = 0; i < BAT; ++i) {  // masks and table entries in flight together (clamped rows)
+        const int jj = min(jb + 4 * i + sub, j1 - 1);
+        m[i] = tile_mask(mrow, jj);
+        tv[i] = tsr[jj];
+      }
+#pragma unroll
+      for (int i = 0; i < BAT; ++i) {
+        const int j = jb + 4 * i + sub;
+        if (j < j1 && j * kTile + off < L) dense_seg<T>(dr, sdu, e0c[c], m[i], tv[i], off, j * kTile + off);
+      }
+    }
+  };
+  bool done = false;
+  for (int it = 0; it < kRowWriterPolls && !done; ++it) {
+    done = true;
+    bool wrote = false;
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      if (hi[c] == 0) continue;
+      done = false;
+      const int w = wk + 4 * (c / kSLRows);
+      const int pg = __hip_atomic_load(&prog[w * kSLRows + c % kSLRows], __ATOMIC_ACQUIRE,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+      // the ready tiles of [0, hi) are a suffix (the table rises with j)
+      const uint64_t ready = __ballot(lane < hi[c] && tsv[c] - e0c[c] >= pg);
+      const int jlo = ready ? (int)__builtin_ctzll(ready) : hi[c];
+      if (jlo < hi[c]) {
+        write_tiles(c, jlo, hi[c]);
+        hi[c] = jlo;
+        wrote = true;
+      }
+    }
+    if (!done && !wrote) __builtin_amdgcn_s_sleep(2);
+  }
+  if (!done && a.status && lane == 0) a.status[0] = BCM_SCAN_ROWS_INCOMPLETE;
+  __syncthreads();  // the compute waves' final barrier
+}
+
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR = false>
+__global__ __launch_bounds__(WR ? kScanThreads + 4 * kWave : kScanThreads) void k_scan_bwd_sl(
+    const bcm_scan_args a, const ScanRows rw, int nw, int S, int rank) {
   __shared__ float sT[SLShape<NL>::TabSz];
   __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   __shared__ float sacc[kScanThreads / kWave * kSLRows * SLShape<NL>::NA];
   __shared__ int sord[kSortMax];
+  __shared__ int sprog[WR ? kScanThreads / kWave * kSLRows : 1];
   static_assert(sizeof(sX) >= kSortMax * sizeof(int), "the transpose tiles hold the ranking keys");
   extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
-  sl_bwd_body<T, HAS_Z, DXR, NL>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
-                                 sdu + (wave * kSLRows + grp) * kSLRowCap, sord, reinterpret_cast<int*>(&sX[0][0]), nw,
-                                 S, rank);
+  if constexpr (WR) {
+    if (wave >= nw) {
+      sl_row_writer<T>(a, rw, sdu, sprog, nw, S);
+      return;
+    }
+  }
+  // row writers need a single unranked round (the host's choice); rank 0
+  // keeps the barrier count of both kinds of wave equal
+  sl_bwd_body<T, HAS_Z, DXR, NL, WR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
+                                     sdu + (wave * kSLRows + grp) * kSLRowCap, sord,
+                                     reinterpret_cast<int*>(&sX[0][0]), sprog, nw, S, WR ? 0 : rank);
 }
 
 // ------------------------------------------------------------------- host
@@ -937,8 +1062,19 @@ template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, 
     using T = decltype(tag);
     if constexpr (NL == 1) {
       if (rw) {
-        hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1>), grid, block, (size_t)nw * kSLRows * kSLRowCap * 4, st,
-                           a, rows, nw, S, rank);
+        const size_t lds = (size_t)nw * kSLRows * kSLRowCap * 4;
+        // one unranked round of channels on rows of at most 64 tiles, one
+        // compute wave per SIMD: row writers beside the compute waves (config
+        // 2: scan backward 43.5 -> 41.2 us). With two compute waves per SIMD
+        // the writers' work slows the adjoint loops more than the rows' burst
+        // at the end costs (config 1: 42.5-42.8 -> 45.3-45.7 us, whatever the
+        // writers' poll interval), so those shapes write the rows in-wave.
+        const int64_t per_d = (a.n_channels + a.dim - 1) / a.dim;
+        if (!rank && nw <= 4 && per_d <= (int64_t)nw * kSLRows * S && rows.nT <= kRowWriterTiles)
+          hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1, true>), grid, dim3(block.x + 4 * kWave), lds, st, a,
+                             rows, nw, S, rank);
+        else
+          hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1>), grid, block, lds, st, a, rows, nw, S, rank);
         return;
       }
     }

@@ -126,9 +126,13 @@ class _SeqlenStatus:
         a.status = self.t.data_ptr() if self.t is not None else None
 
     def check(self):
-        if self.t is not None and int(self.t.item()) == _nat.SCAN_SEQLEN_EXCEEDED:
+        v = int(self.t.item()) if self.t is not None else 0
+        if v == _nat.SCAN_SEQLEN_EXCEEDED:
             raise RuntimeError(f"{self.fn}: a channel holds more than max_seqlen = {self.max_seqlen} events "
                                "(cu_seqlens and max_seqlen disagree)")
+        if v == _nat.SCAN_ROWS_INCOMPLETE:
+            raise RuntimeError(f"{self.fn}: the dense gradient rows are incomplete (a row writer stopped waiting "
+                               "for the scan)")
 
 
 def _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB=None, dC=None):

@@ -257,7 +257,8 @@ typedef struct bcm_scan_args {
    * more than max_seqlen events: x and chunk_g are sized from max_seqlen,
    * so such a channel's saved states (and with them the backward of its
    * later passes, and bcm_scan_bwd_rows' dense row) are incomplete. Every
-   * write stays inside the buffers either way. */
+   * write stays inside the buffers either way. bcm_scan_bwd_rows may also
+   * set BCM_SCAN_ROWS_INCOMPLETE (see below). */
   int32_t* status;
   /* Events per pass that chunk_g is laid out for: the pass_len that
    * bcm_scan_chunking returned when the caller sized chunk_g (the forward
@@ -270,6 +271,10 @@ typedef struct bcm_scan_args {
 } bcm_scan_args;
 
 #define BCM_SCAN_SEQLEN_EXCEEDED 1
+/* bcm_scan_bwd_rows only: the dense rows were left incomplete because a row
+ * writer stopped waiting for the scan waves (a bounded wait that correct
+ * runs never reach; reported rather than risking a wave that never ends). */
+#define BCM_SCAN_ROWS_INCOMPLETE 2
 
 /* Which kernel family runs a depthwise scan, for the whole process:
  * BCM_SCAN_AUTO picks by shape (the state lanes of dstate 16 from one wave

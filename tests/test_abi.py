@@ -79,6 +79,7 @@ def test_scan_rows_arguments_are_rejected_before_launch(lib):
 def test_header_constants_match_binding():
     text = open(HEADER).read()
     for name, value in (("BCM_ABI_VERSION", nat.ABI_VERSION), ("BCM_SCAN_SEQLEN_EXCEEDED", nat.SCAN_SEQLEN_EXCEEDED),
+                        ("BCM_SCAN_ROWS_INCOMPLETE", nat.SCAN_ROWS_INCOMPLETE),
                         ("BCM_RESTORE_BWD_NOALLOC_MAX_TILES", nat.RESTORE_BWD_NOALLOC_MAX_TILES)):
         m = re.search(r"#define\s+%s\s+(\d+)" % name, text)
         assert m and int(m.group(1)) == value, name
