@@ -34,6 +34,7 @@ class ScanArgs(ctypes.Structure):
         ("du", c_p), ("dA", c_p), ("dW_B", c_p), ("dW_C", c_p), ("ddt_idle", c_p),
         ("ddt_active", c_p), ("dD", c_p), ("dz", c_p), ("chunk_g", c_p), ("chunk_g_bytes", c_i64),
         ("split_ws", c_p), ("split_ws_bytes", c_i64), ("status", c_p), ("chunk_g_pass", c_i32),
+        ("acc", c_p),
     ]
 
 

@@ -349,6 +349,19 @@ __global__ __launch_bounds__((kScanThreadsG<G, false>)) void k_scan_fwd(const bc
           }
         }
       }
+      if (a.acc) {  // the per-event state sums for a backward that reuses them (uniform)
+        const __amdgpu_buffer_rsrc_t racc = buf_rsrc(a.acc, E * 4);
+        wave_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r) mine[r] = acc[r];
+        wave_sync();
+        const int jo = opaque(j);
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          const int idx = q * G + jo;
+          buf_store_f32(racc, idx < cnt ? (eb + idx) * 4u : kBufOOB, tp.at(tile, q));
+        }
+      }
       wave_sync();  // the tile and the carry (written by lane G-1) are reused in the next chunk
     }
     // chunks past the channel's end keep the reference's zero state

@@ -253,6 +253,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
   const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
   const __amdgpu_buffer_rsrc_t ro = buf_rsrc(a.out, E * SZ);
   const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), roz = buf_rsrc(a.out_z, HAS_Z ? E * SZ : 0);
+  const __amdgpu_buffer_rsrc_t racc = buf_rsrc(a.acc, a.acc ? E * 4 : 0);  // empty: the stores are dropped
 
   // The slot's first channel leads the kernel's loads: the first events'
   // loads wait for its bounds alone, and their latency overlaps the rest of
@@ -388,6 +389,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
         const float y = fmaf(Dv, uv, uv * acc);
         const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
         buf_store<T>(ro, eo, y);
+        buf_store_f32(racc, valid ? off(e0, bk) * 4u : kBufOOB, acc);  // for the backward (dropped without acc)
         if (HAS_Z) buf_store<T>(roz, eo, y * (zv / (1.0f + __expf(-zv))));
         // saved states at the block end: x after every 2048 events and after
         // the channel's last one; chunk_g at every pass start
@@ -567,12 +569,16 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
   const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.chunk_g, a.chunk_g ? a.chunk_g_bytes : 0);
+  // the forward's per-event state sums: phase A then rebuilds the states
+  // alone, without the transpose of each block (uniform over the launch)
+  const bool use_acc = a.acc != nullptr;
+  const __amdgpu_buffer_rsrc_t racc = buf_rsrc(a.acc, use_acc ? E * 4 : 0);
 
   // The lane's events of pass p: e0 + Pass·p + 16t + s (t < NB); loads past
   // the channel's end read the next channel's values or 0 and are unused.
   // A pass's loads are issued when the pass after it (in the walk: before
   // it) starts; unconditional, so the registers never merge with old values.
-  float Un[NB], Dn[NB], Zn[NB], On[NB], Gn[NL];
+  float Un[NB], Dn[NB], Zn[NB], On[NB], Gn[NL], An[NB];
   int Kn[NB];
   auto issue = [&](int e0, int64_t ch, int p) {
 #pragma unroll
@@ -581,6 +587,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
       Un[t] = buf_load<T>(ru, o * SZ);
       Kn[t] = buf_load_i32(rk, o * 4u);
       Dn[t] = buf_load<T>(rdo, o * SZ);
+      An[t] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(racc, o * 4u, 0, 0));
       Zn[t] = HAS_Z ? buf_load<T>(rz, o * SZ) : 0.0f;
       On[t] = HAS_Z ? buf_load<T>(ros, o * SZ) : 0.0f;
     }
@@ -660,6 +667,8 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         tb[t] = valid ? (uint32_t)min(kk, Sh::Tab) * Sh::Gap : 0u;
         big[t] = valid && kk > Sh::Tab;
       }
+#pragma unroll
+      for (int t = 0; t < NB; ++t) acc2[t] = An[t];  // the forward's sums (0 without acc: replaced below)
       float g_in[NL];
 #pragma unroll
       for (int j = 0; j < NL; ++j) g_in[j] = (p >= 1 && p < np && p < g_rows && wb[j] != 0.0f) ? Gn[j] / wb[j] : 0.0f;
@@ -682,48 +691,59 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         }
       };
       // ---- phase A: states (and decays) of the pass, Σ_s W_B W_C g_s per event
+      // (USE: taken from the forward's sums instead; uniform, so the two forms
+      // are separate code)
       float gb[Sh::Pass][NL], ab[KEEPA ? Sh::Pass : 1][NL];
-      float g[NL];
+      auto phase_a = [&](auto use_tag) {
+        constexpr bool USE = decltype(use_tag)::value;
+        float g[NL];
 #pragma unroll
-      for (int j = 0; j < NL; ++j) g[j] = g_in[j];
+        for (int j = 0; j < NL; ++j) g[j] = g_in[j];
 #pragma unroll
-      for (int t = 0; t < NB; ++t) {
-        forr<0, kSLB / H>([&](auto hc) {
-        constexpr int Q0 = decltype(hc)::value * H;
-        float av[NL][kSLB];
-        decays(av, t, std::integral_constant<int, Q0>{});
-        forr<Q0, H>([&](auto q) {
-          constexpr int Q = decltype(q)::value;
-          if constexpr (NL == 1) {
-            g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2[t]));
-            gb[t * kSLB + Q][0] = g[0];
-            ab[t * kSLB + Q][0] = av[0][Q];
-            xt[Q * (kSLN + 1) + s] = g[0];
-          } else {
-            const float x = bcast_f<Q>(du2[t]);
+        for (int t = 0; t < NB; ++t) {
+          forr<0, kSLB / H>([&](auto hc) {
+            constexpr int Q0 = decltype(hc)::value * H;
+            float av[NL][kSLB];
+            decays(av, t, std::integral_constant<int, Q0>{});
+            forr<Q0, H>([&](auto q) {
+              constexpr int Q = decltype(q)::value;
+              if constexpr (NL == 1) {
+                g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2[t]));
+                gb[t * kSLB + Q][0] = g[0];
+                ab[t * kSLB + Q][0] = av[0][Q];
+                if constexpr (!USE) xt[Q * (kSLN + 1) + s] = g[0];
+              } else {
+                const float x = bcast_f<Q>(du2[t]);
 #pragma unroll
-            for (int j = 0; j < NL; ++j) {
-              g[j] = fmaf(av[j][Q], g[j], x);
-              gb[t * kSLB + Q][j] = g[j];
-              if constexpr (KEEPA) ab[t * kSLB + Q][j] = av[j][Q];
+                for (int j = 0; j < NL; ++j) {
+                  g[j] = fmaf(av[j][Q], g[j], x);
+                  gb[t * kSLB + Q][j] = g[j];
+                  if constexpr (KEEPA) ab[t * kSLB + Q][j] = av[j][Q];
+                }
+                if constexpr (!USE) {
+                  float w = wbcs[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
+#pragma unroll
+                  for (int j = 1; j < NL; ++j) w = fmaf(wbcs[j], g[j], w);
+                  xt[Q * (kSLN + 1) + s] = w;
+                }
+              }
+            });
+          });
+          if constexpr (!USE) {
+            wave_sync();
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < kSLN; ++m) {
+              if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
+              else acc += xt[s * (kSLN + 1) + m];
             }
-            float w = wbcs[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
-#pragma unroll
-            for (int j = 1; j < NL; ++j) w = fmaf(wbcs[j], g[j], w);
-            xt[Q * (kSLN + 1) + s] = w;
+            acc2[t] = acc;
+            wave_sync();
           }
-        });
-        });
-        wave_sync();
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < kSLN; ++m) {
-          if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
-          else acc += xt[s * (kSLN + 1) + m];
         }
-        acc2[t] = acc;
-        wave_sync();
-      }
+      };
+      if (use_acc) phase_a(std::true_type{});
+      else phase_a(std::false_type{});
       // ---- phase B: the adjoint, blocks and events last to first
 #pragma unroll
       for (int tt = 0; tt < NB; ++tt) {

@@ -140,9 +140,11 @@ def _event_scan_fwd(ctx, x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_activ
     dt_idle, dt_active = dt_idle.contiguous(), dt_active.contiguous()
     A, W_B, W_C = A.contiguous(), W_B.contiguous(), W_C.contiguous()
     chunk_g = selective_scan_cuda.chunk_states_buffer(x_ev, cu_seqlens, max_seqlen, A)
+    acc = torch.empty(x_ev.shape, dtype=torch.float32, device=x_ev.device)  # per-event state sums
     out, xs = selective_scan_cuda.fwd_flat_ch(x_ev, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, W_B, W_C, D,
-                                              None, is_depthwise_bc=True, _chunk_g=chunk_g, _trusted_seqlen=True)
-    ctx.chunk_g, ctx.max_seqlen, ctx.has_D = chunk_g, max_seqlen, D is not None
+                                              None, is_depthwise_bc=True, _chunk_g=chunk_g, _trusted_seqlen=True,
+                                              _acc=acc)
+    ctx.chunk_g, ctx.acc, ctx.max_seqlen, ctx.has_D = chunk_g, acc, max_seqlen, D is not None
     return out, [x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs] + ([D] if D is not None else [])
 
 
@@ -155,7 +157,7 @@ def _event_scan_bwd(ctx, saved, dout, rows=None):
     D = saved[9] if ctx.has_D else None
     res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, W_B, W_C,
                                           dout.contiguous(), xs, D, is_depthwise_bc=True, _chunk_g=ctx.chunk_g,
-                                          _rows=rows, _trusted_seqlen=True)
+                                          _rows=rows, _trusted_seqlen=True, _acc=ctx.acc)
     du, dA, dW_B, dW_C, ddt_idle, ddt_active = res[:6]
     return du, ddt_idle, ddt_active, dA, dW_B, dW_C, (res[6] if D is not None else None)
 

@@ -60,6 +60,7 @@ class FusedStep:
         self.k_buf = torch.empty(cap, **i32)
         self.u_buf = torch.empty(cap, dtype=w.dtype, device=dev)
         self.y_buf = torch.empty(cap, dtype=w.dtype, device=dev)
+        self.acc_buf = torch.empty(cap, dtype=torch.float32, device=dev)  # the forward's per-event state sums
         self.dy32_buf = torch.empty(cap, dtype=torch.float32, device=dev)
         self.dy_buf = self.dy32_buf if w.dtype == torch.float32 else torch.empty(cap, dtype=w.dtype, device=dev)
         self.du_buf = torch.empty(cap, dtype=w.dtype, device=dev)
@@ -82,6 +83,7 @@ class FusedStep:
         a.dt_idle, a.dt_active = w.dt_idle.data_ptr(), w.dt_active.data_ptr()
         a.A, a.W_B, a.W_C, a.D = w.A.data_ptr(), w.W_B.data_ptr(), w.W_C.data_ptr(), w.D_skip.data_ptr()
         a.out, a.x = self.y_buf.data_ptr(), self.x.data_ptr()
+        a.acc = self.acc_buf.data_ptr()  # written by the forward, read by the backward
         a.dout, a.x_saved, a.du = self.dy_buf.data_ptr(), self.x.data_ptr(), self.du_buf.data_ptr()
         a.dA, a.dW_B, a.dW_C, a.ddt_idle, a.ddt_active, a.dD = (g.data_ptr() for g in self.grads)
         return a

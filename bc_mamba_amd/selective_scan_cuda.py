@@ -135,6 +135,15 @@ class _SeqlenStatus:
                                "for the scan)")
 
 
+def _acc_ptr(fn, acc, u_flat):
+    """Device pointer of a per-event state-sum buffer (float32 [E]), or None."""
+    if acc is None:
+        return None
+    _check(acc.dtype == torch.float32 and acc.is_contiguous() and acc.numel() == u_flat.numel()
+           and acc.device == u_flat.device, f"{fn}: _acc must be a contiguous float32 (E,) tensor on u's device")
+    return acc.data_ptr()
+
+
 def _bc(mode, B, C, E, tile_offsets, tile_chunk_size, dB=None, dC=None):
     """bcm_scan_bc of the legacy / tiled modes. Legacy B/C are per event when
     their second dimension is E, else per model channel, as
@@ -197,13 +206,16 @@ def _args(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D
 
 def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D=None, z=None,
                 tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False, pw_B=None, pw_C=None, _chunk_g=None,
-                _trusted_seqlen=False):
+                _trusted_seqlen=False, _acc=None):
     """Flat per-channel scan forward -> [out, x] or [out, x, out_z]
     (selective_scan.cpp:674-884). x is [n_channels, n_chunks, 2*dstate]
     float32 holding, per 2048-event chunk and state, (prod of decays, h).
     `_chunk_g` (not in the reference signature): a float32 tensor from
     chunk_states_buffer() that receives the pass-start states, so that
-    bwd_flat_ch need not recompute them (depthwise mode).
+    bwd_flat_ch need not recompute them (depthwise mode). `_acc` (not in the
+    reference signature either): a float32 [E] tensor that receives the
+    per-event state sums Σ_s W_B W_C h/W_B, which bwd_flat_ch(_acc=...) then
+    reads instead of rebuilding them (depthwise mode).
     In depthwise mode the kernels report a channel longer than max_seqlen
     and this call raises RuntimeError (one host sync to read the report);
     `_trusted_seqlen=True` skips the report for callers whose max_seqlen
@@ -231,6 +243,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.out_z = out_z.data_ptr() if out_z is not None else None
         if mode == "depthwise":
             _nat.attach_chunk_g(a, _chunk_g)
+            a.acc = _acc_ptr(fn, _acc, u_flat)
             status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
             status.attach(a)
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
@@ -243,7 +256,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
-                pw_B=None, pw_C=None, _chunk_g=None, _rows=None, _trusted_seqlen=False):
+                pw_B=None, pw_C=None, _chunk_g=None, _rows=None, _trusted_seqlen=False, _acc=None):
     """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
     ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
     dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
@@ -253,6 +266,8 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     (bitmask, mask_row_div, tile_start, dx) of the extraction's event index
     and a contiguous [n_channels, L] tensor of u_flat's dtype, which also
     receives the gather backward of du (du at the events, 0 elsewhere).
+    `_acc`: the per-event state sums a fwd_flat_ch(_acc=...) of the same
+    inputs wrote (depthwise mode), read instead of rebuilt.
     As fwd_flat_ch, raises RuntimeError when a channel holds more than
     max_seqlen events (unless `_trusted_seqlen`)."""
     fn = "selective_scan_bwd_flat_ch"
@@ -325,6 +340,7 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 status.attach(f)
                 _nat.call("bcm_scan_fwd", f, s)
             _nat.attach_chunk_g(a, _chunk_g)
+            a.acc = _acc_ptr(fn, _acc, u_flat)
             split_bytes = int(_nat.lib().bcm_scan_bwd_workspace_bytes(a))
             split_ws = torch.empty(split_bytes // 4, dtype=torch.float32, device=dev) if split_bytes else None
             a.split_ws = split_ws.data_ptr() if split_ws is not None else None

@@ -47,13 +47,16 @@ class SelectiveScanFlatChFn(torch.autograd.Function):
             pw_B = pw_B.contiguous()
         if pw_C is not None:
             pw_C = pw_C.contiguous()
-        chunk_g = None
+        chunk_g = acc = None
         if is_depthwise_bc and tile_offsets is None:
             chunk_g = selective_scan_cuda.chunk_states_buffer(u_flat, cu_seqlens, max_seqlen, A)
+            # the per-event state sums, kept so the backward need not rebuild them
+            acc = torch.empty(u_flat.shape, dtype=torch.float32, device=u_flat.device)
         result = selective_scan_cuda.fwd_flat_ch(
             u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, D, z,
-            tile_offsets, tile_chunk_size, is_depthwise_bc, pw_B, pw_C, _chunk_g=chunk_g)
-        ctx.chunk_g = chunk_g  # pass-start states for the backward (not an autograd input)
+            tile_offsets, tile_chunk_size, is_depthwise_bc, pw_B, pw_C, _chunk_g=chunk_g, _acc=acc)
+        # pass-start states and state sums for the backward (not autograd inputs)
+        ctx.chunk_g, ctx.acc = chunk_g, acc
         out_flat, x = result[0], result[1]
         ctx.has_z, ctx.has_D, ctx.has_pw = z is not None, D is not None, pw_B is not None
         ctx.max_seqlen = max_seqlen
@@ -96,7 +99,7 @@ class SelectiveScanFlatChFn(torch.autograd.Function):
             result = selective_scan_cuda.bwd_flat_ch(
                 u_flat, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, B, C, dout.contiguous(), x,
                 D, z, out_flat, tile_offsets, ctx.tile_chunk_size, ctx.is_depthwise_bc, pw_B, pw_C,
-                _chunk_g=ctx.chunk_g, _trusted_seqlen=True)  # the forward checked max_seqlen
+                _chunk_g=ctx.chunk_g, _trusted_seqlen=True, _acc=ctx.acc)  # the forward checked max_seqlen
         du, dA, dW_B, dW_C, ddt_idle, ddt_active = result[:6]
         ridx = 6
         dD = dz = dpw_B = dpw_C = None

@@ -268,6 +268,13 @@ typedef struct bcm_scan_args {
    * a stale chunk count, selective_scan.cpp:1009-1014). Ignored when chunk_g
    * is NULL. */
   int32_t chunk_g_pass;
+  /* Optional (NULL: not used) [E] float32, depthwise mode: the forward's
+   * per-event state sum acc_i = sum_s W_B[d,s] W_C[d,s] g_i,s (so that
+   * y_i = D u_i + u_i acc_i, with g = h / W_B). A forward given it writes
+   * it; a backward given it reads it instead of rebuilding the sums from
+   * the saved states (the caller hands the backward what the forward of the
+   * same inputs wrote). No counterpart in the reference, which recomputes. */
+  float* acc;
 } bcm_scan_args;
 
 #define BCM_SCAN_SEQLEN_EXCEEDED 1

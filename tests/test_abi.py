@@ -48,8 +48,8 @@ def test_library_exports_every_header_symbol(lib):
 def test_scan_args_layout_matches_header():
     assert [f for f, _ in nat.ScanArgs._fields_] == header_struct_fields()
     # 1 int64 + 6 int32 (= 32 bytes incl. no padding) + 27 pointers + 2 int64 sizes + int32 chunk_g_pass
-    # (padded to the struct's 8-byte alignment)
-    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 27 * 8 + 2 * 8 + 8
+    # (padded to 8 bytes for the next pointer) + the acc pointer
+    assert ctypes.sizeof(nat.ScanArgs) == 8 + 6 * 4 + 27 * 8 + 2 * 8 + 8 + 8
 
 
 def test_scan_bc_layout_matches_header():

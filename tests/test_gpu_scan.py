@@ -44,13 +44,16 @@ def _case(B, D, L, p, N, dtype, seed, with_z=False, with_D=True, empty_every=0, 
     return dict(ch=ch, t=t, k=k, cu=cu, ms=ms, u=u, dout=dout, z=z, dt_i=dt_i, dt_a=dt_a, A=A, WB=WB, WC=WC, D=Dv)
 
 
-def _run_and_check(c, dtype, dev):
+def _run_and_check(c, dtype, dev, use_acc=False):
+    """Forward and backward through the raw API against the oracle; use_acc:
+    the forward keeps its per-event state sums and the backward reads them."""
     f32 = lambda x: None if x is None else x.float().numpy()
     cud = lambda x: None if x is None else x.to(dev)
     k_t = torch.from_numpy(c["k"]).to(dev)
     cu_t = torch.from_numpy(c["cu"]).to(dev)
     args = (cud(c["u"]), k_t, cu_t, c["ms"], cud(c["dt_i"]), cud(c["dt_a"]), cud(c["A"]), cud(c["WB"]), cud(c["WC"]))
-    res = ssc.fwd_flat_ch(*args, D=cud(c["D"]), z=cud(c["z"]), is_depthwise_bc=True)
+    acc = torch.empty(len(c["k"]), dtype=torch.float32, device=dev) if use_acc else None
+    res = ssc.fwd_flat_ch(*args, D=cud(c["D"]), z=cud(c["z"]), is_depthwise_bc=True, _acc=acc)
     ref = orc.scan_fwd(f32(c["u"]), c["k"], c["cu"], c["ms"], f32(c["dt_i"]), f32(c["dt_a"]), f32(c["A"]),
                        f32(c["WB"]), f32(c["WC"]), f32(c["D"]), f32(c["z"]))
     rtol, atol = TOL[dtype]
@@ -60,7 +63,7 @@ def _run_and_check(c, dtype, dev):
     if c["z"] is not None:
         assert_close(res[2].float().cpu(), ref[2], rtol, atol, "out_z")
     gb = ssc.bwd_flat_ch(*args, cud(c["dout"]), res[1], D=cud(c["D"]), z=cud(c["z"]),
-                         out=res[0] if c["z"] is not None else None, is_depthwise_bc=True)
+                         out=res[0] if c["z"] is not None else None, is_depthwise_bc=True, _acc=acc)
     # the backward's z-gate reads the stored (rounded) forward output
     out_used = res[0].float().cpu().numpy() if c["z"] is not None else None
     gref = orc.scan_bwd(f32(c["u"]), c["k"], c["cu"], c["ms"], f32(c["dt_i"]), f32(c["dt_a"]), f32(c["A"]),
@@ -146,12 +149,15 @@ def test_scan_clamped_decays(cuda_device):
 
 @pytest.mark.parametrize("N", [16, 32, 64])
 @pytest.mark.parametrize("with_z", [False, True])
-def test_scan_states_per_lane(cuda_device, N, with_z):
+@pytest.mark.parametrize("use_acc", [False, True])
+def test_scan_states_per_lane(cuda_device, N, with_z, use_acc):
     """One, two and four states per lane of the state-lane kernels (dstate
     16, 32, 64; the lane groups under the other family): z gate, clamped
-    long-gap decays past the table (sparse channels) and gaps within it."""
+    long-gap decays past the table (sparse channels) and gaps within it;
+    the backward rebuilding the per-event state sums or reading the
+    forward's (use_acc: written by either family's forward)."""
     c = _case(2, 8, 1500, 0.15, N, torch.float32, seed=40 + N, with_z=with_z, p_short=0.01, long_every=3)
-    _run_and_check(c, torch.float32, cuda_device)
+    _run_and_check(c, torch.float32, cuda_device, use_acc=use_acc)
 
 
 @pytest.mark.parametrize("N", [16, 32, 64])
@@ -181,14 +187,17 @@ def test_autograd_function_matches_raw(cuda_device):
                                            is_depthwise_bc=True)
     assert not x.requires_grad
     out.backward(c["dout"].to(dev))
+    # the autograd function keeps the forward's state sums for its backward:
+    # the raw calls do the same
+    acc = torch.empty(len(c["k"]), dtype=torch.float32, device=dev)
     raw = ssc.fwd_flat_ch(*(leaves[n].detach() for n in ("u",)), k_t, cu_t, c["ms"],
                           *(leaves[n].detach() for n in ("dt_i", "dt_a", "A", "WB", "WC")),
-                          D=leaves["D"].detach(), z=leaves["z"].detach(), is_depthwise_bc=True)
+                          D=leaves["D"].detach(), z=leaves["z"].detach(), is_depthwise_bc=True, _acc=acc)
     assert torch.equal(out.detach(), raw[2])
     gb = ssc.bwd_flat_ch(leaves["u"].detach(), k_t, cu_t, c["ms"],
                          *(leaves[n].detach() for n in ("dt_i", "dt_a", "A", "WB", "WC")),
                          c["dout"].to(dev), raw[1], D=leaves["D"].detach(), z=leaves["z"].detach(), out=raw[0],
-                         is_depthwise_bc=True)
+                         is_depthwise_bc=True, _acc=acc)
     for name, g in zip(("u", "A", "WB", "WC", "dt_i", "dt_a", "D", "z"), (gb[0], gb[1], gb[2], gb[3], gb[4], gb[5],
                                                                          gb[6], gb[7])):
         assert torch.equal(leaves[name].grad, g), name
@@ -223,8 +232,10 @@ def test_scan_multipass_chunk_states(cuda_device, B, D, L, p, ps, le, N):
     pass_len, n_pass, needs = ssc._nat.scan_chunking(a)
     assert needs and pass_len < 2048 and n_pass > 1
     # direct API: the backward recomputes the pass states
-    _, gb_direct = _run_and_check(c, torch.float32, cuda_device)
-    # autograd: the forward's pass states are kept for the backward
+    _run_and_check(c, torch.float32, cuda_device)
+    # ... and reading the forward's state sums, as the autograd function does
+    _, gb_direct = _run_and_check(c, torch.float32, cuda_device, use_acc=True)
+    # autograd: the forward's pass states (and state sums) are kept for the backward
     dev = cuda_device
     leaves = {n: c[n].to(dev).requires_grad_(True) for n in ("u", "dt_i", "dt_a", "A", "WB", "WC", "D", "z")}
     k_t, cu_t = torch.from_numpy(c["k"]).to(dev), torch.from_numpy(c["cu"]).to(dev)

@@ -63,17 +63,21 @@ def _expanded_case(B, D, L, p, N, dtype, seed, with_z, p_short, expand):
 
 
 @pytest.mark.parametrize("B,D,L,p,N,dtype,with_z,ps", CASES)
-@pytest.mark.parametrize("expand", [1, 2])
-def test_scan_bwd_rows_matches_scan_then_gather(cuda_device, B, D, L, p, N, dtype, with_z, ps, expand):
-    print(f"scan_bwd_rows case B={B} D={D} L={L} p={p}/{ps} N={N} {dtype} z={with_z} expand={expand}", flush=True)
+@pytest.mark.parametrize("expand,use_acc", [(1, False), (2, False), (1, True)])
+def test_scan_bwd_rows_matches_scan_then_gather(cuda_device, B, D, L, p, N, dtype, with_z, ps, expand, use_acc):
+    """bcm_scan_bwd_rows equals bcm_scan_bwd followed by the gather backward,
+    bit for bit (and with the forward's per-event state sums read by both)."""
+    print(f"scan_bwd_rows case B={B} D={D} L={L} p={p}/{ps} N={N} {dtype} z={with_z} expand={expand} "
+          f"acc={use_acc}", flush=True)
     dev = cuda_device
     c = _expanded_case(B, D, L, p, N, dtype, L + N + expand, with_z, ps, expand)
     NC = B * D
     cud = lambda x: None if x is None else x.to(dev)
     k_t, cu_t = torch.from_numpy(c["k"]).to(dev), torch.from_numpy(c["cu"]).to(dev)
     args = (cud(c["u"]), k_t, cu_t, c["ms"], cud(c["dt_i"]), cud(c["dt_a"]), cud(c["A"]), cud(c["WB"]), cud(c["WC"]))
-    res = ssc.fwd_flat_ch(*args, D=cud(c["D"]), z=cud(c["z"]), is_depthwise_bc=True)
-    kw = dict(D=cud(c["D"]), z=cud(c["z"]), out=res[0] if with_z else None, is_depthwise_bc=True)
+    acc = torch.empty(len(c["k"]), dtype=torch.float32, device=dev) if use_acc else None
+    res = ssc.fwd_flat_ch(*args, D=cud(c["D"]), z=cud(c["z"]), is_depthwise_bc=True, _acc=acc)
+    kw = dict(D=cud(c["D"]), z=cud(c["z"]), out=res[0] if with_z else None, is_depthwise_bc=True, _acc=acc)
     g_plain = ssc.bwd_flat_ch(*args, cud(c["dout"]), res[1], **kw)
     bitmask, tile_start = _index(c, NC, L, dev, expand)
     dx = torch.full((NC, L), float("nan"), dtype=dtype, device=dev)  # every element must be written
