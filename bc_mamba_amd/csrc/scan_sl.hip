@@ -127,13 +127,18 @@ __device__ __forceinline__ void tab16(float (&av)[NL][16], const float* sT, uint
 // s_nop 1 of the first add covers the source's last write; the hazard check
 // over the built assembly (tests/test_dpp_hazards.py) keeps it honest.
 // One event's table address: tb of lane Q of the row plus the lane's row base.
+// volatile: the adds of a range keep their order, so the first (with the
+// s_nop) stays first after tb's write. Without it the scheduler may move a
+// later add ahead of it: a DPP read two wait states early, whose result
+// varies with the other waves' timing (seen in a loop of another shape).
 template <int Q, bool NOP> __device__ __forceinline__ uint32_t tab_addr(uint32_t tb, uint32_t rowb) {
   uint32_t o;
   if constexpr (NOP)
-    asm("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-        : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
+    asm volatile("s_nop 1\n\tv_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
   else
-    asm("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
+    asm volatile("v_add_u32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "=&v"(o) : "v"(tb), "v"(rowb), "n"(Q));
   return o;
 }
 template <int NL, int Q0, int NQ, int... Q>

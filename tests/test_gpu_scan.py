@@ -268,6 +268,67 @@ def test_scan_split_workgroups(cuda_device, B, D, L, p, ps, N):
     assert all(torch.equal(x, y) for x, y in zip(g1, g2))  # deterministic
 
 
+@pytest.mark.parametrize("B,D,L,p,ps,N,dtype,markov,dim", [
+    (64, 2, 1200, 0.6, 0.02, 16, torch.float32, False, None),  # split workgroups, 24-pass channels
+    (64, 2, 1200, 0.6, 0.02, 64, torch.float32, False, None),  # four states per lane: 48-pass channels
+    (40, 3, 900, 0.5, 0.02, 32, torch.float32, False, None),   # two states per lane, rounds not filled
+    (64, 2, 1500, 0.5, 0.01, 16, torch.bfloat16, False, None),
+    (48, 5, 1700, 0.0, 0.0, 16, torch.float32, True, None),    # Markov bursts: gaps past the decay table
+    (48, 5, 1700, 0.0, 0.0, 64, torch.float32, True, None),
+    (37, 4, 1300, 0.7, 0.03, 16, torch.float32, False, 5),     # 148 channels on 5 model channels (30 / 29 each)
+])
+def test_scan_bursty_ranked(cuda_device, B, D, L, p, ps, N, dtype, markov, dim):
+    """Bursty streams with many channels per model channel: the state lanes
+    rank the channels by length (the longest more than twice the mean) and
+    split each model channel over workgroups. Parity against the oracle
+    (forward, backward with and without the forward's state sums), Markov
+    bursts with gaps past the decay table, a channel count that the model
+    channels do not divide, and determinism."""
+    print(f"bursty ranked case B={B} D={D} L={L} p={p}/{ps} N={N} {dtype} markov={markov} dim={dim}", flush=True)
+    if markov:  # config 3's event law at a smaller size
+        from bc_mamba_amd.workloads import _markov_events
+        g = torch.Generator().manual_seed(B * L + N)
+        mem = _markov_events(g, B * D, L).view(B, D, L).float()
+        ch, t, k, cu, _, ms = orc.extract_base_events(mem.numpy(), 0.5)
+        assert int(k.max()) > 256  # gaps past the decay table (computed decays)
+        E = len(ch)
+        c = dict(ch=ch, t=t, k=k, cu=cu, ms=ms, u=torch.randn(E, generator=g).to(dtype),
+                 dout=torch.randn(E, generator=g).to(dtype), z=None,
+                 dt_i=torch.nn.functional.softplus(torch.randn(D, generator=g) - 2.0),
+                 dt_a=torch.nn.functional.softplus(torch.randn(D, generator=g) - 2.0),
+                 A=-torch.exp(torch.rand(D, N, generator=g) * math.log(16.0)),
+                 WB=torch.randn(D, N, generator=g) / math.sqrt(N), WC=torch.randn(D, N, generator=g) / math.sqrt(N),
+                 D=torch.randn(D, generator=g))
+    else:
+        c = _case(B, D, L, p, N, dtype, seed=B + L + N, p_short=ps, dim=dim)
+    NC, E, ms = B * D, len(c["ch"]), int(c["ms"])
+    assert 2 * E < ms * NC  # bursty: the state lanes rank the channels
+    _, g1 = _run_and_check(c, dtype, cuda_device)
+    _run_and_check(c, dtype, cuda_device, use_acc=True)
+    _, g2 = _run_and_check(c, dtype, cuda_device)
+    assert all(torch.equal(x, y) for x, y in zip(g1, g2))  # deterministic
+
+
+@pytest.mark.parametrize("N", [16, 64])
+def test_scan_ranked_understated_max_seqlen(cuda_device, N):
+    """A ranked, split backward under a max_seqlen of half the longest
+    channel: every write stays inside the buffers sized from max_seqlen and
+    the status word makes the entry point raise."""
+    c = _case(64, 2, 1200, 0.6, N, torch.float32, seed=13, p_short=0.02, long_every=8)
+    ms = int(c["ms"]) // 2
+    NC, E = 128, len(c["ch"])
+    assert 2 * E < ms * NC
+    print(f"ranked seqlen status case: max_seqlen {ms} for channels of up to {int(c['ms'])} events", flush=True)
+    dev = cuda_device
+    cud = lambda x: x.to(dev)
+    k_t, cu_t = torch.from_numpy(c["k"]).to(dev), torch.from_numpy(c["cu"]).to(dev)
+    args = (cud(c["u"]), k_t, cu_t, ms, cud(c["dt_i"]), cud(c["dt_a"]), cud(c["A"]), cud(c["WB"]), cud(c["WC"]))
+    x = torch.zeros((NC, ssc.n_chunks_for(ms), 2 * N), device=dev)
+    with pytest.raises(RuntimeError, match="more than max_seqlen"):
+        ssc.bwd_flat_ch(*args, cud(c["dout"]), x, D=cud(c["D"]), is_depthwise_bc=True)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("N", [16, 64])
 @pytest.mark.parametrize("true_ms_scale", [3, 1])
 def test_scan_reports_understated_max_seqlen(cuda_device, true_ms_scale, N):
