@@ -39,7 +39,8 @@ constexpr int kPT = 64;          // output tile edge
 constexpr int kKC = 32;          // contraction chunk (16 MFMA steps)
 constexpr int kRS = kKC + 4;     // LDS row stride of an operand chunk (16-byte rows, conflict-free 16-byte reads)
 constexpr int kDS = kPT + 1;     // LDS row stride of a dz tile
-constexpr int kSeg = 1024;       // sequence steps per dW partial
+constexpr int kSeg = 512;        // sequence steps per dW partial (1600 items at a config-4 layer)
+static_assert(kSeg % 64 == 0, "a dW segment starts a 64-step tile");
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -503,34 +504,36 @@ __global__ __launch_bounds__(256) void k_restore_proj_fwd_dma(const float* __res
 }
 
 // ----------------------------------------------------------- dW partials
-// Item (p = b * nSeg + seg, nb, db): rows n0 = 64 nb .. of dW, channels
+// Item (p = b * nSeg + seg, nb, db): rows n0 = 128 nb .. of dW, channels
 // d0 = 64 db .., the steps of segment seg of sequence b in 32-step chunks.
-// Wave w: W rows 32 (w & 1), channels 32 (w >> 1). Per chunk, dOut
+// Wave w: W rows 32 w, all 64 channels in two accumulators (two
+// independent MFMA chains per wave, 32 MFMAs per chunk). Per chunk, dOut
 // (transposed to [row of W][step] on its way to LDS) and z ([channel][step],
 // lane = step: each gather reads one channel's events, two channels per
 // instruction) are staged in LDS, so both operand runs (along the steps)
-// are 16-byte LDS reads.
+// are 16-byte LDS reads; z is gathered once per 128 rows of W.
+constexpr int kPTW = 128;  // rows of W per dW item
 __global__ __launch_bounds__(256) void k_restore_proj_dw(const float* __restrict__ dout,
                                                          const float* __restrict__ y, int64_t n_events,
                                                          const uint32_t* __restrict__ bitmask, int64_t Wd,
                                                          int64_t mrd, const int32_t* __restrict__ tile_start,
                                                          int nT, int dim, int L, int dm, int nNB, int nDB,
                                                          int nSeg, float* __restrict__ part) {
-  __shared__ float4 s_ab[2 * 2 * kPT * kRS / 4];
-  float* sA = reinterpret_cast<float*>(s_ab);  // [2][64][kRS]: dOut chunk [row of W][step]
-  float* sZ = sA + 2 * kPT * kRS;              // [2][64][kRS]: z chunk [channel][step]
+  __shared__ float4 s_ab[2 * (kPTW + kPT) * kRS / 4];
+  float* sA = reinterpret_cast<float*>(s_ab);  // [2][128][kRS]: dOut chunk [row of W][step]
+  float* sZ = sA + 2 * kPTW * kRS;             // [2][64][kRS]: z chunk [channel][step]
   const int item = xcd_block(blockIdx.x, gridDim.x);
   const int db = item % nDB, r1 = item / nDB;
   const int nb = r1 % nNB, p = r1 / nNB;
   const int seg = p % nSeg, b = p / nSeg;
-  const int n0 = nb * kPT, d0 = db * kPT;
+  const int n0 = nb * kPTW, d0 = db * kPT;
   const int tid = threadIdx.x, lane = lane_id();
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int rb = 32 * (w & 1), cb = 32 * (w >> 1);
+  const int rb = 32 * w;
   const int li = lane & 31, h = lane >> 5;
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + (int64_t)b * L * dm, (int64_t)L * dm * 4);
   const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y, n_events * 4);
-  // dOut: step (tid >> 6) + 4 i of the chunk, row n0 + (tid & 63)
+  // dOut: step (tid >> 6) + 4 i of the chunk, rows n0 + (tid & 63) and + 64
   const int an = tid & 63, at = tid >> 6;
   // z: lane step li, channels d0 + 32 h + 8 w + q
   int32_t zfirst[8];
@@ -546,49 +549,74 @@ __global__ __launch_bounds__(256) void k_restore_proj_dw(const float* __restrict
     zts[q] = tile_start + ch * (nT + 1);
     zfirst[q] = zts[q][0];
   }
-  float ar_[8], zr[8];
-  auto load = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = t0 + at + 4 * i;
-      ar_[i] = buf_load<float>(rg, (t < L && n0 + an < dm) ? (uint32_t)(t * dm + n0 + an) * 4u : kBufOOB);
-    }
-    const int jt = t0 >> 6, so = (t0 & 63) + li;  // the chunk's 32 steps lie in tile jt
+  // the index words (tile mask, first event at or after the tile) of the
+  // current 64-step tile and of the next one, fetched a tile ahead, so a
+  // chunk's gathers of y wait for no index load of their own (the next
+  // tile's row is clamped at the last tile: in range, unused)
+  uint64_t mcur[8], mnxt[8];
+  int32_t tcur[8], tnxt[8];
+  auto index_words = [&](int jt) {
+    const int jc = min(jt, nT - 1);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const uint64_t m = zok[q] ? tile_mask(zmrow[q], jt) : 0ull;
-      zr[q] = buf_load<float>(ry, zoh_off(m, so, zts[q][jt], zfirst[q], zok[q]));
+      mnxt[q] = zok[q] ? tile_mask(zmrow[q], jc) : 0ull;
+      tnxt[q] = zts[q][jc];
     }
   };
+  float ar_[16], zr[8];
+  auto load = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = t0 + at + 4 * (i & 7), n = n0 + an + 64 * (i >> 3);
+      ar_[i] = buf_load<float>(rg, (t < L && n < dm) ? (uint32_t)(t * dm + n) * 4u : kBufOOB);
+    }
+    const int jt = t0 >> 6, so = (t0 & 63) + li;  // the chunk's 32 steps lie in tile jt
+    if ((t0 & 63) == 0) {  // the first chunk of tile jt: its words are in, the next tile's go out
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        mcur[q] = mnxt[q];
+        tcur[q] = tnxt[q];
+      }
+      index_words(jt + 1);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) zr[q] = buf_load<float>(ry, zoh_off(mcur[q], so, tcur[q], zfirst[q], zok[q]));
+  };
   const int tb = seg * kSeg, te = min(L, tb + kSeg);
-  f32x16 acc = {};
+  f32x16 acc0 = {}, acc1 = {};
+  index_words(tb >> 6);  // a segment starts a tile (kSeg % 64 == 0)
   load(tb);
   for (int t0 = tb, c = 0; t0 < te; t0 += kKC, ++c) {
-    float* ab = sA + (c & 1) * kPT * kRS;
+    float* ab = sA + (c & 1) * kPTW * kRS;
     float* zb = sZ + (c & 1) * kPT * kRS;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ab[an * kRS + at + 4 * i] = ar_[i];
+    for (int i = 0; i < 16; ++i) ab[(an + 64 * (i >> 3)) * kRS + at + 4 * (i & 7)] = ar_[i];
 #pragma unroll
     for (int q = 0; q < 8; ++q) zb[(32 * h + 8 * w + q) * kRS + li] = zr[q];
     __syncthreads();
     if (t0 + kKC < te) load(t0 + kKC);
     const float4* aa = reinterpret_cast<const float4*>(ab + (rb + li) * kRS + 16 * h);
-    const float4* za = reinterpret_cast<const float4*>(zb + (cb + li) * kRS + 16 * h);
+    const float4* za0 = reinterpret_cast<const float4*>(zb + li * kRS + 16 * h);
+    const float4* za1 = reinterpret_cast<const float4*>(zb + (32 + li) * kRS + 16 * h);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const float4 a = aa[v], bq = za[v];
-      acc = mfma32(a.x, bq.x, acc);
-      acc = mfma32(a.y, bq.y, acc);
-      acc = mfma32(a.z, bq.z, acc);
-      acc = mfma32(a.w, bq.w, acc);
+      const float4 a = aa[v], b0 = za0[v], b1 = za1[v];
+      acc0 = mfma32(a.x, b0.x, acc0);
+      acc1 = mfma32(a.x, b1.x, acc1);
+      acc0 = mfma32(a.y, b0.y, acc0);
+      acc1 = mfma32(a.y, b1.y, acc1);
+      acc0 = mfma32(a.z, b0.z, acc0);
+      acc1 = mfma32(a.z, b1.z, acc1);
+      acc0 = mfma32(a.w, b0.w, acc0);
+      acc1 = mfma32(a.w, b1.w, acc1);
     }
   }
   float* pp = part + (int64_t)p * dm * dim;
-  const int dc = d0 + cb + li;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int nr = n0 + rb + acc_row(r, h);
-    if (nr < dm && dc < dim) pp[(int64_t)nr * dim + dc] = acc[r];
+    if (nr < dm && d0 + li < dim) pp[(int64_t)nr * dim + d0 + li] = acc0[r];
+    if (nr < dm && d0 + 32 + li < dim) pp[(int64_t)nr * dim + d0 + 32 + li] = acc1[r];
   }
 }
 
@@ -609,7 +637,7 @@ __global__ __launch_bounds__(256) void k_restore_proj_dw_sum(const float* __rest
 }
 
 struct ProjShape {
-  int64_t W, nT, nNB, nDB, nSeg, n_parts;
+  int64_t W, nT, nNB, nNBW, nDB, nSeg, n_parts;
 };
 
 static ProjShape proj_shape(int64_t n_rows, int64_t dim, int64_t L, int64_t dm) {
@@ -617,6 +645,7 @@ static ProjShape proj_shape(int64_t n_rows, int64_t dim, int64_t L, int64_t dm) 
   s.W = bitmask_words(L);
   s.nT = tile_count(L);
   s.nNB = (dm + kPT - 1) / kPT;
+  s.nNBW = (dm + kPTW - 1) / kPTW;
   s.nDB = (dim + kPT - 1) / kPT;
   s.nSeg = (L + kSeg - 1) / kSeg;
   s.n_parts = (n_rows / dim) * s.nSeg;
@@ -725,9 +754,9 @@ int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events, co
   }
   if (dweight) {  // no tokens (n_parts = 0): the sum writes dW = 0
     if (s.n_parts > 0)
-      hipLaunchKernelGGL(k_restore_proj_dw, dim3((unsigned)(s.n_parts * s.nNB * s.nDB)), dim3(256), 0, st, dout, y,
+      hipLaunchKernelGGL(k_restore_proj_dw, dim3((unsigned)(s.n_parts * s.nNBW * s.nDB)), dim3(256), 0, st, dout, y,
                        n_events, bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, (int)d_model,
-                       (int)s.nNB, (int)s.nDB, (int)s.nSeg, part);
+                       (int)s.nNBW, (int)s.nDB, (int)s.nSeg, part);
     if ((rc = check_launch(fn))) return rc;
     const int64_t count = d_model * dim;
     hipLaunchKernelGGL(k_restore_proj_dw_sum, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, part,
