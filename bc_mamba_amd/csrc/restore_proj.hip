@@ -620,9 +620,133 @@ __global__ __launch_bounds__(256) void k_restore_proj_dw(const float* __restrict
   }
 }
 
+// dW by LDS DMA (d_model % 128 == 0, L % 32 == 0: every DMA row is a
+// whole 512-byte run of one step of dOut inside the sequence). The
+// transposed product dW^T[d][n] = sum_t z[t][d] dOut[t][n]: z is the MFMA A
+// operand ([channel][step] in LDS, 16-byte reads along the steps, as
+// above) and dOut the B operand in its own [step][n] layout, brought into
+// LDS by global_load_lds_dwordx4 (no register staging, no transposing
+// stores), one 4-byte read per MFMA step. Item (p, nb, db): n0 = 128 nb,
+// d0 = 64 db; wave w: n block 32 w, channel blocks 0 and 1 (two chains).
+// A chunk's 32 dOut rows sit in row pairs of kDwPair floats (two 512-byte
+// rows and 16 bytes of padding): the lane halves read rows 16 apart, 8 row
+// pairs = 2080 floats apart, on opposite halves of the 64 banks. The
+// partials are laid out [p][d][n] (lanes write consecutive n).
+constexpr int kDwPair = 2 * kPTW + 4;  // floats per dOut row pair in LDS
+__global__ __launch_bounds__(256) void k_restore_proj_dw_dma(const float* __restrict__ dout,
+                                                             const float* __restrict__ y, int64_t n_events,
+                                                             const uint32_t* __restrict__ bitmask, int64_t Wd,
+                                                             int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                             int nT, int dim, int L, int dm, int nNB, int nDB,
+                                                             int nSeg, float* __restrict__ part) {
+  __shared__ float4 s_dw[(2 * (kKC / 2) * kDwPair + 2 * kPT * kRS) / 4];
+  float* sB = reinterpret_cast<float*>(s_dw);    // [2][16 row pairs][kDwPair]: dOut chunk [step][n]
+  float* sZ = sB + 2 * (kKC / 2) * kDwPair;      // [2][64][kRS]: z chunk [channel][step]
+  const int item = xcd_block(blockIdx.x, gridDim.x);
+  const int db = item % nDB, r1 = item / nDB;
+  const int nb = r1 % nNB, p = r1 / nNB;
+  const int seg = p % nSeg, b = p / nSeg;
+  const int n0 = nb * kPTW, d0 = db * kPT;
+  const int tid = threadIdx.x, lane = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int li = lane & 31, h = lane >> 5;
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y, n_events * 4);
+  // z: lane step li, channels d0 + 32 h + 8 w + q
+  int32_t zfirst[8];
+  const int32_t* zts[8];
+  const uint32_t* zmrow[8];
+  bool zok[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int d = d0 + 32 * h + 8 * w + q;
+    zok[q] = d < dim;
+    const int64_t ch = (int64_t)b * dim + (zok[q] ? d : dim - 1);
+    zmrow[q] = bitmask + (ch / mrd) * Wd;
+    zts[q] = tile_start + ch * (nT + 1);
+    zfirst[q] = zts[q][0];
+  }
+  uint64_t mcur[8], mnxt[8];
+  int32_t tcur[8], tnxt[8];
+  auto index_words = [&](int jt) {  // a tile ahead, as in k_restore_proj_dw
+    const int jc = min(jt, nT - 1);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      mnxt[q] = zok[q] ? tile_mask(zmrow[q], jc) : 0ull;
+      tnxt[q] = zts[q][jc];
+    }
+  };
+  float zr[8];
+  auto gather = [&](int t0) {
+    const int jt = t0 >> 6, so = (t0 & 63) + li;
+    if ((t0 & 63) == 0) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        mcur[q] = mnxt[q];
+        tcur[q] = tnxt[q];
+      }
+      index_words(jt + 1);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) zr[q] = buf_load<float>(ry, zoh_off(mcur[q], so, tcur[q], zfirst[q], zok[q]));
+  };
+  // wave w brings row pairs 4 w .. 4 w + 3 of the chunk: lane l takes 16
+  // bytes of row 2 pp + (l >> 5) at n0 + 4 (l & 31)
+  const float* gd = dout + (int64_t)b * L * dm + n0 + 4 * li;
+  auto dma = [&](int t0, int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pp = 4 * w + i;
+      lds_dma16(gd + (int64_t)(t0 + 2 * pp + h) * dm, lds_off(sB + (st * (kKC / 2) + pp) * kDwPair));
+    }
+  };
+  const int tb = seg * kSeg, te = min(L, tb + kSeg);
+  f32x16 acc0 = {}, acc1 = {};
+  index_words(tb >> 6);
+  dma(tb, 0);
+  gather(tb);
+  for (int t0 = tb, c = 0; t0 < te; t0 += kKC, ++c) {
+    const int st = c & 1;
+    float* zb = sZ + st * kPT * kRS;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) zb[(32 * h + 8 * w + q) * kRS + li] = zr[q];
+    wait_vmcnt0();  // this wave's dOut rows of chunk c have landed
+    __syncthreads();
+    if (t0 + kKC < te) {
+      dma(t0 + kKC, st ^ 1);
+      gather(t0 + kKC);
+    }
+    const float* bl = sB + st * (kKC / 2) * kDwPair + h * 8 * kDwPair + 32 * w + li;
+    const float4* za0 = reinterpret_cast<const float4*>(zb + li * kRS + 16 * h);
+    const float4* za1 = reinterpret_cast<const float4*>(zb + (32 + li) * kRS + 16 * h);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float4 a0 = za0[v], a1 = za1[v];
+      const float a0v[4] = {a0.x, a0.y, a0.z, a0.w}, a1v[4] = {a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sidx = 4 * v + e;  // MFMA step: steps 16 h + sidx of the chunk
+        const float bv = bl[(sidx >> 1) * kDwPair + (sidx & 1) * kPTW];
+        acc0 = mfma32(a0v[e], bv, acc0);
+        acc1 = mfma32(a1v[e], bv, acc1);
+      }
+    }
+  }
+  float* pp = part + (int64_t)p * dm * dim;
+  const int n = n0 + 32 * w + li;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int dr = d0 + acc_row(r, h);
+    if (dr < dim) pp[(int64_t)dr * dm + n] = acc0[r];
+    if (dr + 32 < dim) pp[(int64_t)(dr + 32) * dm + n] = acc1[r];
+  }
+}
+
 // dW = sum of the partials in partial order.
+// dmajor: partials laid out [p][d][n] (the DMA form); the thread of partial
+// element i (consecutive i: coalesced reads) writes dW[n][d].
 __global__ __launch_bounds__(256) void k_restore_proj_dw_sum(const float* __restrict__ part, int64_t n_parts,
-                                                             int64_t count, float* __restrict__ dw) {
+                                                             int64_t count, int dm, int dim, int dmajor,
+                                                             float* __restrict__ dw) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= count) return;
   float v = 0.0f;
@@ -633,7 +757,7 @@ __global__ __launch_bounds__(256) void k_restore_proj_dw_sum(const float* __rest
     v = (((v + a0) + a1) + a2) + a3;
   }
   for (; q < n_parts; ++q) v += part[q * count + i];
-  dw[i] = v;
+  dw[dmajor ? (i % dm) * dim + i / dm : i] = v;
 }
 
 struct ProjShape {
@@ -753,14 +877,22 @@ int bcm_restore_proj_bwd(const float* dout, const float* y, int64_t n_events, co
     if ((rc = restore_bwd_fix(s.nT, n_rows, head, tail, tend, dy, n_events, st, fn))) return rc;
   }
   if (dweight) {  // no tokens (n_parts = 0): the sum writes dW = 0
-    if (s.n_parts > 0)
-      hipLaunchKernelGGL(k_restore_proj_dw, dim3((unsigned)(s.n_parts * s.nNBW * s.nDB)), dim3(256), 0, st, dout, y,
-                       n_events, bitmask, s.W, mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, (int)d_model,
-                       (int)s.nNBW, (int)s.nDB, (int)s.nSeg, part);
+    // the LDS-DMA form where every dOut row it brings is a whole 512-byte
+    // run inside the sequence
+    const bool dma = d_model % kPTW == 0 && L % kKC == 0;
+    const dim3 grid((unsigned)(s.n_parts * s.nNBW * s.nDB));
+    if (s.n_parts > 0 && dma)
+      hipLaunchKernelGGL(k_restore_proj_dw_dma, grid, dim3(256), 0, st, dout, y, n_events, bitmask, s.W,
+                         mask_row_div, tile_start, (int)s.nT, (int)dim, (int)L, (int)d_model, (int)s.nNBW,
+                         (int)s.nDB, (int)s.nSeg, part);
+    else if (s.n_parts > 0)
+      hipLaunchKernelGGL(k_restore_proj_dw, grid, dim3(256), 0, st, dout, y, n_events, bitmask, s.W, mask_row_div,
+                         tile_start, (int)s.nT, (int)dim, (int)L, (int)d_model, (int)s.nNBW, (int)s.nDB,
+                         (int)s.nSeg, part);
     if ((rc = check_launch(fn))) return rc;
     const int64_t count = d_model * dim;
     hipLaunchKernelGGL(k_restore_proj_dw_sum, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, part,
-                       s.n_parts, count, dweight);
+                       s.n_parts, count, (int)d_model, (int)dim, dma ? 1 : 0, dweight);
     if ((rc = check_launch(fn))) return rc;
   }
   return BCM_OK;

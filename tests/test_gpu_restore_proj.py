@@ -66,6 +66,8 @@ CASES = [  # B, D, L, d_model, density, mask_row_div
     (4, 512, 1024, 256, 0.07, 1),  # config-4 layer slice
     (3, 64, 300, 64, 0.3, 1),      # LDS-DMA forward with an odd tile count (5 tiles: a half item pair)
     (1, 4096, 128, 64, 0.1, 1),    # dim past the DMA forward's LDS: the register-staged form runs
+    (2, 100, 1024, 128, 0.2, 1),   # LDS-DMA weight gradient: two 512-step segments, a partial channel block
+    (1, 192, 1056, 256, 0.1, 1),   # ... and a last segment of 32 steps, two 128-row blocks of W
 ]
 
 
