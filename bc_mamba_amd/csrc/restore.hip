@@ -145,6 +145,80 @@ __global__ __launch_bounds__(256) void k_restore_fwd(const TI* __restrict__ y, i
   }
 }
 
+// Restore forward for 16-bit outputs with two channels per lane (dim even):
+// one wave per (b, 128 consecutive channels, 64-step tile), so each store
+// instruction writes a whole 256-byte run of a (b, t) row (two packed
+// 16-bit values per lane), as the one-channel form does for fp32, whose
+// 16-bit stores filled only half of that (config 2, bf16: restore forward
+// at 2.5 TB/s). Loads as in k_restore_fwd, per channel of the lane; with
+// TI == TO the values travel as raw 16-bit words.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_restore_fwd_pair(const TI* __restrict__ y, int64_t n_events,
+                                                          const uint32_t* __restrict__ bitmask, int64_t W,
+                                                          int64_t mrd, const int32_t* __restrict__ tile_start,
+                                                          int nT, int nG, int waves, int dim, int64_t L,
+                                                          int64_t out_elems, TO* __restrict__ out) {
+  static_assert(sizeof(TO) == 2, "16-bit outputs");
+  constexpr bool RAW = std::is_same<TI, TO>::value;
+  asm volatile("" ::"s"(tile_start), "s"(bitmask), "s"(y), "s"(W), "s"(mrd), "s"(L), "s"(out_elems));
+  if (tile_wave_id(waves) >= waves) return;
+  const int wid = __builtin_amdgcn_readfirstlane(tile_wave_id(waves));
+  const int g = wid % nG, bj = wid / nG;
+  const int j = bj % nT, b = bj / nT;
+  const int lane = lane_id();
+  const int d = g * 2 * kWave + 2 * lane;
+  const bool ok = d < dim;  // dim is even: both channels of the lane exist or neither
+  const int64_t ch = (int64_t)b * dim + (ok ? d : dim - 2);
+  const int32_t* ts0 = tile_start + ch * (nT + 1);
+  const int32_t* ts1 = ts0 + (nT + 1);
+  const int32_t c0 = ts0[0], lo0 = ts0[j], c1 = ts1[0], lo1 = ts1[j];
+  const uint64_t m0 = ok ? tile_mask(bitmask + (ch / mrd) * W, j) : 0ull;
+  const uint64_t m1 = ok ? tile_mask(bitmask + ((ch + 1) / mrd) * W, j) : 0ull;
+  const int e_base = __builtin_amdgcn_readfirstlane(tile_start[((int64_t)b * dim + g * 2 * kWave) * (nT + 1)]);
+  const __amdgpu_buffer_rsrc_t ry = buf_rsrc(y + e_base, (n_events - e_base) * (int64_t)sizeof(TI));
+  auto ld = [&](uint32_t off) -> uint32_t {  // raw 16-bit word, or the fp32 value's bits
+    if constexpr (RAW) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ry, off, 0, 0);
+    else return __float_as_uint(buf_load<TI>(ry, off));
+  };
+  // the values held before the tile, then the tile's event values, in the
+  // order the stores use them (out-of-range offsets where a step has none)
+  uint32_t val0 = ld(ok && lo0 > c0 ? (uint32_t)(lo0 - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
+  uint32_t val1 = ld(ok && lo1 > c1 ? (uint32_t)(lo1 - 1 - e_base) * (uint32_t)sizeof(TI) : kBufOOB);
+  uint32_t v0[kTile], v1[kTile];
+  uint32_t i0 = (uint32_t)(lo0 - e_base), i1 = (uint32_t)(lo1 - e_base);
+#pragma unroll
+  for (int s = 0; s < kTile; ++s) {
+    const uint32_t b0 = (uint32_t)(m0 >> s) & 1u, b1 = (uint32_t)(m1 >> s) & 1u;
+    v0[s] = ld(b0 ? i0 * (uint32_t)sizeof(TI) : kBufOOB);
+    v1[s] = ld(b1 ? i1 * (uint32_t)sizeof(TI) : kBufOOB);
+    i0 += b0;
+    i1 += b1;
+  }
+  asm volatile("" : "+v"(val0), "+v"(val1));
+  const int64_t t0 = (int64_t)j * kTile;
+  const int steps = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const int64_t obase = ((int64_t)b * L + t0) * dim + (int64_t)g * 2 * kWave;
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(out + obase, (out_elems - obase) * 2);
+  const uint32_t lane_off = ok ? (uint32_t)lane * 4u : kBufOOB;
+  const uint32_t row_bytes = (uint32_t)dim * 2u;
+  auto bits16 = [&](uint32_t v) -> uint32_t {
+    if constexpr (RAW) return v;
+    else {
+      const TO h = from_f<TO>(__uint_as_float(v));
+      unsigned short u;
+      __builtin_memcpy(&u, &h, 2);
+      return u;
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < kTile; ++s) {
+    val0 = ((m0 >> s) & 1ull) ? v0[s] : val0;
+    val1 = ((m1 >> s) & 1ull) ? v1[s] : val1;
+    __builtin_amdgcn_raw_buffer_store_b32(bits16(val0) | (bits16(val1) << 16), ro,
+                                          s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB, 0, kStream);
+  }
+}
+
 // Restore backward, tile pass. Runs that start and end inside the tile are
 // final; the partial runs at the tile edges (head: before the first event;
 // tail: from the last event to the tile end) go to per-tile side arrays
@@ -371,6 +445,17 @@ int bcm_restore_fwd(const void* y, int y_dtype, int64_t n_events, const uint32_t
   auto go = [&](auto ti, auto to) {
     using TI = decltype(ti);
     using TO = decltype(to);
+    if constexpr (sizeof(TO) == 2) {
+      // two channels per lane: whole 256-byte row runs per store (dim even;
+      // 4-byte aligned stores)
+      if (dim % 2 == 0 && reinterpret_cast<uintptr_t>(out) % 4 == 0) {
+        const int64_t nG2 = (dim + 2 * kWave - 1) / (2 * kWave), waves2 = (n_rows / dim) * nT * nG2;
+        hipLaunchKernelGGL((k_restore_fwd_pair<TI, TO>), dim3(nblk(waves2)), dim3(256), 0, hs(stream),
+                           static_cast<const TI*>(y), n_events, bitmask, W, mask_row_div, tile_start, (int)nT,
+                           (int)nG2, (int)waves2, (int)dim, L, n_rows * L, static_cast<TO*>(out));
+        return;
+      }
+    }
     hipLaunchKernelGGL((k_restore_fwd<TI, TO>), dim3(nblk(waves)), dim3(256), 0, hs(stream),
                        static_cast<const TI*>(y), n_events, bitmask, W, mask_row_div, tile_start, (int)nT, (int)nG,
                        (int)waves, (int)dim, L, n_rows * L, static_cast<TO*>(out));

@@ -32,8 +32,10 @@ CASES = [  # B, D, L, density
 
 
 @pytest.mark.parametrize("B,D,L,p", CASES)
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_restore_fwd_bwd(cuda_device, B, D, L, p, dtype):
+    """16-bit values with an even D take the two-channels-per-lane forward
+    (an odd D the one-channel form); every value is a copy: bit-exact."""
     print(f"restore case B={B} D={D} L={L} p={p} {dtype}", flush=True)
     ch, t, cu = _events(B, D, L, p, seed=L + D, empty_every=5)
     g = torch.Generator().manual_seed(1)
