@@ -479,7 +479,7 @@ int bcm_restore_proj_fwd(const float* y, int64_t n_events, const uint32_t* bitma
 
 /* Workspace of bcm_restore_proj_bwd: the restore backward's per-tile
  * arrays (3 * 4 * n_rows * tile_count(L)) and the weight gradient's
- * partials (4 * d_model * dim per (sequence, 1024-step segment)). A call
+ * partials (4 * d_model * dim per (sequence, 512-step segment)). A call
  * with dweight == NULL needs only the per-tile arrays (the size of
  * bcm_restore_bwd_workspace_bytes(n_rows, L)). */
 int64_t bcm_restore_proj_bwd_workspace_bytes(int64_t n_rows, int64_t dim, int64_t L,

@@ -99,10 +99,10 @@ def test_restore_bwd_noalloc_rejects_before_launch(lib):
 
 def test_restore_proj_checks_before_launch(lib):
     """The fused restore -> out_proj entry points: workspace size formula
-    (fix-up arrays + one d_model x dim partial per 1024-step segment of each
+    (fix-up arrays + one d_model x dim partial per 512-step segment of each
     sequence) and argument errors raised before any launch."""
     n_rows, dim, L, dm = 128, 64, 1100, 32
-    nT, n_parts = nat.tile_count(L), (n_rows // dim) * 2
+    nT, n_parts = nat.tile_count(L), (n_rows // dim) * 3
     ws = lib.bcm_restore_proj_bwd_workspace_bytes(n_rows, dim, L, dm)
     assert ws == 3 * 4 * n_rows * nT + 4 * n_parts * dm * dim
     assert lib.bcm_restore_proj_bwd_workspace_bytes(n_rows, 0, L, dm) == 0
