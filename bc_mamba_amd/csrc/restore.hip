@@ -12,8 +12,10 @@
 // from the tile table, so all value loads are independent (no search, no
 // serial pointer chasing). Each kernel runs in branch-free phases (all loads,
 // register work, back-to-back stores) so no store waits on another. The
-// backward uses no atomics: runs inside a tile are written by the tile pass,
-// runs that cross a tile edge by a small fix-up pass, each event exactly once
+// backward uses no atomics on dy: runs inside a tile are written by the tile
+// pass, runs that cross a tile edge by a small fix-up pass (bcm_restore_bwd)
+// or, in one kernel, by a look-back over the preceding tiles' published
+// partials (bcm_restore_bwd_chained); each event exactly once
 // (deterministic, no zero-fill of dy).
 #include "bcm_common.hpp"
 
@@ -358,6 +360,183 @@ __global__ __launch_bounds__(256) void k_restore_bwd_fix(int64_t nT, int64_t n_r
   dy[e_end - 1] = acc;
 }
 
+// Restore backward in one pass: the tile pass above, with the runs that
+// cross tile edges closed by decoupled look-back instead of a fix-up pass.
+//
+// Sync area (64-bit words, zero before the first call, zero again after
+// every call): word 0 reserved, word 1 a status word (nonzero: a look-back
+// wait gave up), then one slot per (tile j, channel) at 2 + j * n_rows + ch.
+//  * Waves take wave ids in the tile kernels' order (channel group fastest,
+//    then tile, then batch), so tile j - 1 of a channel has a smaller id than
+//    tile j. The host launches the ids in ranges of at most 4 blocks per CU,
+//    which fit the device at once (launch bounds of 4 blocks, 32 KB of LDS
+//    each): a wave waits only on smaller ids, of its own launch (resident
+//    with it, whatever order the hardware dispatches workgroups in) or of an
+//    earlier one (complete), so every wait ends.
+//  * A tile publishes, per channel, the partial it hands on: the run open
+//    at its end (status 2, the tile holds an event) or its whole sum
+//    (status 1, no event), as one 64-bit word (status << 32 | value). It
+//    publishes where an event lies at or before the tile and the tile is
+//    not the last, i.e. where some later tile will read the slot.
+//  * A tile whose first event has an earlier event in the channel closes
+//    that event's run: its head (the steps before its first event) plus the
+//    slots of the tiles before it, walked back to the nearest one with
+//    status 2. The last tile closes the channel's last run the same way
+//    when it holds no event (its whole sum plus the walk), else from its
+//    own open run. A tile clears each slot it reads. Every published slot
+//    is read by exactly one tile (the channel's next tile with an event,
+//    else its last tile), so after the launch every slot is zero again.
+//  * A run closed at a tile's first event goes to dy[first event - 1],
+//    beside the tile's other runs in the same staged stores; only the
+//    channel's last run is a separate store.
+constexpr uint32_t kChainSpin = 1u << 20;  // polls before a wait gives up (about a second; never reached
+                                           // when every wave of a launch can be resident)
+constexpr int64_t kSyncHead = 2;           // sync words before the slots
+constexpr int kChainBlocksPerCu = 4;       // the kernel's launch bounds: 4 blocks of 256 fit a CU
+constexpr int kChainBatch = 4;             // slots a look-back round reads after its first
+
+template <typename TI>
+__global__ __launch_bounds__(256, kChainBlocksPerCu) void k_restore_bwd_chain(
+    const TI* __restrict__ dout, int64_t n_events, const uint32_t* __restrict__ bitmask, int64_t W, int64_t mrd,
+    const int32_t* __restrict__ tile_start, int nT, int nG, int waves, int wid0, int nblk, int dim, int64_t L,
+    int64_t n_rows, float* __restrict__ dy, uint64_t* __restrict__ sync) {
+  __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
+  asm volatile("" ::"s"(tile_start), "s"(bitmask), "s"(dout), "s"(W), "s"(mrd), "s"(L), "s"(n_rows), "s"(sync));
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int wid = __builtin_amdgcn_readfirstlane(wid0 + xcd_block(blockIdx.x, nblk) * kTileWaves + wave);
+  if (wid >= waves) return;
+  TileWave w;
+  w.g = wid % nG;
+  w.j = (wid / nG) % nT;
+  w.b = wid / nG / nT;
+  {
+    const int d = w.g * kWave + lane;
+    w.ok = d < dim;
+    w.dd = w.ok ? d : dim - 1;
+    w.ch = w.b * dim + w.dd;
+  }
+  const int32_t* ts = tile_start + (int64_t)w.ch * (nT + 1);
+  const int e_base = __builtin_amdgcn_readfirstlane(tile_start[(int64_t)(w.b * dim + w.g * kWave) * (nT + 1)]);
+  const int64_t t0 = (int64_t)w.j * kTile;
+  const int steps = (int)(L - t0 < kTile ? L - t0 : kTile);
+  const int64_t gbase = ((int64_t)w.b * L + t0) * dim + (int64_t)w.g * kWave;
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(dout + gbase, (n_rows * L - gbase) * (int64_t)sizeof(TI));
+  const uint32_t lane_off = w.ok ? (uint32_t)lane * (uint32_t)sizeof(TI) : kBufOOB;
+  const uint32_t row_bytes = (uint32_t)dim * (uint32_t)sizeof(TI);
+  const int32_t elo = ts[w.j], ts0 = ts[0], tsN = ts[nT];
+  const uint64_t m = w.ok ? tile_mask(bitmask + (w.ch / mrd) * W, w.j) : 0ull;
+  float gv[kTile];
+#pragma unroll
+  for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI, kStream>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
+  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
+  const int nev = __popcll(m);
+  const int incl = wave_incl_sum_dpp(nev);
+  const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+  const bool staged = total <= kBwdStage;  // wave-uniform
+  uint2* sr = s_run[wave];
+  const int pre = incl - nev;
+  float sum = 0.0f, hsum = 0.0f;
+  if (staged) {
+    uint32_t slot = (uint32_t)pre;
+    uint32_t dst = (uint32_t)(elo - e_base) - 1u;  // event whose run the next event closes
+#pragma unroll
+    for (int s = 0; s < kTile; ++s) {
+      const bool bit = (m >> s) & 1ull;
+      if (bit) {
+        sr[slot] = make_uint2(__float_as_uint(sum), dst);
+        ++slot;
+        ++dst;
+      }
+      sum = (bit ? 0.0f : sum) + gv[s];
+    }
+    hsum = nev ? __uint_as_float(sr[pre].x) : sum;
+  } else {
+    uint32_t r = 0;  // events seen so far in the tile
+    const uint32_t ebase = (uint32_t)(elo - e_base);
+    const int first = m ? __builtin_ctzll(m) : kTile;  // step of the tile's first event
+#pragma unroll
+    for (int s = 0; s < kTile; ++s) {
+      const uint32_t bit = (uint32_t)(m >> s) & 1u;
+      // the run of event (elo + r - 1) closes here when r >= 1
+      buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
+      r += bit;
+      sum = (bit ? 0.0f : sum) + gv[s];
+      hsum += s < first ? gv[s] : 0.0f;
+    }
+  }
+  // publish the partial this tile hands on, then close the run that ends
+  // at the tile's first event (or, in the last tile, the channel's last run)
+  uint64_t* slots = sync + kSyncHead;
+  const int32_t enext = elo + nev;  // first event at or after tile j + 1
+  if (w.ok && w.j < nT - 1 && enext > ts0)
+    __hip_atomic_store(&slots[(int64_t)w.j * n_rows + w.ch],
+                       ((uint64_t)(nev ? 2u : 1u) << 32) | (uint64_t)__float_as_uint(sum), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = w.ok && w.j == nT - 1 && tsN > ts0;  // the channel's last run ends in this tile
+  const bool head = w.ok && nev > 0 && elo > ts0;        // the run open at the tile's start ends here
+  const bool need = head || (last && nev == 0);
+  float carry = nev ? hsum : sum;
+  bool open = need;
+  int jj = w.j - 1;
+  // the walk reads one slot a round trip, four once it has met a tile
+  // without events (long silences: fewer serial round trips)
+  int nq = 1;
+  bool wide = false;
+  for (uint32_t it = 0; __builtin_amdgcn_ballot_w64(open); ++it) {
+    bool idle = false;
+    if (open) {
+      if (jj < 0 || it >= kChainSpin) {  // cannot happen with consistent inputs; recorded, never hangs
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(sync + 1), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        open = false;
+      } else {
+        uint64_t v[kChainBatch];
+#pragma unroll
+        for (int q = 0; q < kChainBatch; ++q)
+          v[q] = (q < nq && jj - q >= 0)
+                     ? __hip_atomic_load(&slots[(int64_t)(jj - q) * n_rows + w.ch], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT)
+                     : 0ull;
+        // take the slots in order up to the first unpublished one or the
+        // first with status 2
+#pragma unroll
+        for (int q = 0; q < kChainBatch; ++q) {
+          if (open && !idle && q < nq) {
+            if (v[q]) {
+              __hip_atomic_store(&slots[(int64_t)jj * n_rows + w.ch], (uint64_t)0, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+              carry += __uint_as_float((uint32_t)v[q]);
+              if ((uint32_t)(v[q] >> 32) == 2u) {
+                open = false;
+              } else {
+                --jj;
+                wide = true;
+              }
+            } else {
+              idle = jj >= 0;  // not yet published (jj < 0 is caught above on the next round)
+            }
+          }
+        }
+        nq = wide ? kChainBatch : 1;
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(idle)) __builtin_amdgcn_s_sleep(1);
+  }
+  if (staged) {
+    if (nev) sr[pre] = make_uint2(__float_as_uint(carry), head ? (uint32_t)(elo - e_base) - 1u : kNoDst);
+    wave_sync();
+    for (int k = 0; k < total; k += kWave) {
+      const int i = k + lane;
+      const uint2 v = sr[i < total ? i : 0];
+      buf_store_f32(rdy, i < total ? v.y * 4u : kBufOOB, __uint_as_float(v.x));
+    }
+  } else {
+    buf_store_f32(rdy, head ? ((uint32_t)(elo - e_base) - 1u) * 4u : kBufOOB, carry);
+  }
+  // the channel's last run: the tile's open run, or (no event in the tile)
+  // the walked-back sum
+  if (last) buf_store_f32(rdy, (uint32_t)(tsN - 1 - e_base) * 4u, nev ? sum : carry);
+}
+
 static unsigned nblk(int64_t waves) { return (unsigned)((waves + 3) / 4); }
 
 // Scratch of the allocation-free restore backward (bcm_restore_bwd_noalloc):
@@ -549,6 +728,41 @@ int bcm_restore_bwd_noalloc(const void* dout, int dtype, const uint32_t* bitmask
   if (rc) return rc;
   return restore_bwd_run(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events, ws,
                          hs(stream));
+}
+
+int64_t bcm_restore_bwd_sync_bytes(int64_t n_rows, int64_t L) {
+  return (n_rows < 0 || L < 1) ? 0 : 8 * (kSyncHead + n_rows * tile_count(L));
+}
+
+int bcm_restore_bwd_chained(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
+                            const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy,
+                            int64_t n_events, void* sync, int64_t sync_bytes, bcm_stream_t stream) {
+  const char* fn = "bcm_restore_bwd_chained";
+  const int c = restore_bwd_checks(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events);
+  if (c) return c > 0 ? BCM_OK : -c;
+  if (!sync || (reinterpret_cast<uintptr_t>(sync) & 7) != 0 || sync_bytes < bcm_restore_bwd_sync_bytes(n_rows, L))
+    return set_error(BCM_EINVAL, "%s: an 8-byte aligned sync area of %lld bytes required", fn,
+                     (long long)bcm_restore_bwd_sync_bytes(n_rows, L));
+  const int64_t W = bitmask_words(L), nT = tile_count(L), nG = (dim + kWave - 1) / kWave;
+  const int64_t waves = (n_rows / dim) * nT * nG;
+  if (waves > INT32_MAX / 2 || dim > (1 << 22)) return set_error(BCM_EINVAL, "%s: problem too large", fn);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    return set_error(BCM_EHIP, "%s: cannot read the device's compute-unit count", fn);
+  // launches of at most kChainBlocksPerCu blocks per CU, in wave-id order
+  const int64_t per_launch = (int64_t)cus * kChainBlocksPerCu * kTileWaves;
+  dispatch_dtype(dtype, [&](auto tag) {
+    using T = decltype(tag);
+    for (int64_t w0 = 0; w0 < waves; w0 += per_launch) {
+      const int64_t n = std::min(per_launch, waves - w0);
+      const int nb = (int)nblk(n);
+      hipLaunchKernelGGL(k_restore_bwd_chain<T>, dim3(nb), dim3(256), 0, hs(stream), static_cast<const T*>(dout),
+                         n_events, bitmask, W, mask_row_div, tile_start, (int)nT, (int)nG, (int)waves, (int)w0, nb,
+                         (int)dim, L, n_rows, dy, static_cast<uint64_t*>(sync));
+    }
+  });
+  return check_launch(fn);
 }
 
 }  // extern "C"

@@ -10,7 +10,9 @@ full-size parity tests check.
             -> flat selective scan (bcm_scan_fwd)
             -> zero-order-hold restore (bcm_restore_fwd, from the bitmask
             and tile table: no t stream)
-  backward: restore backward (bcm_restore_bwd, fp32 dy)
+  backward: restore backward (bcm_restore_bwd_chained: one kernel, the runs
+            that cross tile edges closed by look-back, where its tile grid
+            fits one launch; else bcm_restore_bwd; fp32 dy)
             -> scan backward with the gather backward in the same kernel
             where the shape allows (bcm_scan_bwd_rows: du, the six
             parameter gradients and the dense dx rows)
@@ -41,8 +43,20 @@ class FusedStep:
 
     KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd"]
 
-    def __init__(self, w, dev):
-        self.w, self.dev = w, dev
+    def __init__(self, w, dev, restore_bwd="auto"):
+        """restore_bwd: "chained" (one kernel, bcm_restore_bwd_chained),
+        "two_pass" (tile pass + fix-up pass, bcm_restore_bwd) or "auto": the
+        chained form where its tile grid fits one launch (at most 4 blocks
+        of 4 waves per CU; configs 1 and 2), else the two-pass form (the
+        chained form's later launches cannot overlap the earlier ones:
+        config 3, 54 against 40 us)."""
+        if restore_bwd not in ("auto", "chained", "two_pass"):
+            raise ValueError(f"restore_bwd must be 'auto', 'chained' or 'two_pass', not {restore_bwd!r}")
+        if restore_bwd == "auto":
+            waves = w.B * nat.tile_count(w.L) * -(-w.D // 64)
+            cus = torch.cuda.get_device_properties(dev).multi_processor_count
+            restore_bwd = "chained" if waves <= 16 * cus else "two_pass"
+        self.w, self.dev, self.restore_bwd = w, dev, restore_bwd
         B, D, L = w.B, w.D, w.L
         self.NC = B * D
         i32 = dict(dtype=torch.int32, device=dev)
@@ -54,6 +68,10 @@ class FusedStep:
         self.tile_start = torch.empty((self.NC, nat.tile_count(L) + 1), **i32)
         self.dense = torch.empty((B, L, D), dtype=w.dtype, device=dev)
         self.dx = torch.empty((B, D, L), dtype=w.dtype, device=dev)
+        # the chained restore backward's sync area: zeroed once here, left
+        # zeroed by every call
+        self.sync = torch.zeros(nat.lib().bcm_restore_bwd_sync_bytes(self.NC, L) // 8, dtype=torch.int64,
+                                device=dev)
         self.ws = torch.empty(nat.lib().bcm_restore_bwd_workspace_bytes(self.NC, L) // 4, dtype=torch.float32,
                               device=dev)
         cap = self.NC * L  # upper bound of E
@@ -152,9 +170,14 @@ class FusedStep:
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y_buf), dt, E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense), dt, s))
-        mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), dt, P(self.bitmask), 1,
-                                             P(self.tile_start), self.NC, D, L, P(self.dy32_buf), E, P(self.ws),
-                                             4 * self.ws.numel(), s))
+        if self.restore_bwd == "chained":
+            mark("restore_bwd", lambda: nat.call("bcm_restore_bwd_chained", P(w.dout), dt, P(self.bitmask), 1,
+                                                 P(self.tile_start), self.NC, D, L, P(self.dy32_buf), E,
+                                                 P(self.sync), 8 * self.sync.numel(), s))
+        else:
+            mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), dt, P(self.bitmask), 1,
+                                                 P(self.tile_start), self.NC, D, L, P(self.dy32_buf), E,
+                                                 P(self.ws), 4 * self.ws.numel(), s))
         if self.dy_buf is not self.dy32_buf:  # the scan takes dout in u's dtype
             self.dy_buf[:E].copy_(self.dy32_buf[:E])
         # the scan backward writes du and the dense dx rows (the gather

@@ -40,7 +40,7 @@ FLUSH_BYTES = 512 << 20  # read before each timed step: more than the 8 L2s plus
 # device kernels behind each stage of FusedStep.KERNELS (symbol substrings)
 STAGE_KERNELS = {"count": ["k_count"], "fill": ["k_fill"],
                  "scan_fwd": ["k_scan_fwd"], "restore_fwd": ["k_restore_fwd"],
-                 "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix"],
+                 "restore_bwd": ["k_restore_bwd_tiles", "k_restore_bwd_fix", "k_restore_bwd_chain"],
                  "scan_bwd": ["k_scan_bwd", "k_scan_param_reduce", "k_gather_bwd_rows"]}
 
 
@@ -201,6 +201,9 @@ def main():
                     help="skip the two rocprofv3 --pmc child runs that measure the dominant kernel's HBM bytes")
     ap.add_argument("--out-proj", choices=["gemm", "mfma", "off"], default="gemm",
                     help="config 4: the blocks' restore -> out_proj op (default gemm; off: restore then linear)")
+    ap.add_argument("--restore-bwd", choices=["auto", "chained", "two_pass"], default="auto",
+                    help="restore backward form: one kernel with look-back, tile pass + fix-up pass, or the "
+                         "first where its tile grid fits one launch")
     ap.add_argument("--no-peak", action="store_true",
                     help="config 4: skip the peak-memory steps (fused and reference composition) after timing")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
@@ -220,7 +223,7 @@ def main():
         print(json.dumps(model_step_bench(args, dev)), flush=True)
         return
     w = make_workload(args.cfg).to(dev)
-    path = FusedStep(w, dev)
+    path = FusedStep(w, dev, restore_bwd=args.restore_bwd)
 
     if args.pmc_child:  # a few steps and the calibration copy, run under rocprofv3 --pmc by the parent
         for _ in range(3):
@@ -289,6 +292,7 @@ def main():
         "config": {"workload": f"config {args.cfg}: extract+gather -> flat scan -> ZOH restore, fwd+bwd",
                    "B": w.B, "D": w.D, "L": w.L, "N": w.N, "events": E, "density": E / (w.B * w.D * w.L),
                    "max_seqlen": ms},
+        "restore_bwd_form": path.restore_bwd,
         "achieved_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
         "algorithmic_bytes": total_bytes,
         # the same time against this build's own compulsory traffic (no ch /

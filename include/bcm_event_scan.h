@@ -463,6 +463,30 @@ int bcm_restore_bwd_noalloc(const void* dout, int dtype, const uint32_t* bitmask
                             int64_t n_rows, int64_t dim, int64_t L, float* dy,
                             int64_t n_events, bcm_stream_t stream);
 
+/* Sync area of bcm_restore_bwd_chained: 8 * (2 + n_rows * tile_count(L))
+ * bytes. */
+int64_t bcm_restore_bwd_sync_bytes(int64_t n_rows, int64_t L);
+
+/* restore_dense_bwd (restore_dense.cpp:138-202,
+ * restore_dense_bwd_kernel.cuh:42-112) in one kernel: the result of
+ * bcm_restore_bwd (every event with 0 <= t_e < L written exactly once, no
+ * atomics on dy), with the runs that cross 64-step tile edges closed by a
+ * look-back over the preceding tiles' published partials instead of a
+ * second pass. Sums within a run follow a different order than
+ * bcm_restore_bwd where a run crosses two or more tile edges (fp32
+ * rounding; equal otherwise).
+ * `sync` (8-byte aligned, sync_bytes >= bcm_restore_bwd_sync_bytes) must
+ * be zero before its first use; every call that completes leaves it zero
+ * again, so a caller zeroes it once and reuses it. Word 1 (uint64) becomes
+ * nonzero if a wait gave up, which consistent inputs never cause; the area
+ * must then be zeroed again. Calls that share a sync area must be ordered
+ * (one stream); calls with separate areas may overlap. */
+int bcm_restore_bwd_chained(const void* dout, int dtype, const uint32_t* bitmask,
+                            int64_t mask_row_div, const int32_t* tile_start,
+                            int64_t n_rows, int64_t dim, int64_t L, float* dy,
+                            int64_t n_events, void* sync, int64_t sync_bytes,
+                            bcm_stream_t stream);
+
 /* ---- (3') restore -> out_proj ------------------------------------------- */
 /* The block's restore followed by its output projection (e_model.py:499-504:
  * y_dense = restore_dense_fn(y_flat, ...); out = self.out_proj(y_dense)),
