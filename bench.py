@@ -322,9 +322,59 @@ def main():
         # the drop-in Python API path (autograd Functions over the same
         # library), warm: what a caller of the reference's interface sees
         result["api_ms_per_step"] = api_path_ms(w, dev, args.steps, args.warmup)
+    if args.cfg == 3:
+        # the reference encodes config 3's two towers as two B = 32 calls
+        # (lra_impl.py:1685-1688): the same inputs as two half-batch steps
+        result["towers_2x32"] = towers_bench(w, dev, args)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cfg, args.cpu_batches)
     print(json.dumps(result), flush=True)
+
+
+class TwoTowers:
+    """One step over workload w as two calls of half the batch each (the
+    towers of config 3), one FusedStep per half, one after the other on
+    the stream."""
+
+    def __init__(self, w, dev, **kw):
+        from bc_mamba_amd.fused_step import FusedStep
+        from bc_mamba_amd.workloads import Workload
+        h = w.B // 2
+        self.parts = []
+        for sl in (slice(0, h), slice(h, w.B)):
+            f = {k: getattr(w, k) for k in w.__dataclass_fields__}
+            f["B"] = sl.stop - sl.start
+            for k in ("membrane", "x_conv", "dout"):
+                f[k] = getattr(w, k)[sl].contiguous()
+            self.parts.append(FusedStep(Workload(**f), dev, **kw))
+
+    def step(self):
+        for p in self.parts:
+            p.step()
+
+    @property
+    def E(self):
+        return sum(p.E for p in self.parts)
+
+
+def towers_bench(w, dev, args):
+    """Cold and warm step time of the two-call encoding (same protocol as
+    the headline figure)."""
+    import torch
+    two = TwoTowers(w, dev, restore_bwd=args.restore_bwd)
+    for _ in range(args.warmup):
+        two.step()
+    cold = cold_steps_ms(two, dev, args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        two.step()
+    torch.cuda.synchronize()
+    warm_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    E = two.E
+    return {"calls": [p.w.B for p in two.parts], "events": E, "ms_per_step": cold["median"],
+            "events_per_s": E / (cold["median"] * 1e-3), "warm_ms_per_step": warm_ms,
+            "restore_bwd_form": [p.restore_bwd for p in two.parts]}
 
 
 def model_step_bench(args, dev):
