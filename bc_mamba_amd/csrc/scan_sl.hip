@@ -21,12 +21,14 @@
 //     loads are in flight while a block computes (a ring of registers), so
 //     memory latency overlaps the VALU.
 //   * Sums over the states of one event (y, and the backward's Σ_s W_B W_C e
-//     and Σ_s W_B W_C g) go through a padded LDS tile per row: state lane s
-//     writes its 16 values of the block at (q·17 + s), event lane j reads its
-//     16 states at (j·17 + m): conflict-free both ways. With one state per
-//     lane the reader applies the per-state weight; with several, each lane
-//     first forms its states' weighted sum, so the tile traffic per event
-//     stays one write and one read per lane.
+//     and Σ_s W_B W_C g): with one state per lane, each lane keeps its
+//     weighted values of the block's 16 events in registers and a DPP
+//     reduce-scatter over the row leaves event j's sum in lane j (four
+//     halving steps, no LDS round trip and no wave barrier). With several
+//     states per lane, each lane forms its states' weighted sum and the
+//     sums go through a padded LDS tile per row: state lane s writes its 16
+//     values at (q·17 + s), event lane j reads its 16 at (j·17 + m):
+//     conflict-free both ways, one write and one read per lane and event.
 //   * The forward saves the state h at the start of every 32-event pass in
 //     chunk_g; the backward walks a channel's passes last to first, rebuilds
 //     the pass's states (and, up to two states per lane, decays) in registers
@@ -206,6 +208,31 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+// Sums over the 16 lanes of each DPP row of v[Q], Q = 0..15, leaving lane s
+// of the row with the sum for Q = s: a reduce-scatter in four halving steps
+// (partners s and 15 - s, then mirrors within 8 lanes, then quad xors), each
+// lane keeping the half of its values that holds its own index and adding
+// its partner's copy of that half. All VALU (DPP), no LDS round trip.
+__device__ __forceinline__ float row_reduce_scatter16(const float (&v)[kSLN]) {
+  const int s = lane_id() & (kSLN - 1);
+  auto add_dpp = [](float kp, float snd, auto ctrl) {
+    constexpr int C = decltype(ctrl)::value;
+    return kp + __uint_as_float(dpp<C>(__float_as_uint(snd)));
+  };
+  float a[8], b[4], c[2];
+  const bool l8 = s < 8, l4 = (s & 7) < 4, l2 = (s & 3) < 2, l1 = (s & 1) == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    a[i] = add_dpp(l8 ? v[i] : v[8 + i], l8 ? v[8 + i] : v[i], std::integral_constant<int, 0x140>{});  // row_mirror
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    b[i] = add_dpp(l4 ? a[i] : a[4 + i], l4 ? a[4 + i] : a[i], std::integral_constant<int, kDppHalfMirror>{});
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    c[i] = add_dpp(l2 ? b[i] : b[2 + i], l2 ? b[2 + i] : b[i], std::integral_constant<int, kDppXor2>{});
+  return add_dpp(l1 ? c[0] : c[1], l1 ? c[1] : c[0], std::integral_constant<int, kDppXor1>{});
+}
+
 // Decay table of model channel d: T[m][0] = 1 (padding), T[m][k] = the
 // decay of gap k, the same expression as the per-event path. Thread t
 // builds the entries of state t % N (consecutive threads: consecutive
@@ -291,16 +318,7 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
     const int64_t ix = (int64_t)d * N + s + kSLN * j;
     Al[j] = a.A[ix] * kLog2e;
     wb[j] = a.W_B[ix];
-    cw[j] = NL > 1 ? wb[j] * a.W_C[ix] : 0.0f;
-  }
-  // one state per lane: W_B·W_C of every state, the event lanes' weights
-  // (wave-uniform, scalar registers); several: each lane weights its own
-  float wbc[NL == 1 ? kSLN : 1];
-  if constexpr (NL == 1) {
-#pragma unroll
-    for (int m = 0; m < kSLN; ++m)
-      wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
-          __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
+    cw[j] = wb[j] * a.W_C[ix];  // one state per lane: W_B W_C of the lane's own state
   }
   const uint32_t rowb = sl_tab_lane(s, grp);
 
@@ -364,12 +382,13 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
             }
           });
         }
+        float wq[kSLN];  // one state per lane: W_B W_C g of the lane's state after each event
         for16([&](auto q) {
           constexpr int Q = decltype(q)::value;
           if constexpr (NL == 1) {
             g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2));
             if (EXACT) P[0] *= av[0][Q];
-            xt[Q * (kSLN + 1) + s] = g[0];
+            wq[Q] = cw[0] * g[0];
           } else {
             const float x = bcast_f<Q>(du2);
 #pragma unroll
@@ -383,14 +402,16 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
             xt[Q * (kSLN + 1) + s] = w;
           }
         });
-        wave_sync();
         float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
+        if constexpr (NL == 1) {
+          // the row's 16 states summed per event across the lanes (DPP)
+          acc = row_reduce_scatter16(wq);
+        } else {
+          wave_sync();
 #pragma unroll
-        for (int m = 0; m < kSLN; ++m) {
-          if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
-          else acc += xt[s * (kSLN + 1) + m];
+          for (int m = 0; m < kSLN; ++m) acc += xt[s * (kSLN + 1) + m];
+          wave_sync();  // the tile is rewritten by the next block
         }
-        wave_sync();  // the tile is rewritten by the next block
         const float y = fmaf(Dv, uv, uv * acc);
         const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
         buf_store<T>(ro, eo, y);
@@ -466,8 +487,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_arg
 // event before (and across passes). Per state: T0 = Σ tg, T1 = Σ tg·(k-1)
 // with tg = f·g_{i-1}, and Σ e·Δu² (dW_B; dW_C is the same sum, since
 // Σ_i dout_i u_i g_i = Σ_i e_i Δ_i u_i² over a channel). Per event lane:
-// Σ_s W_B W_C g_s (phase A) and Σ_s W_B W_C e_s (phase B) through the
-// transpose tile, then du, the Δ terms of ddt and dD.
+// Σ_s W_B W_C g_s (phase A) and Σ_s W_B W_C e_s (phase B), summed over the
+// row (see the file's head), then du, the Δ terms of ddt and dD.
 constexpr int kSLRowCap = 512;  // events of one channel kept in LDS for its dense row
 
 // Four steps t0..t0+3 of a channel's dense gradient row (the gather
@@ -511,7 +532,12 @@ template <int NL, typename F> __device__ __forceinline__ void forj(F&& f) {
 // WR: the dense rows are written by the workgroup's row writers
 // (sl_row_writer) as the passes finish; the waves here publish, per slot,
 // the first event whose du is final in prog.
-template <typename T, bool HAS_Z, bool DXR, int NL, bool WR>
+// RS (one state per lane): the per-event sums over the row's states by DPP
+// reduce-scatter instead of the LDS tile (pays at one wave per SIMD, where
+// nothing hides the tile's round trips; at two the other wave hides them
+// and the reduce-scatter's VALU costs more: config 2 scan backward 39.0 ->
+// 36.5 us, config 1 38.6 -> 39.1 us).
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR, bool RS>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
                                             float* sacc, float* sdu, int* sord, int* keys, int* prog, int nw, int S,
                                             int rank) {
@@ -553,15 +579,6 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
     wc[j] = a.W_C[ix];
     wbcs[j] = wb[j] * wc[j];
     wbca[j] = wbcs[j] * Av;
-  }
-  // one state per lane: W_B·W_C of every state, the event lanes' weights
-  // (wave-uniform, scalar registers); several: each lane weights its own
-  float wbc[NL == 1 ? kSLN : 1];
-  if constexpr (NL == 1) {
-#pragma unroll
-    for (int m = 0; m < kSLN; ++m)
-      wbc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(
-          __float_as_int(a.W_B[(int64_t)d * N + m] * a.W_C[(int64_t)d * N + m])));
   }
   const uint32_t rowb = sl_tab_lane(s, grp);
 
@@ -706,6 +723,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
         for (int j = 0; j < NL; ++j) g[j] = g_in[j];
 #pragma unroll
         for (int t = 0; t < NB; ++t) {
+          float wq[kSLN];  // one state per lane: W_B W_C g of the lane's state after each event
           forr<0, kSLB / H>([&](auto hc) {
             constexpr int Q0 = decltype(hc)::value * H;
             float av[NL][kSLB];
@@ -716,7 +734,10 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
                 g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2[t]));
                 gb[t * kSLB + Q][0] = g[0];
                 ab[t * kSLB + Q][0] = av[0][Q];
-                if constexpr (!USE) xt[Q * (kSLN + 1) + s] = g[0];
+                if constexpr (!USE) {
+                  if constexpr (RS) wq[Q] = wbcs[0] * g[0];
+                  else xt[Q * (kSLN + 1) + s] = wbcs[0] * g[0];
+                }
               } else {
                 const float x = bcast_f<Q>(du2[t]);
 #pragma unroll
@@ -735,15 +756,16 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
             });
           });
           if constexpr (!USE) {
-            wave_sync();
-            float acc = 0.0f;
+            if constexpr (NL == 1 && RS) {
+              acc2[t] = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
+            } else {
+              wave_sync();
+              float acc = 0.0f;
 #pragma unroll
-            for (int m = 0; m < kSLN; ++m) {
-              if constexpr (NL == 1) acc = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc);
-              else acc += xt[s * (kSLN + 1) + m];
+              for (int m = 0; m < kSLN; ++m) acc += xt[s * (kSLN + 1) + m];
+              acc2[t] = acc;
+              wave_sync();
             }
-            acc2[t] = acc;
-            wave_sync();
           }
         }
       };
@@ -753,6 +775,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
 #pragma unroll
       for (int tt = 0; tt < NB; ++tt) {
         const int t = NB - 1 - tt;
+        float wq[kSLN];  // one state per lane: W_B W_C e of the lane's state at each event
         rforr<0, kSLB / H>([&](auto hc) {
         constexpr int Q0 = decltype(hc)::value * H;
         float av[KEEPA ? 1 : NL][kSLB];  // four states per lane: the block's decays read again
@@ -767,7 +790,8 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
             T0[0] += tg;
             fmac_bcast<Q, Q == kSLB - 1>(T1[0], km[t], tg);   // T1 += (k-1)·tg
             fmac_bcast<Q, Q == kSLB - 1>(dWB[0], du2[t], e);  // dWB += Δu²·e
-            xt[Q * (kSLN + 1) + s] = e;
+            if constexpr (RS) wq[Q] = wbcs[0] * e;
+            else xt[Q * (kSLN + 1) + s] = wbcs[0] * e;
           } else {
             const float dq = bcast_f<Q>(doutu[t]);
             float w = 0.0f;
@@ -788,14 +812,15 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
           }
         });
         });
-        wave_sync();
         float acc1 = 0.0f;
+        if constexpr (NL == 1 && RS) {
+          acc1 = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
+        } else {
+          wave_sync();
 #pragma unroll
-        for (int m = 0; m < kSLN; ++m) {
-          if constexpr (NL == 1) acc1 = fmaf(xt[s * (kSLN + 1) + m], wbc[m], acc1);
-          else acc1 += xt[s * (kSLN + 1) + m];
+          for (int m = 0; m < kSLN; ++m) acc1 += xt[s * (kSLN + 1) + m];
+          wave_sync();
         }
-        wave_sync();
         // the lane's own event of block t: du, the Δu² terms of ddt, dD
         const int i = p * Sh::Pass + t * kSLB + s;
         const float duv = fmaf(gg[t], Dv + acc2[t], 2.0f * dl[t] * uv[t] * acc1);
@@ -977,7 +1002,7 @@ __device__ void sl_row_writer(const bcm_scan_args& a, const ScanRows& rw, const 
   __syncthreads();  // the compute waves' final barrier
 }
 
-template <typename T, bool HAS_Z, bool DXR, int NL, bool WR = false>
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR = false, bool RS = false>
 __global__ __launch_bounds__(WR ? kScanThreads + 4 * kWave : kScanThreads) void k_scan_bwd_sl(
     const bcm_scan_args a, const ScanRows rw, int nw, int S, int rank) {
   __shared__ float sT[SLShape<NL>::TabSz];
@@ -996,7 +1021,7 @@ __global__ __launch_bounds__(WR ? kScanThreads + 4 * kWave : kScanThreads) void 
   }
   // row writers need a single unranked round (the host's choice); rank 0
   // keeps the barrier count of both kinds of wave equal
-  sl_bwd_body<T, HAS_Z, DXR, NL, WR>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
+  sl_bwd_body<T, HAS_Z, DXR, NL, WR, RS>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
                                      sdu + (wave * kSLRows + grp) * kSLRowCap, sord,
                                      reinterpret_cast<int*>(&sX[0][0]), sprog, nw, S, WR ? 0 : rank);
 }
@@ -1083,9 +1108,19 @@ int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
 template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, dim3 grid, dim3 block, int nw, int S,
                                         int rank, const ScanRows* rw) {
   const ScanRows rows = rw ? *rw : ScanRows{};
+  // one compute wave per SIMD (the grid's waves fit the SIMDs once): the
+  // per-event state sums by DPP reduce-scatter (RS)
+  const bool rs = (int64_t)grid.x * nw <= 4ll * device_cus();
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
     if constexpr (NL == 1) {
+      auto go = [&](auto z, auto dxr, auto wr, dim3 blk, size_t lds) {
+        constexpr bool Z = decltype(z)::value, X = decltype(dxr)::value, W = decltype(wr)::value;
+        if (rs) hipLaunchKernelGGL((k_scan_bwd_sl<T, Z, X, 1, W, true>), grid, blk, lds, st, a, rows, nw, S, rank);
+        else hipLaunchKernelGGL((k_scan_bwd_sl<T, Z, X, 1, W, false>), grid, blk, lds, st, a, rows, nw, S, rank);
+      };
+      using Y = std::true_type;
+      using F = std::false_type;
       if (rw) {
         const size_t lds = (size_t)nw * kSLRows * kSLRowCap * 4;
         // one unranked round of channels on rows of at most 64 tiles, one
@@ -1096,15 +1131,17 @@ template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, 
         // writers' poll interval), so those shapes write the rows in-wave.
         const int64_t per_d = (a.n_channels + a.dim - 1) / a.dim;
         if (!rank && nw <= 4 && per_d <= (int64_t)nw * kSLRows * S && rows.nT <= kRowWriterTiles)
-          hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1, true>), grid, dim3(block.x + 4 * kWave), lds, st, a,
-                             rows, nw, S, rank);
+          go(F{}, Y{}, Y{}, dim3(block.x + 4 * kWave), lds);
         else
-          hipLaunchKernelGGL((k_scan_bwd_sl<T, false, true, 1>), grid, block, lds, st, a, rows, nw, S, rank);
+          go(F{}, Y{}, F{}, block, lds);
         return;
       }
+      if (a.z) go(Y{}, F{}, F{}, block, 0);
+      else go(F{}, F{}, F{}, block, 0);
+    } else {
+      if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
+      else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
     }
-    if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
-    else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
   });
 }
 
