@@ -21,14 +21,13 @@
 //     loads are in flight while a block computes (a ring of registers), so
 //     memory latency overlaps the VALU.
 //   * Sums over the states of one event (y, and the backward's Σ_s W_B W_C e
-//     and Σ_s W_B W_C g): with one state per lane, each lane keeps its
-//     weighted values of the block's 16 events in registers and a DPP
-//     reduce-scatter over the row leaves event j's sum in lane j (four
-//     halving steps, no LDS round trip and no wave barrier). With several
-//     states per lane, each lane forms its states' weighted sum and the
-//     sums go through a padded LDS tile per row: state lane s writes its 16
-//     values at (q·17 + s), event lane j reads its 16 at (j·17 + m):
-//     conflict-free both ways, one write and one read per lane and event.
+//     and Σ_s W_B W_C g): each lane forms its states' weighted share for
+//     each of the block's 16 events, and a DPP reduce-scatter over the row
+//     leaves event j's sum in lane j (four halving steps, no LDS round trip
+//     and no wave barrier). The backward with one state per lane at two
+//     compute waves per SIMD keeps a padded LDS tile per row instead: state
+//     lane s writes its 16 shares at (q·17 + s), event lane j reads its 16
+//     at (j·17 + m), conflict-free both ways.
 //   * The forward saves the state h at the start of every 32-event pass in
 //     chunk_g; the backward walks a channel's passes last to first, rebuilds
 //     the pass's states (and, up to two states per lane, decays) in registers
@@ -399,19 +398,12 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
             float w = cw[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
 #pragma unroll
             for (int j = 1; j < NL; ++j) w = fmaf(cw[j], g[j], w);
-            xt[Q * (kSLN + 1) + s] = w;
+            wq[Q] = w;
           }
         });
-        float acc = 0.0f;  // Σ_s W_B W_C g_s of the lane's event
-        if constexpr (NL == 1) {
-          // the row's 16 states summed per event across the lanes (DPP)
-          acc = row_reduce_scatter16(wq);
-        } else {
-          wave_sync();
-#pragma unroll
-          for (int m = 0; m < kSLN; ++m) acc += xt[s * (kSLN + 1) + m];
-          wave_sync();  // the tile is rewritten by the next block
-        }
+        // Σ_s W_B W_C g_s of the lane's event: the row's lanes' shares
+        // summed per event across the lanes (DPP)
+        const float acc = row_reduce_scatter16(wq);
         const float y = fmaf(Dv, uv, uv * acc);
         const uint32_t eo = valid ? off(e0, bk) * SZ : kBufOOB;
         buf_store<T>(ro, eo, y);
@@ -532,11 +524,12 @@ template <int NL, typename F> __device__ __forceinline__ void forj(F&& f) {
 // WR: the dense rows are written by the workgroup's row writers
 // (sl_row_writer) as the passes finish; the waves here publish, per slot,
 // the first event whose du is final in prog.
-// RS (one state per lane): the per-event sums over the row's states by DPP
-// reduce-scatter instead of the LDS tile (pays at one wave per SIMD, where
-// nothing hides the tile's round trips; at two the other wave hides them
-// and the reduce-scatter's VALU costs more: config 2 scan backward 39.0 ->
-// 36.5 us, config 1 38.6 -> 39.1 us).
+// RS: the per-event sums over the row's states by DPP reduce-scatter
+// instead of the LDS tile. With several states per lane always (config 3
+// scan backward 180 -> 177 us); with one state per lane at one compute wave
+// per SIMD, where nothing hides the tile's round trips (config 2 39.0 ->
+// 36.5 us), not at two, where the other wave hides them and the
+// reduce-scatter's VALU costs more (config 1 38.6 -> 39.1 us).
 template <typename T, bool HAS_Z, bool DXR, int NL, bool WR, bool RS>
 __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
                                             float* sacc, float* sdu, int* sord, int* keys, int* prog, int nw, int S,
@@ -750,13 +743,14 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
                   float w = wbcs[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
 #pragma unroll
                   for (int j = 1; j < NL; ++j) w = fmaf(wbcs[j], g[j], w);
-                  xt[Q * (kSLN + 1) + s] = w;
+                  if constexpr (RS) wq[Q] = w;
+                  else xt[Q * (kSLN + 1) + s] = w;
                 }
               }
             });
           });
           if constexpr (!USE) {
-            if constexpr (NL == 1 && RS) {
+            if constexpr (RS) {
               acc2[t] = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
             } else {
               wave_sync();
@@ -808,12 +802,13 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
               fmac_bcast<Q, Q == kSLB - 1 && J == 0>(dWB[J], du2[t], e);  // dWB += Δu²·e
               w = J == 0 ? wbcs[0] * e : fmaf(wbcs[J], e, w);
             });
-            xt[Q * (kSLN + 1) + s] = w;
+            if constexpr (RS) wq[Q] = w;
+            else xt[Q * (kSLN + 1) + s] = w;
           }
         });
         });
         float acc1 = 0.0f;
-        if constexpr (NL == 1 && RS) {
+        if constexpr (RS) {
           acc1 = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
         } else {
           wave_sync();
@@ -1139,8 +1134,8 @@ template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, 
       if (a.z) go(Y{}, F{}, F{}, block, 0);
       else go(F{}, F{}, F{}, block, 0);
     } else {
-      if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
-      else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
+      if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL, false, true>), grid, block, 0, st, a, rows, nw, S, rank);
+      else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL, false, true>), grid, block, 0, st, a, rows, nw, S, rank);
     }
   });
 }
