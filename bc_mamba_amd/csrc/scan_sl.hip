@@ -262,8 +262,8 @@ __device__ __forceinline__ int sl_slot_order(int wave, int grp, int nw) {
 // rank: rank the model channel's channels by length first (sord: [kSortMax]
 // ints of LDS, keys: kSortMax ints of scratch LDS, dead after the ranking).
 template <typename T, bool HAS_Z, int NL>
-__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, float* xt, int* sord, int* keys,
-                                            int nw, int S, int rank) {
+__device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, int* sord, int* keys, int nw, int S,
+                                            int rank) {
 #pragma clang fp contract(off)  // fmas are written out where they are meant
   using Sh = SLShape<NL>;
   constexpr uint32_t SZ = sizeof(T);
@@ -463,12 +463,9 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, f
 template <typename T, bool HAS_Z, int NL>
 __global__ __launch_bounds__(kScanThreads) void k_scan_fwd_sl(const bcm_scan_args a, int nw, int S, int rank) {
   __shared__ float sT[SLShape<NL>::TabSz];
-  __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   __shared__ int sord[kSortMax];
-  static_assert(sizeof(sX) >= kSortMax * sizeof(int), "the transpose tiles hold the ranking keys");
-  const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
-  float* xt = &sX[wave][grp * kSLTileSz];
-  sl_fwd_body<T, HAS_Z, NL>(a, sT, xt, sord, reinterpret_cast<int*>(&sX[0][0]), nw, S, rank);
+  __shared__ int skeys[kSortMax];  // the ranking's scratch keys
+  sl_fwd_body<T, HAS_Z, NL>(a, sT, sord, skeys, nw, S, rank);
 }
 
 // ----------------------------------------------------------------- backward
