@@ -107,8 +107,8 @@ SIGNATURES = {
     "bcm_restore_bwd": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_i64, c_p]),
     "bcm_restore_bwd_noalloc": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p]),
     "bcm_restore_bwd_sync_bytes": (c_i64, [c_i64, c_i64]),
-    "bcm_restore_bwd_chained": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_i64,
-                                        c_p]),
+    "bcm_restore_bwd_chained": (c_i32, [c_p, c_i32, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_i64, c_p,
+                                        c_i64, c_p]),
     "bcm_restore_proj_fwd": (c_i32, [c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_p, c_i64, c_p, c_p]),
     "bcm_restore_proj_bwd_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
     "bcm_restore_proj_bwd": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p, c_i64, c_p, c_p,

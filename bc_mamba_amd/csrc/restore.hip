@@ -395,11 +395,14 @@ constexpr int64_t kSyncHead = 2;           // sync words before the slots
 constexpr int kChainBlocksPerCu = 4;       // the kernel's launch bounds: 4 blocks of 256 fit a CU
 constexpr int kChainBatch = 4;             // slots a look-back round reads after its first
 
-template <typename TI>
+// TO: dy's type (fp32, or u's 16-bit type: the cast the reference's
+// autograd applies before the scan backward, rounded the same way).
+template <typename TI, typename TO>
 __global__ __launch_bounds__(256, kChainBlocksPerCu) void k_restore_bwd_chain(
     const TI* __restrict__ dout, int64_t n_events, const uint32_t* __restrict__ bitmask, int64_t W, int64_t mrd,
     const int32_t* __restrict__ tile_start, int nT, int nG, int waves, int wid0, int nblk, int dim, int64_t L,
-    int64_t n_rows, float* __restrict__ dy, uint64_t* __restrict__ sync) {
+    int64_t n_rows, TO* __restrict__ dy, uint64_t* __restrict__ sync) {
+  constexpr uint32_t SO = sizeof(TO);
   __shared__ uint2 s_run[4][kBwdStage];  // (value bits, destination)
   asm volatile("" ::"s"(tile_start), "s"(bitmask), "s"(dout), "s"(W), "s"(mrd), "s"(L), "s"(n_rows), "s"(sync));
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(256, kChainBlocksPerCu) void k_restore_bwd_chain(
   float gv[kTile];
 #pragma unroll
   for (int s = 0; s < kTile; ++s) gv[s] = buf_load<TI, kStream>(rg, s < steps ? lane_off + (uint32_t)s * row_bytes : kBufOOB);
-  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * 4);
+  const __amdgpu_buffer_rsrc_t rdy = buf_rsrc(dy + e_base, (n_events - e_base) * (int64_t)SO);
   const int nev = __popcll(m);
   const int incl = wave_incl_sum_dpp(nev);
   const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(256, kChainBlocksPerCu) void k_restore_bwd_chain(
     for (int s = 0; s < kTile; ++s) {
       const uint32_t bit = (uint32_t)(m >> s) & 1u;
       // the run of event (elo + r - 1) closes here when r >= 1
-      buf_store_f32(rdy, (bit && r) ? (ebase + r - 1) * 4u : kBufOOB, sum);
+      buf_store<TO>(rdy, (bit && r) ? (ebase + r - 1) * SO : kBufOOB, sum);
       r += bit;
       sum = (bit ? 0.0f : sum) + gv[s];
       hsum += s < first ? gv[s] : 0.0f;
@@ -527,14 +530,14 @@ __global__ __launch_bounds__(256, kChainBlocksPerCu) void k_restore_bwd_chain(
     for (int k = 0; k < total; k += kWave) {
       const int i = k + lane;
       const uint2 v = sr[i < total ? i : 0];
-      buf_store_f32(rdy, i < total ? v.y * 4u : kBufOOB, __uint_as_float(v.x));
+      buf_store<TO>(rdy, i < total ? v.y * SO : kBufOOB, __uint_as_float(v.x));
     }
   } else {
-    buf_store_f32(rdy, head ? ((uint32_t)(elo - e_base) - 1u) * 4u : kBufOOB, carry);
+    buf_store<TO>(rdy, head ? ((uint32_t)(elo - e_base) - 1u) * SO : kBufOOB, carry);
   }
   // the channel's last run: the tile's open run, or (no event in the tile)
   // the walked-back sum
-  if (last) buf_store_f32(rdy, (uint32_t)(tsN - 1 - e_base) * 4u, nev ? sum : carry);
+  if (last) buf_store<TO>(rdy, (uint32_t)(tsN - 1 - e_base) * SO, nev ? sum : carry);
 }
 
 static unsigned nblk(int64_t waves) { return (unsigned)((waves + 3) / 4); }
@@ -735,10 +738,13 @@ int64_t bcm_restore_bwd_sync_bytes(int64_t n_rows, int64_t L) {
 }
 
 int bcm_restore_bwd_chained(const void* dout, int dtype, const uint32_t* bitmask, int64_t mask_row_div,
-                            const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, float* dy,
-                            int64_t n_events, void* sync, int64_t sync_bytes, bcm_stream_t stream) {
+                            const int32_t* tile_start, int64_t n_rows, int64_t dim, int64_t L, void* dy,
+                            int dy_dtype, int64_t n_events, void* sync, int64_t sync_bytes, bcm_stream_t stream) {
   const char* fn = "bcm_restore_bwd_chained";
-  const int c = restore_bwd_checks(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L, dy, n_events);
+  if (dy_dtype != BCM_F32 && dy_dtype != dtype)
+    return set_error(BCM_EINVAL, "%s: dy must be fp32 or dout's dtype", fn);
+  const int c = restore_bwd_checks(fn, dout, dtype, bitmask, mask_row_div, tile_start, n_rows, dim, L,
+                                   static_cast<const float*>(dy), n_events);
   if (c) return c > 0 ? BCM_OK : -c;
   if (!sync || (reinterpret_cast<uintptr_t>(sync) & 7) != 0 || sync_bytes < bcm_restore_bwd_sync_bytes(n_rows, L))
     return set_error(BCM_EINVAL, "%s: an 8-byte aligned sync area of %lld bytes required", fn,
@@ -754,13 +760,19 @@ int bcm_restore_bwd_chained(const void* dout, int dtype, const uint32_t* bitmask
   const int64_t per_launch = (int64_t)cus * kChainBlocksPerCu * kTileWaves;
   dispatch_dtype(dtype, [&](auto tag) {
     using T = decltype(tag);
-    for (int64_t w0 = 0; w0 < waves; w0 += per_launch) {
-      const int64_t n = std::min(per_launch, waves - w0);
-      const int nb = (int)nblk(n);
-      hipLaunchKernelGGL(k_restore_bwd_chain<T>, dim3(nb), dim3(256), 0, hs(stream), static_cast<const T*>(dout),
-                         n_events, bitmask, W, mask_row_div, tile_start, (int)nT, (int)nG, (int)waves, (int)w0, nb,
-                         (int)dim, L, n_rows, dy, static_cast<uint64_t*>(sync));
-    }
+    auto go = [&](auto otag) {
+      using TO = decltype(otag);
+      for (int64_t w0 = 0; w0 < waves; w0 += per_launch) {
+        const int64_t n = std::min(per_launch, waves - w0);
+        const int nb = (int)nblk(n);
+        hipLaunchKernelGGL((k_restore_bwd_chain<T, TO>), dim3(nb), dim3(256), 0, hs(stream),
+                           static_cast<const T*>(dout), n_events, bitmask, W, mask_row_div, tile_start, (int)nT,
+                           (int)nG, (int)waves, (int)w0, nb, (int)dim, L, n_rows, static_cast<TO*>(dy),
+                           static_cast<uint64_t*>(sync));
+      }
+    };
+    if (dy_dtype == BCM_F32) go(float{});
+    else go(T{});
   });
   return check_launch(fn);
 }

@@ -38,7 +38,7 @@ class FusedStep:
     benchmark / serving workspace). After step(), the attributes hold the
     step's results: E, ms (max_seqlen), cu, k[:E], u[:E], tile_start,
     bitmask, y[:E] (scan out), xs (saved states), dense (restore out
-    [B, L, D]), dy32[:E] (restore backward), du[:E], dx ([B, D, L], the
+    [B, L, D]), dy_restore[:E] (restore backward), du[:E], dx ([B, D, L], the
     gather backward) and grads (dA, dW_B, dW_C, ddt_idle, ddt_active, dD)."""
 
     KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd"]
@@ -90,6 +90,7 @@ class FusedStep:
         self.rows.bitmask, self.rows.mask_row_div = self.bitmask.data_ptr(), 1
         self.rows.tile_start, self.rows.seqlen, self.rows.dx = self.tile_start.data_ptr(), L, self.dx.data_ptr()
         self.E = self.ms = -1
+        self.dy_out = self.dy32_buf
         self.chunk_g = self.split_ws = None
         self.events = {}
 
@@ -110,7 +111,9 @@ class FusedStep:
     k = property(lambda self: self.k_buf[:self.E])
     u = property(lambda self: self.u_buf[:self.E])
     y = property(lambda self: self.y_buf[:self.E])
-    dy32 = property(lambda self: self.dy32_buf[:self.E])
+    # the restore backward's dy as the step wrote it: fp32 (the two-pass
+    # form), or u's dtype (the one-kernel form)
+    dy_restore = property(lambda self: self.dy_out[:self.E])
     du = property(lambda self: self.du_buf[:self.E])
 
     @property
@@ -171,15 +174,19 @@ class FusedStep:
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y_buf), dt, E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense), dt, s))
         if self.restore_bwd == "chained":
+            # dy in the dtype the scan reads (u's): a 16-bit dy is rounded as
+            # the kernel stores it, no separate cast
+            self.dy_out = self.dy_buf
             mark("restore_bwd", lambda: nat.call("bcm_restore_bwd_chained", P(w.dout), dt, P(self.bitmask), 1,
-                                                 P(self.tile_start), self.NC, D, L, P(self.dy32_buf), E,
+                                                 P(self.tile_start), self.NC, D, L, P(self.dy_buf), dt, E,
                                                  P(self.sync), 8 * self.sync.numel(), s))
         else:
+            self.dy_out = self.dy32_buf
             mark("restore_bwd", lambda: nat.call("bcm_restore_bwd", P(w.dout), dt, P(self.bitmask), 1,
                                                  P(self.tile_start), self.NC, D, L, P(self.dy32_buf), E,
                                                  P(self.ws), 4 * self.ws.numel(), s))
-        if self.dy_buf is not self.dy32_buf:  # the scan takes dout in u's dtype
-            self.dy_buf[:E].copy_(self.dy32_buf[:E])
+            if self.dy_buf is not self.dy32_buf:  # the scan takes dout in u's dtype
+                self.dy_buf[:E].copy_(self.dy32_buf[:E])
         # the scan backward writes du and the dense dx rows (the gather
         # backward) in one kernel where the shape allows, else in two
         mark("scan_bwd", lambda: nat.call("bcm_scan_bwd_rows", self.args, self.rows, s))

@@ -474,7 +474,10 @@ int64_t bcm_restore_bwd_sync_bytes(int64_t n_rows, int64_t L);
  * look-back over the preceding tiles' published partials instead of a
  * second pass. Sums within a run follow a different order than
  * bcm_restore_bwd where a run crosses two or more tile edges (fp32
- * rounding; equal otherwise).
+ * rounding; equal otherwise). dy_dtype: BCM_F32 (the reference's dy), or
+ * dout's 16-bit dtype: the fp32 sums rounded to nearest even as stored,
+ * the cast the reference's autograd applies to dy before the scan
+ * backward (e_model.py's RestoreDenseFn feeding SelectiveScanFlatChFn).
  * `sync` (8-byte aligned, sync_bytes >= bcm_restore_bwd_sync_bytes) must
  * be zero before its first use; every call that completes leaves it zero
  * again, so a caller zeroes it once and reuses it. Word 1 (uint64) becomes
@@ -483,9 +486,9 @@ int64_t bcm_restore_bwd_sync_bytes(int64_t n_rows, int64_t L);
  * (one stream); calls with separate areas may overlap. */
 int bcm_restore_bwd_chained(const void* dout, int dtype, const uint32_t* bitmask,
                             int64_t mask_row_div, const int32_t* tile_start,
-                            int64_t n_rows, int64_t dim, int64_t L, float* dy,
-                            int64_t n_events, void* sync, int64_t sync_bytes,
-                            bcm_stream_t stream);
+                            int64_t n_rows, int64_t dim, int64_t L, void* dy,
+                            int dy_dtype, int64_t n_events, void* sync,
+                            int64_t sync_bytes, bcm_stream_t stream);
 
 /* ---- (3') restore -> out_proj ------------------------------------------- */
 /* The block's restore followed by its output projection (e_model.py:499-504:

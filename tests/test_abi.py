@@ -104,13 +104,16 @@ def test_restore_bwd_chained_checks_before_launch(lib):
     need = 8 * (2 + n_rows * nat.tile_count(L))
     assert lib.bcm_restore_bwd_sync_bytes(n_rows, L) == need
     assert lib.bcm_restore_bwd_sync_bytes(-1, L) == 0
-    args = (16, 0, 16, 1, 16, n_rows, 64, L, 16, 10)
+    args = (16, 0, 16, 1, 16, n_rows, 64, L, 16, 0, 10)
     assert lib.bcm_restore_bwd_chained(*args, None, need, None) == 1
     assert "sync area of %d bytes" % need in lib.bcm_last_error().decode()
     assert lib.bcm_restore_bwd_chained(*args, 16, need - 8, None) == 1
     assert lib.bcm_restore_bwd_chained(*args, 12, need, None) == 1  # not 8-byte aligned
-    assert lib.bcm_restore_bwd_chained(16, 0, 16, 1, 16, n_rows, 60, L, 16, 10, 16, need, None) == 1
+    assert lib.bcm_restore_bwd_chained(16, 0, 16, 1, 16, n_rows, 60, L, 16, 0, 10, 16, need, None) == 1
     assert "divisible by dim" in lib.bcm_last_error().decode()
+    # dy in fp32 or dout's dtype only
+    assert lib.bcm_restore_bwd_chained(16, 2, 16, 1, 16, n_rows, 64, L, 16, 1, 10, 16, need, None) == 1
+    assert "dy must be fp32 or dout's dtype" in lib.bcm_last_error().decode()
 
 
 def test_restore_proj_checks_before_launch(lib):

@@ -24,8 +24,8 @@ def _chained(dout, index, n_ch, dim, L, n_events, sync):
     bm, ts, mrd = index
     dy = torch.full((n_events,), float("nan"), device=dout.device)  # every entry must be written
     nat.call("bcm_restore_bwd_chained", nat.ptr(dout), nat.dtype_code(dout.dtype), nat.ptr(bm), int(mrd),
-             nat.ptr(ts), n_ch, dim, L, nat.ptr(dy), n_events, nat.ptr(sync), 8 * sync.numel(),
-             nat.stream_of(dout))
+             nat.ptr(ts), n_ch, dim, L, nat.ptr(dy), nat.dtype_code(dy.dtype), n_events, nat.ptr(sync),
+             8 * sync.numel(), nat.stream_of(dout))
     return dy
 
 
@@ -146,3 +146,27 @@ def test_restore_bwd_chained_no_events(cuda_device):
     dy = _chained(dout, (bm, ts, 1), B * D, D, L, 0, sync)
     assert dy.numel() == 0 and torch.count_nonzero(sync).item() == 0
     assert mem.sum() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_restore_bwd_chained_16bit_dy(cuda_device, dtype):
+    """dy stored in dout's 16-bit dtype: the fp32 dy of the same kernel,
+    rounded as torch rounds it (bit-equal), every entry written."""
+    print(f"chained restore bwd 16-bit dy {dtype}", flush=True)
+    B, D, L = 2, 256, 2048
+    g = torch.Generator().manual_seed(31)
+    mem = (torch.rand(B * D, L, generator=g) < 0.1).float()
+    mem[::7] = 0.0
+    ch, t, k, cu, counts, ms = orc.extract_base_events(mem.numpy()[None], 0.5)
+    E = len(t)
+    bm, ts = rd.build_event_index(_steps(t, cuda_device), torch.from_numpy(cu).to(cuda_device), L)
+    dout = torch.randn(B, L, D, generator=g).to(dtype).to(cuda_device)
+    sync = _sync(B * D, L, cuda_device)
+    dy32 = _chained(dout, (bm, ts, 1), B * D, D, L, E, sync)
+    dy16 = torch.full((E,), float("nan"), dtype=dtype, device=cuda_device)
+    nat.call("bcm_restore_bwd_chained", nat.ptr(dout), nat.dtype_code(dtype), nat.ptr(bm), 1, nat.ptr(ts), B * D, D,
+             L, nat.ptr(dy16), nat.dtype_code(dtype), E, nat.ptr(sync), 8 * sync.numel(), nat.stream_of(dout))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(sync).item() == 0
+    assert not torch.isnan(dy16).any()
+    assert torch.equal(dy16.cpu(), dy32.cpu().to(dtype))

@@ -38,7 +38,7 @@ def test_two_tower_calls_match_one_call(cuda_device, restore_bwd):
     finally:
         nat.set_scan_family(prev)
     assert one.E == sum(p.E for p in parts) and one.E > 0
-    for name in ("k", "u", "y", "dy32", "du"):
+    for name in ("k", "u", "y", "dy_restore", "du"):
         got = torch.cat([getattr(p, name) for p in parts])
         assert torch.equal(got, getattr(one, name)), name
     for name in ("dense", "dx"):
