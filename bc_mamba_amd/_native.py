@@ -157,9 +157,20 @@ def dtype_code(dtype):
         raise RuntimeError(f"bc_mamba_amd: unsupported dtype {dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_of_device(dev):
+    """The current torch stream of device dev as a hipStream_t (read without
+    building a torch Stream object where torch exposes the raw handle)."""
+    if _raw_stream is not None:
+        return c_p(_raw_stream(dev.index if dev.index is not None else torch.cuda.current_device()))
+    return c_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
 def stream_of(t):
     """The current torch stream of t's device as a hipStream_t."""
-    return c_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return stream_of_device(t.device)
 
 
 def bitmask_words(L):
@@ -222,13 +233,16 @@ class HostMeta:
         return c_p(self.t.data_ptr())
 
     def wait(self, stream, timeout_s=10.0):
-        """(E, max_seqlen) once written. Falls back to a stream sync (which
-        also makes any pending write visible) if polling times out."""
+        """(E, max_seqlen) once written. Falls back to a sync of `stream` (a
+        torch Stream, or a device whose current stream is meant), which also
+        makes any pending write visible, if polling times out."""
         import time
         t0 = time.perf_counter()
         v = self._v
         while v[0] < 0:
             if time.perf_counter() - t0 > timeout_s:
+                if not isinstance(stream, torch.cuda.Stream):
+                    stream = torch.cuda.current_stream(stream)
                 stream.synchronize()
                 if v[0] < 0:
                     raise RuntimeError("bc_mamba_amd: offsets kernel did not deliver the event count")

@@ -9,10 +9,14 @@ by the native library on the current stream.
 """
 import torch
 
+import threading
+
 try:
     from . import _native as _nat
+    from . import _provenance as _prov
 except ImportError:  # imported with this directory on sys.path
     import _native as _nat
+    import _provenance as _prov
 
 __all__ = ["extract_events", "extract_base_events", "expand_base_events",
            "gather_events_fwd", "gather_events_bwd", "extract_events_indexed"]
@@ -29,22 +33,37 @@ def _empty_i32(n, dev):
     return torch.empty(n, dtype=_I32, device=dev)
 
 
-def _count_scan(x2d, dtype_code, threshold, host_meta=False):
-    """Passes 1-2: bitmask, counts, cu_seqlens, meta=(E, max), on the device
-    or (host_meta) in pinned host memory that the offsets kernel writes
-    directly, read after an event sync with no copy kernel."""
+_metas = threading.local()
+
+
+def _host_meta(dev):
+    """This thread's pinned (E, max_seqlen) words for device dev. Every user
+    reads its values before returning, so one pair per thread and device
+    serves every call."""
+    d = getattr(_metas, "by_dev", None)
+    if d is None:
+        d = _metas.by_dev = {}
+    key = torch.device(dev).index
+    if key not in d:
+        d[key] = _nat.HostMeta()
+    return d[key]
+
+
+def _count_scan(x2d, dtype_code, threshold):
+    """Passes 1-2: bitmask, counts, cu_seqlens, and meta = (E, max) in pinned
+    host memory that the offsets kernel writes directly; meta.wait() polls
+    it (no copy kernel, no stream sync)."""
     NC, L = x2d.shape
     dev = x2d.device
     bitmask = torch.empty((NC, _nat.bitmask_words(L)), dtype=_I32, device=dev)
     counts = _empty_i32(NC, dev)
     cu = _empty_i32(NC + 1, dev)
-    meta = _nat.HostMeta() if host_meta else _empty_i32(2, dev)
-    if host_meta:
-        meta.arm()
+    meta = _host_meta(dev)
+    meta.arm()
     s = _nat.stream_of(x2d)
     _nat.call("bcm_extract_count", _nat.ptr(x2d), dtype_code, NC, L, float(threshold),
               _nat.ptr(bitmask), _nat.ptr(counts), s)
-    _nat.call("bcm_extract_scan", _nat.ptr(counts), NC, _nat.ptr(cu), meta.ptr() if host_meta else _nat.ptr(meta), s)
+    _nat.call("bcm_extract_scan", _nat.ptr(counts), NC, _nat.ptr(cu), meta.ptr(), s)
     return bitmask, counts, cu, meta
 
 
@@ -54,8 +73,15 @@ def extract_base_events(base_input, threshold):
 
     An event is float(base_input[b, d, t]) > float(threshold); events are
     channel-major (channel = b*d_model + d), time-ascending; k = t+1 for a
-    channel's first event, else the gap to the previous one. One host sync
-    reads the total event count to size the outputs, like the reference."""
+    channel's first event, else the gap to the previous one. The host reads
+    the total event count to size the outputs, like the reference (here by
+    polling pinned memory the offsets kernel writes, not by a stream sync).
+
+    The fill also writes the event index (bitmask and tile table), which is
+    kept on t_steps, and the host-read longest channel is kept on
+    cu_seqlens: restore_dense_fwd / _bwd, gather_events_bwd and the scan
+    read them instead of recomputing them while those tensors are unchanged
+    (bc_mamba_amd._provenance)."""
     _check(base_input.is_cuda, "base_input must be CUDA")
     _check(base_input.is_contiguous(), "base_input must be contiguous")
     _check(base_input.dim() == 3, "base_input must be 3-D [B, d_model, L]")
@@ -66,14 +92,17 @@ def extract_base_events(base_input, threshold):
     with torch.cuda.device(dev):
         x2d = base_input.view(B * Dm, L)
         bitmask, counts, cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold)
-        E = int(meta[0].item())
+        E, max_seqlen = meta.wait(dev)
+        _prov.attach_max_seqlen(cu, max_seqlen)
         if E == 0:
             ei = torch.zeros(0, dtype=_I32, device=dev)
             return [ei, ei, ei, cu, counts, torch.zeros(1, dtype=_I32, device=dev)]
         ch, t, k = _empty_i32(E, dev), _empty_i32(E, dev), _empty_i32(E, dev)
+        tile_start = torch.empty((B * Dm, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
         _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(cu), B * Dm, L, 1, None, 0,
-                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), None, None, None, _nat.stream_of(x2d))
-        return [ch, t, k, cu, counts, meta[1].clone()]
+                  _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), None, _nat.ptr(tile_start), None, _nat.stream_of(x2d))
+        _prov.attach_event_index(t, ch, cu, L, bitmask, tile_start)
+        return [ch, t, k, cu, counts, torch.full((), max_seqlen, dtype=_I32, device=dev)]
 
 
 def expand_base_events(base_ch_ids, base_t_steps, base_k_flat, base_cu_seqlens, B, d_model, expand):
@@ -106,6 +135,9 @@ def expand_base_events(base_ch_ids, base_t_steps, base_k_flat, base_cu_seqlens, 
                   _nat.ptr(k), _nat.ptr(cu), s)
         ms = torch.empty((), dtype=_I32, device=dev)
         _nat.call("bcm_seqlen_max", _nat.ptr(base_cu_seqlens), NC_base, _nat.ptr(ms), s)
+        base_max = _prov.max_seqlen_of(base_cu_seqlens)
+        if base_max is not None:  # every logical channel holds its base channel's events
+            _prov.attach_max_seqlen(cu, base_max)
         return [ch, t, k, cu, ms]
 
 
@@ -120,14 +152,15 @@ def extract_events(mask):
     with torch.cuda.device(dev):
         x2d = mask.view(B * D, L)
         bitmask, counts, cu, meta = _count_scan(x2d, _nat.U8, 0.5)
-        E = int(meta[0].item())
+        E, max_seqlen = meta.wait(dev)
+        _prov.attach_max_seqlen(cu, max_seqlen)
         if E == 0:
             ei = torch.zeros(0, dtype=_I32, device=dev)
             return [ei, ei, ei, cu, torch.zeros(1, dtype=_I32, device=dev), ei]
         ch, t, k, hf = (_empty_i32(E, dev) for _ in range(4))
         _nat.call("bcm_extract_fill", _nat.ptr(bitmask), _nat.ptr(cu), B * D, L, 1, None, 0,
                   _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), None, None, _nat.ptr(hf), _nat.stream_of(x2d))
-        return [ch, t, k, cu, meta[1].clone(), hf]
+        return [ch, t, k, cu, torch.full((), max_seqlen, dtype=_I32, device=dev), hf]
 
 
 def gather_events_fwd(x, channel_ids, time_steps):
@@ -152,7 +185,10 @@ def gather_events_fwd(x, channel_ids, time_steps):
 
 def gather_events_bwd(grad_x, channel_ids, time_steps, NC, L):
     """dx [NC, L] = 0 except dx[channel_ids[e], time_steps[e]] = grad_x[e]
-    -> [dx] (extract_events_cuda.cu:717-754). (ch, t) pairs must be unique."""
+    -> [dx] (extract_events_cuda.cu:717-754). (ch, t) pairs must be unique.
+    For the streams of extract_base_events (unchanged), dx is written row
+    by row from the extraction's event index (bcm_gather_bwd_rows: no zero
+    pass, no scatter; the same values)."""
     _check(grad_x.is_cuda, "gather_events_bwd: grad tensor must be CUDA")
     _check(channel_ids.dtype == _I32, "gather_events_bwd: channel_ids must be int32")
     _check(time_steps.dtype == _I32, "gather_events_bwd: time_steps must be int32")
@@ -160,6 +196,12 @@ def gather_events_bwd(grad_x, channel_ids, time_steps, NC, L):
     dx = torch.empty((NC, L), dtype=grad_x.dtype, device=grad_x.device)
     with torch.cuda.device(grad_x.device):
         g = grad_x.contiguous()
+        idx = _prov.event_index_for(time_steps, None, L, channel_ids)
+        if (idx is not None and idx[0].size(0) == NC and g.dim() == 1 and g.size(0) == time_steps.size(0)
+                and g.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            _nat.call("bcm_gather_bwd_rows", _nat.ptr(g), _nat.dtype_code(g.dtype), _nat.ptr(idx[0]), 1,
+                      _nat.ptr(idx[1]), NC, L, _nat.ptr(dx), _nat.stream_of(g))
+            return [dx]
         _nat.call("bcm_gather_bwd", _nat.ptr(g), _nat.dtype_code(g.dtype), _nat.ptr(channel_ids.contiguous()),
                   _nat.ptr(time_steps.contiguous()), int(g.size(0)), NC, L, _nat.ptr(dx), _nat.stream_of(g))
     return [dx]
@@ -172,9 +214,8 @@ def _extract_indexed_exact(base_input, threshold, expand, x, positions):
     dev = base_input.device
     with torch.cuda.device(dev):
         x2d = base_input.view(B * Dm, L)
-        bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold,
-                                                     host_meta=True)
-        E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
+        bitmask, counts, base_cu, meta = _count_scan(x2d, _nat.dtype_code(base_input.dtype), threshold)
+        E_base, max_seqlen = meta.wait(dev)
         NCi = B * Dm * expand
         cu = base_cu if expand == 1 else _empty_i32(NCi + 1, dev)
         s = _nat.stream_of(x2d)
@@ -276,7 +317,7 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
         ch, t = (_empty_i32(cap, dev), _empty_i32(cap, dev)) if positions else (None, None)
         tile_start = torch.empty((NCi, _nat.tile_count(L) + 1), dtype=_I32, device=dev)
         xe = torch.empty(cap, dtype=x.dtype, device=dev) if x is not None else None
-        meta = _nat.HostMeta()
+        meta = _host_meta(dev)
         meta.arm()
         if bits is not None:
             _nat.call("bcm_extract_count_bits", _nat.ptr(bitmask), NC, L, _nat.ptr(counts), _nat.ptr(bsums), s)
@@ -296,7 +337,7 @@ def extract_events_indexed(base_input, threshold, expand=1, x=None, positions=Tr
                       meta.ptr(), NC, L, expand, _nat.ptr(x), _nat.dtype_code(x.dtype), x.stride(0), x.stride(1),
                       Dm * expand, _nat.ptr(w), _nat.ptr(b), int(w.size(1)), int(bool(silu)), _nat.ptr(cu),
                       _nat.ptr(ch), _nat.ptr(t), _nat.ptr(k), _nat.ptr(xe), _nat.ptr(tile_start), s)
-        E_base, max_seqlen = meta.wait(torch.cuda.current_stream(dev))
+        E_base, max_seqlen = meta.wait(dev)
         E = E_base * expand
         # exact-size copies of the event streams, so that callers that keep
         # them (autograd saves k and x_events for the backward) hold E

@@ -16,8 +16,10 @@ import torch
 
 try:
     from . import _native as _nat
+    from . import _provenance as _prov
 except ImportError:  # imported with this directory on sys.path
     import _native as _nat
+    import _provenance as _prov
 
 __all__ = ["restore_dense_fwd", "restore_dense_bwd", "build_event_index", "restore_fwd_indexed",
            "restore_bwd_indexed", "restore_proj_fwd_indexed", "restore_proj_bwd_indexed"]
@@ -55,12 +57,52 @@ def restore_fwd_indexed(y_flat, event_index, n_ch, dim, seqlen, out_dtype=None):
     return out
 
 
-def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy):
+_sync_areas = {}  # (device index, stream handle) -> int64 tensor, zero between calls
+_cu_counts = {}  # device index -> compute units
+
+
+def _chained_fits(n_ch, dim, seqlen, dev):
+    """The one-kernel restore backward where its tile grid fits one launch
+    (at most 16 waves per compute unit), else the two-pass form: the
+    one-kernel form's later launches cannot overlap the earlier ones."""
+    key = dev.index
+    if key not in _cu_counts:
+        _cu_counts[key] = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves = (n_ch // dim) * _nat.tile_count(seqlen) * -(-dim // 64)
+    return waves <= 16 * _cu_counts[key]
+
+
+def _sync_area(dev, n_ch, seqlen):
+    """The stream's sync area for bcm_restore_bwd_chained, zeroed once when
+    it is made (or grown); every completed call leaves it zero. One area per
+    stream: the calls that share it are ordered by that stream."""
+    nbytes = int(_nat.lib().bcm_restore_bwd_sync_bytes(n_ch, seqlen))
+    key = (dev.index, _nat.stream_of_device(dev).value)
+    area = _sync_areas.get(key)
+    if area is None or 8 * area.numel() < nbytes:
+        area = _sync_areas[key] = torch.zeros(nbytes // 8, dtype=torch.int64, device=dev)
+    return area
+
+
+def restore_bwd_indexed(dout, event_index, n_ch, dim, seqlen, dy, chained=None):
     """Restore backward from an event index into the float32 dy (every
-    event's entry is written; no zero-init needed)."""
+    event's entry is written; no zero-init needed). chained: True for the
+    one-kernel form (bcm_restore_bwd_chained, whose look-back relies on the
+    index being the extraction's own), False for the two-pass form
+    (bcm_restore_bwd), None to choose by size (the one-kernel form where it
+    fits one launch)."""
     bitmask, tile_start, mrd = event_index
+    dev = dout.device
+    if chained is None:
+        chained = _chained_fits(n_ch, dim, seqlen, dev)
+    if chained:
+        area = _sync_area(dev, n_ch, seqlen)
+        _nat.call("bcm_restore_bwd_chained", _nat.ptr(dout), _nat.dtype_code(dout.dtype), _nat.ptr(bitmask),
+                  int(mrd), _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), _nat.F32,
+                  int(dy.numel()), _nat.ptr(area), 8 * area.numel(), _nat.stream_of(dout))
+        return dy
     ws = torch.empty(_nat.lib().bcm_restore_bwd_workspace_bytes(n_ch, seqlen) // 4, dtype=torch.float32,
-                     device=dout.device)
+                     device=dev)
     _nat.call("bcm_restore_bwd", _nat.ptr(dout), _nat.dtype_code(dout.dtype), _nat.ptr(bitmask), int(mrd),
               _nat.ptr(tile_start), n_ch, int(dim), int(seqlen), _nat.ptr(dy), int(dy.numel()), _nat.ptr(ws),
               4 * ws.numel(),
@@ -132,7 +174,8 @@ def restore_dense_fwd(y_flat, time_steps, cu_seqlens, dim, seqlen, out_dtype=Non
     if y_flat.numel() == 0:  # no events: every position precedes its channel's first event
         return torch.zeros((n_ch // dim, seqlen, dim), dtype=out_dtype, device=y_flat.device)
     with torch.cuda.device(y_flat.device):
-        bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen)
+        idx = _prov.event_index_for(time_steps, cu_seqlens, seqlen)  # the extraction's own, when unchanged
+        bitmask, tile_start = idx if idx is not None else build_event_index(time_steps, cu_seqlens, seqlen)
         return restore_fwd_indexed(y_flat, (bitmask, tile_start, 1), n_ch, dim, seqlen, out_dtype)
 
 
@@ -158,7 +201,11 @@ def restore_dense_bwd(dout, time_steps, cu_seqlens, dim, seqlen):
     if dy.numel() == 0:
         return dy
     with torch.cuda.device(dout.device):
-        bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen, zero_f32=dy)
-        if n_ch > 0:
-            restore_bwd_indexed(dout, (bitmask, tile_start, 1), n_ch, dim, seqlen, dy)
+        idx = _prov.event_index_for(time_steps, cu_seqlens, seqlen)
+        if idx is not None:  # the extraction's index: every event is in it, no zero-fill
+            restore_bwd_indexed(dout, idx + (1,), n_ch, dim, seqlen, dy)
+        else:
+            bitmask, tile_start = build_event_index(time_steps, cu_seqlens, seqlen, zero_f32=dy)
+            if n_ch > 0:
+                restore_bwd_indexed(dout, (bitmask, tile_start, 1), n_ch, dim, seqlen, dy, chained=False)
     return dy

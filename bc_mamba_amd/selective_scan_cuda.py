@@ -21,8 +21,10 @@ import torch
 
 try:
     from . import _native as _nat
+    from . import _provenance as _prov
 except ImportError:  # imported with this directory on sys.path
     import _native as _nat
+    import _provenance as _prov
 
 __all__ = ["fwd_flat_ch", "bwd_flat_ch"]
 
@@ -135,6 +137,13 @@ class _SeqlenStatus:
                                "for the scan)")
 
 
+def _needs_report(trusted, n_ch, cu_seqlens, max_seqlen):
+    """Whether a call reads the kernels' length report: not for callers that
+    computed max_seqlen themselves, nor for offsets whose longest channel the
+    extraction recorded (bc_mamba_amd._provenance) and max_seqlen covers."""
+    return not trusted and n_ch > 0 and not _prov.covers_max_seqlen(cu_seqlens, max_seqlen)
+
+
 def _acc_ptr(fn, acc, u_flat):
     """Device pointer of a per-event state-sum buffer (float32 [E]), or None."""
     if acc is None:
@@ -219,7 +228,9 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     In depthwise mode the kernels report a channel longer than max_seqlen
     and this call raises RuntimeError (one host sync to read the report);
     `_trusted_seqlen=True` skips the report for callers whose max_seqlen
-    comes from the extraction itself."""
+    comes from the extraction itself; so does a cu_seqlens returned by this
+    package's extraction (unchanged) with a max_seqlen at least its longest
+    channel, which the extraction recorded on it."""
     fn = "selective_scan_fwd_flat_ch"
     _check(u_flat.is_contiguous() and k_flat.is_contiguous() and cu_seqlens.is_contiguous(),
            f"{fn}: u_flat/k_flat/cu_seqlens must be contiguous")
@@ -244,7 +255,7 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         if mode == "depthwise":
             _nat.attach_chunk_g(a, _chunk_g)
             a.acc = _acc_ptr(fn, _acc, u_flat)
-            status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
+            status = _SeqlenStatus(fn, max_seqlen, dev, _needs_report(_trusted_seqlen, n_ch, cu_seqlens, max_seqlen))
             status.attach(a)
             _nat.call("bcm_scan_fwd", a, _nat.stream_of(u_flat))
             status.check()
@@ -323,7 +334,7 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
         a.dD = dD.data_ptr() if dD is not None else None
         a.dz = dz.data_ptr() if dz is not None else None
         if mode == "depthwise":
-            status = _SeqlenStatus(fn, max_seqlen, dev, not _trusted_seqlen and n_ch > 0)
+            status = _SeqlenStatus(fn, max_seqlen, dev, _needs_report(_trusted_seqlen, n_ch, cu_seqlens, max_seqlen))
             status.attach(a)
             a.dW_B, a.dW_C = dB.data_ptr(), dC.data_ptr()
             _, _, needs_g = _nat.scan_chunking(a)

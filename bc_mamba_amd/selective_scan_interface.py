@@ -74,10 +74,17 @@ class SelectiveScanFlatChFn(torch.autograd.Function):
             saved.extend([pw_B, pw_C])
         ctx.save_for_backward(*saved)
         ctx.mark_non_differentiable(x)
+        # x has no gradient: autograd passes None for it instead of a zero
+        # tensor (and None for out when the graph does not use it)
+        ctx.set_materialize_grads(False)
+        ctx.out_meta = (u_flat.shape, u_flat.dtype, u_flat.device)
         return (result[2] if ctx.has_z else out_flat), x
 
     @staticmethod
     def backward(ctx, dout, _dx):
+        if dout is None:
+            shape, dtype, dev = ctx.out_meta
+            dout = torch.zeros(shape, dtype=dtype, device=dev)
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         saved = list(ctx.saved_tensors)

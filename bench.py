@@ -490,6 +490,11 @@ def api_path_ms(w, dev, steps, warmup):
     x_conv = w.x_conv.detach().requires_grad_(True)
 
     def one():
+        # a training step's zero_grad(set_to_none=True): the backward writes
+        # fresh gradients instead of adding into the last step's
+        x_conv.grad = None
+        for p in params:
+            p.grad = None
         ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
         u = e_model.GatherEventsFn.apply(x_conv, ch, t)
         y, _ = selective_scan_flat_ch_fn(u, k, cu, int(ms), *params[:5], D=params[5], is_depthwise_bc=True)

@@ -1,0 +1,89 @@
+"""The drop-in API path reads what the extraction recorded on its outputs
+(the event index on t_steps, the longest channel on cu_seqlens) instead of
+recomputing it: restore forward / backward from the extraction's index (the
+backward in one kernel where it fits one launch), the gather backward row by
+row, the scan without its length report. Against the same path on copies of
+those tensors (no records: index rebuilt, zero-fill + scatter, two-pass
+restore backward, the report read), every result agrees."""
+import pytest
+import torch
+
+from bc_mamba_amd import _provenance as prov
+from bc_mamba_amd import e_model
+from bc_mamba_amd import extract_events_cuda as ee
+from bc_mamba_amd import restore_dense_cuda_nodecay as rdc
+from bc_mamba_amd.selective_scan_interface import selective_scan_flat_ch_fn
+from bc_mamba_amd.workloads import make_workload
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _path(w, strip):
+    x_conv = w.x_conv.detach().clone().requires_grad_(True)
+    params = [p.detach().clone().requires_grad_(True) for p in (w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, w.D_skip)]
+    ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+    if strip:
+        ch, t, cu = ch.clone(), t.clone(), cu.clone()
+        assert prov.event_index_for(t, cu, w.L) is None and prov.max_seqlen_of(cu) is None
+    else:
+        assert prov.event_index_for(t, cu, w.L, ch) is not None and prov.max_seqlen_of(cu) == int(ms)
+    u = e_model.GatherEventsFn.apply(x_conv, ch, t)
+    y, _ = selective_scan_flat_ch_fn(u, k, cu, int(ms), *params[:5], D=params[5], is_depthwise_bc=True)
+    out = e_model.restore_dense_fn(y, t, cu, w.D, w.L)
+    out.backward(w.dout)
+    return out.detach(), y.detach(), [x_conv.grad] + [p.grad for p in params]
+
+
+@pytest.mark.parametrize("cfg", [0, 1])
+def test_api_path_with_records_matches_without(cuda_device, cfg):
+    print(f"api records: config {cfg}", flush=True)
+    w = make_workload(cfg).to(cuda_device)
+    out_r, y_r, g_r = _path(w, strip=False)
+    out_s, y_s, g_s = _path(w, strip=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_r, y_s)
+    assert torch.equal(out_r, out_s)  # the same index, built twice
+    # dy: the one-kernel restore backward sums runs that cross two or more
+    # tile edges in another order than the two-pass form (fp32 rounding)
+    for name, a, b in zip(("x_conv", "dt_idle", "dt_active", "A", "W_B", "W_C", "D"), g_r, g_s):
+        assert_close(a.cpu(), b.cpu().numpy(), 1e-5, 1e-6, name)
+
+
+def test_extraction_index_equals_built_index(cuda_device):
+    w = make_workload(1, B=4).to(cuda_device)
+    ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+    bm, ts = prov.event_index_for(t, cu, w.L)
+    bm2, ts2 = rdc.build_event_index(t, cu, w.L)
+    assert torch.equal(bm, bm2) and torch.equal(ts, ts2)
+    assert int(ms) == int((cu[1:] - cu[:-1]).max())
+
+
+def test_changed_streams_fall_back(cuda_device):
+    w = make_workload(0).to(cuda_device)
+    ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+    y = torch.randn(t.numel(), device=cuda_device)
+    before = rdc.restore_dense_fwd(y, t, cu, w.D, w.L)
+    # move every channel's first event one step earlier where it can: the
+    # same tensor edited in place, still sorted per channel; the extraction's
+    # index no longer describes it and must not be used
+    first = cu[:-1][cu[1:] > cu[:-1]].long()
+    first = first[t[first] > 0]
+    assert first.numel() > 0
+    t[first] -= 1
+    assert prov.event_index_for(t, cu, w.L) is None
+    got = rdc.restore_dense_fwd(y, t, cu, w.D, w.L)
+    exp = rdc.restore_dense_fwd(y, t.clone(), cu.clone(), w.D, w.L)
+    assert torch.equal(got, exp) and not torch.equal(got, before)
+    dout = torch.randn_like(got)
+    assert torch.equal(rdc.restore_dense_bwd(dout, t, cu, w.D, w.L), rdc.restore_dense_bwd(dout, t.clone(), cu.clone(),
+                                                                                           w.D, w.L))
+
+
+def test_understated_max_seqlen_still_reported(cuda_device):
+    w = make_workload(0).to(cuda_device)
+    ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+    u = ee.gather_events_fwd(w.x_conv, ch, t)[0]
+    with pytest.raises(RuntimeError, match="more than max_seqlen"):
+        selective_scan_flat_ch_fn(u, k, cu, int(ms) - 1, w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, D=w.D_skip,
+                                  is_depthwise_bc=True)
