@@ -24,10 +24,7 @@
 //     and Σ_s W_B W_C g): each lane forms its states' weighted share for
 //     each of the block's 16 events, and a DPP reduce-scatter over the row
 //     leaves event j's sum in lane j (four halving steps, no LDS round trip
-//     and no wave barrier). The backward with one state per lane at two
-//     compute waves per SIMD keeps a padded LDS tile per row instead: state
-//     lane s writes its 16 shares at (q·17 + s), event lane j reads its 16
-//     at (j·17 + m), conflict-free both ways.
+//     and no wave barrier).
 //   * The forward saves the state h at the start of every 32-event pass in
 //     chunk_g; the backward walks a channel's passes last to first, rebuilds
 //     the pass's states (and, up to two states per lane, decays) in registers
@@ -52,7 +49,6 @@ namespace bcm {
 
 constexpr int kSLB = 16;                   // events per block (one per lane of a row)
 constexpr int kSLRows = kWave / kSLN;      // channels per wave
-constexpr int kSLTileSz = kSLN * (kSLN + 1);  // floats of one row's transpose tile (stride 17)
 constexpr int kSLPF = 4;                   // blocks per load round (a round ahead in flight)
 
 // Shape of the state-lane kernels with NL states per lane (dstate 16·NL).
@@ -212,20 +208,39 @@ __device__ __forceinline__ float row_sum(float v) {
 // (partners s and 15 - s, then mirrors within 8 lanes, then quad xors), each
 // lane keeping the half of its values that holds its own index and adding
 // its partner's copy of that half. All VALU (DPP), no LDS round trip.
+// The first two steps split the lanes by 4-lane bank (s < 8: banks 0-1;
+// s & 7 < 4: banks 0 and 2), so each of their outputs is two DPP adds into
+// one register, each writing only the banks that keep its half (bank_mask),
+// with no selects; the quad steps split inside a bank and select. Each asm
+// block starts with s_nop 1 (a DPP read needs two wait states after the
+// VALU write of its source, which may be the instruction just before the
+// block); inside a block every source was written before the block.
 __device__ __forceinline__ float row_reduce_scatter16(const float (&v)[kSLN]) {
   const int s = lane_id() & (kSLN - 1);
+  float a[8], b[4], c[2];
+#define BCM_MIRROR_PAIR(I, J, K)                                                  \
+  "v_add_f32_dpp %" #I ", %" #J ", %" #J " row_mirror row_mask:0xf bank_mask:0x3\n\t" \
+  "v_add_f32_dpp %" #I ", %" #K ", %" #K " row_mirror row_mask:0xf bank_mask:0xc\n\t"
+  asm("s_nop 1\n\t"
+      BCM_MIRROR_PAIR(0, 8, 16) BCM_MIRROR_PAIR(1, 9, 17) BCM_MIRROR_PAIR(2, 10, 18) BCM_MIRROR_PAIR(3, 11, 19)
+      BCM_MIRROR_PAIR(4, 12, 20) BCM_MIRROR_PAIR(5, 13, 21) BCM_MIRROR_PAIR(6, 14, 22) BCM_MIRROR_PAIR(7, 15, 23)
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(a[4]), "=&v"(a[5]), "=&v"(a[6]), "=&v"(a[7])
+      : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]),
+        "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]));
+#undef BCM_MIRROR_PAIR
+#define BCM_HALF_PAIR(I, J, K)                                                         \
+  "v_add_f32_dpp %" #I ", %" #J ", %" #J " row_half_mirror row_mask:0xf bank_mask:0x5\n\t" \
+  "v_add_f32_dpp %" #I ", %" #K ", %" #K " row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+  asm("s_nop 1\n\t"
+      BCM_HALF_PAIR(0, 4, 8) BCM_HALF_PAIR(1, 5, 9) BCM_HALF_PAIR(2, 6, 10) BCM_HALF_PAIR(3, 7, 11)
+      : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]));
+#undef BCM_HALF_PAIR
   auto add_dpp = [](float kp, float snd, auto ctrl) {
     constexpr int C = decltype(ctrl)::value;
     return kp + __uint_as_float(dpp<C>(__float_as_uint(snd)));
   };
-  float a[8], b[4], c[2];
-  const bool l8 = s < 8, l4 = (s & 7) < 4, l2 = (s & 3) < 2, l1 = (s & 1) == 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    a[i] = add_dpp(l8 ? v[i] : v[8 + i], l8 ? v[8 + i] : v[i], std::integral_constant<int, 0x140>{});  // row_mirror
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    b[i] = add_dpp(l4 ? a[i] : a[4 + i], l4 ? a[4 + i] : a[i], std::integral_constant<int, kDppHalfMirror>{});
+  const bool l2 = (s & 3) < 2, l1 = (s & 1) == 0;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
     c[i] = add_dpp(l2 ? b[i] : b[2 + i], l2 ? b[2 + i] : b[i], std::integral_constant<int, kDppXor2>{});
@@ -521,14 +536,14 @@ template <int NL, typename F> __device__ __forceinline__ void forj(F&& f) {
 // WR: the dense rows are written by the workgroup's row writers
 // (sl_row_writer) as the passes finish; the waves here publish, per slot,
 // the first event whose du is final in prog.
-// RS: the per-event sums over the row's states by DPP reduce-scatter
-// instead of the LDS tile. With several states per lane always (config 3
-// scan backward 180 -> 177 us); with one state per lane at one compute wave
-// per SIMD, where nothing hides the tile's round trips (config 2 39.0 ->
-// 36.5 us), not at two, where the other wave hides them and the
-// reduce-scatter's VALU costs more (config 1 38.6 -> 39.1 us).
-template <typename T, bool HAS_Z, bool DXR, int NL, bool WR, bool RS>
-__device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT, float* xt,
+// The per-event sums over the row's states go by DPP reduce-scatter, not
+// through an LDS transpose tile: config 3 scan backward 180 -> 177 us,
+// config 2 39.0 -> 36.5 us (one compute wave per SIMD, where nothing hides
+// the tile's round trips), config 1 cold step 136.3 -> 134.5 us once the
+// reduce-scatter's first halvings needed no selects (before that, the tile
+// won at config 1's two waves per SIMD: 38.6 against 39.1 us).
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR>
+__device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRows& rw, float* sT,
                                             float* sacc, float* sdu, int* sord, int* keys, int* prog, int nw, int S,
                                             int rank) {
   // no implicit fma contraction: the instantiations (with and without the
@@ -724,10 +739,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
                 g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2[t]));
                 gb[t * kSLB + Q][0] = g[0];
                 ab[t * kSLB + Q][0] = av[0][Q];
-                if constexpr (!USE) {
-                  if constexpr (RS) wq[Q] = wbcs[0] * g[0];
-                  else xt[Q * (kSLN + 1) + s] = wbcs[0] * g[0];
-                }
+                if constexpr (!USE) wq[Q] = wbcs[0] * g[0];
               } else {
                 const float x = bcast_f<Q>(du2[t]);
 #pragma unroll
@@ -740,24 +752,12 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
                   float w = wbcs[0] * g[0];  // the lane's states' share of Σ_s W_B W_C g_s
 #pragma unroll
                   for (int j = 1; j < NL; ++j) w = fmaf(wbcs[j], g[j], w);
-                  if constexpr (RS) wq[Q] = w;
-                  else xt[Q * (kSLN + 1) + s] = w;
+                  wq[Q] = w;
                 }
               }
             });
           });
-          if constexpr (!USE) {
-            if constexpr (RS) {
-              acc2[t] = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
-            } else {
-              wave_sync();
-              float acc = 0.0f;
-#pragma unroll
-              for (int m = 0; m < kSLN; ++m) acc += xt[s * (kSLN + 1) + m];
-              acc2[t] = acc;
-              wave_sync();
-            }
-          }
+          if constexpr (!USE) acc2[t] = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
         }
       };
       if (use_acc) phase_a(std::true_type{});
@@ -781,8 +781,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
             T0[0] += tg;
             fmac_bcast<Q, Q == kSLB - 1>(T1[0], km[t], tg);   // T1 += (k-1)·tg
             fmac_bcast<Q, Q == kSLB - 1>(dWB[0], du2[t], e);  // dWB += Δu²·e
-            if constexpr (RS) wq[Q] = wbcs[0] * e;
-            else xt[Q * (kSLN + 1) + s] = wbcs[0] * e;
+            wq[Q] = wbcs[0] * e;
           } else {
             const float dq = bcast_f<Q>(doutu[t]);
             float w = 0.0f;
@@ -799,20 +798,11 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
               fmac_bcast<Q, Q == kSLB - 1 && J == 0>(dWB[J], du2[t], e);  // dWB += Δu²·e
               w = J == 0 ? wbcs[0] * e : fmaf(wbcs[J], e, w);
             });
-            if constexpr (RS) wq[Q] = w;
-            else xt[Q * (kSLN + 1) + s] = w;
+            wq[Q] = w;
           }
         });
         });
-        float acc1 = 0.0f;
-        if constexpr (RS) {
-          acc1 = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
-        } else {
-          wave_sync();
-#pragma unroll
-          for (int m = 0; m < kSLN; ++m) acc1 += xt[s * (kSLN + 1) + m];
-          wave_sync();
-        }
+        const float acc1 = row_reduce_scatter16(wq);  // the row's states summed per event (DPP)
         // the lane's own event of block t: du, the Δu² terms of ddt, dD
         const int i = p * Sh::Pass + t * kSLB + s;
         const float duv = fmaf(gg[t], Dv + acc2[t], 2.0f * dl[t] * uv[t] * acc1);
@@ -994,15 +984,14 @@ __device__ void sl_row_writer(const bcm_scan_args& a, const ScanRows& rw, const 
   __syncthreads();  // the compute waves' final barrier
 }
 
-template <typename T, bool HAS_Z, bool DXR, int NL, bool WR = false, bool RS = false>
+template <typename T, bool HAS_Z, bool DXR, int NL, bool WR = false>
 __global__ __launch_bounds__(WR ? kScanThreads + 4 * kWave : kScanThreads) void k_scan_bwd_sl(
     const bcm_scan_args a, const ScanRows rw, int nw, int S, int rank) {
   __shared__ float sT[SLShape<NL>::TabSz];
-  __shared__ float sX[kScanThreads / kWave][kSLRows * kSLTileSz];
   __shared__ float sacc[kScanThreads / kWave * kSLRows * SLShape<NL>::NA];
   __shared__ int sord[kSortMax];
+  __shared__ int skeys[kSortMax];  // the ranking's scratch keys
   __shared__ int sprog[WR ? kScanThreads / kWave * kSLRows : 1];
-  static_assert(sizeof(sX) >= kSortMax * sizeof(int), "the transpose tiles hold the ranking keys");
   extern __shared__ float sdu[];  // DXR: [slots][kSLRowCap] each channel's du in event order
   const int wave = threadIdx.x / kWave, grp = lane_id() / kSLN;
   if constexpr (WR) {
@@ -1013,9 +1002,8 @@ __global__ __launch_bounds__(WR ? kScanThreads + 4 * kWave : kScanThreads) void 
   }
   // row writers need a single unranked round (the host's choice); rank 0
   // keeps the barrier count of both kinds of wave equal
-  sl_bwd_body<T, HAS_Z, DXR, NL, WR, RS>(a, rw, sT, &sX[wave][grp * kSLTileSz], sacc,
-                                     sdu + (wave * kSLRows + grp) * kSLRowCap, sord,
-                                     reinterpret_cast<int*>(&sX[0][0]), sprog, nw, S, WR ? 0 : rank);
+  sl_bwd_body<T, HAS_Z, DXR, NL, WR>(a, rw, sT, sacc, sdu + (wave * kSLRows + grp) * kSLRowCap, sord, skeys, sprog,
+                                     nw, S, WR ? 0 : rank);
 }
 
 // ------------------------------------------------------------------- host
@@ -1100,16 +1088,12 @@ int sl_launch_fwd(const bcm_scan_args& a, hipStream_t st, const char* fn) {
 template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, dim3 grid, dim3 block, int nw, int S,
                                         int rank, const ScanRows* rw) {
   const ScanRows rows = rw ? *rw : ScanRows{};
-  // one compute wave per SIMD (the grid's waves fit the SIMDs once): the
-  // per-event state sums by DPP reduce-scatter (RS)
-  const bool rs = (int64_t)grid.x * nw <= 4ll * device_cus();
   dispatch_dtype(a.dtype, [&](auto tag) {
     using T = decltype(tag);
     if constexpr (NL == 1) {
       auto go = [&](auto z, auto dxr, auto wr, dim3 blk, size_t lds) {
         constexpr bool Z = decltype(z)::value, X = decltype(dxr)::value, W = decltype(wr)::value;
-        if (rs) hipLaunchKernelGGL((k_scan_bwd_sl<T, Z, X, 1, W, true>), grid, blk, lds, st, a, rows, nw, S, rank);
-        else hipLaunchKernelGGL((k_scan_bwd_sl<T, Z, X, 1, W, false>), grid, blk, lds, st, a, rows, nw, S, rank);
+        hipLaunchKernelGGL((k_scan_bwd_sl<T, Z, X, 1, W>), grid, blk, lds, st, a, rows, nw, S, rank);
       };
       using Y = std::true_type;
       using F = std::false_type;
@@ -1131,8 +1115,8 @@ template <int NL> static void sl_bwd_nl(const bcm_scan_args& a, hipStream_t st, 
       if (a.z) go(Y{}, F{}, F{}, block, 0);
       else go(F{}, F{}, F{}, block, 0);
     } else {
-      if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL, false, true>), grid, block, 0, st, a, rows, nw, S, rank);
-      else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL, false, true>), grid, block, 0, st, a, rows, nw, S, rank);
+      if (a.z) hipLaunchKernelGGL((k_scan_bwd_sl<T, true, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
+      else hipLaunchKernelGGL((k_scan_bwd_sl<T, false, false, NL>), grid, block, 0, st, a, rows, nw, S, rank);
     }
   });
 }
