@@ -83,6 +83,7 @@ SIGNATURES = {
     "bcm_scan_fwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd": (c_i32, [ctypes.POINTER(ScanArgs), c_p]),
     "bcm_scan_bwd_rows": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanRows), c_p]),
+    "bcm_scan_bwd_rows_fused": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanRows)]),
     "bcm_scan_bwd_workspace_bytes": (c_i64, [ctypes.POINTER(ScanArgs)]),
     "bcm_set_scan_family": (c_i32, [c_i32]),
     "bcm_scan_chunking": (c_i32, [ctypes.POINTER(ScanArgs), ctypes.POINTER(c_i32), ctypes.POINTER(c_i32),

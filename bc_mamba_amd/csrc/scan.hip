@@ -425,7 +425,7 @@ __global__ __launch_bounds__((kScanThreadsG<G, true>)) void k_scan_bwd(const bcm
 
   const int64_t E = a.n_events;
   const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
-  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
+  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, a.du ? E * SZ : 0);  // no du: the dense rows alone (stores dropped)
   const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
   const int NC = a.n_channels, dim = a.dim, nck = a.n_chunks;
@@ -1132,7 +1132,9 @@ static int scan_entry(const bcm_scan_args* ap, bcm_stream_t stream, const char* 
   } else {
     if (!a.dA || !a.dW_B || !a.dW_C || !a.ddt_idle || !a.ddt_active)
       return set_error(BCM_EINVAL, "%s: null gradient pointer", fn);
-    if (a.n_events > 0 && (!a.dout || !a.du)) return set_error(BCM_EINVAL, "%s: null dout/du pointer", fn);
+    // du may be NULL when the kernel writes the dense rows itself (rw): the
+    // rows then carry the only copy of it
+    if (a.n_events > 0 && (!a.dout || (!a.du && !rw))) return set_error(BCM_EINVAL, "%s: null dout/du pointer", fn);
     int pass_len, n_pass, needs_g;
     chunking(a, &pass_len, &n_pass, &needs_g);
     if (needs_g && !a.chunk_g)
@@ -1164,8 +1166,8 @@ int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream) {
   return bcm::scan_entry<true>(args, stream, "bcm_scan_bwd");
 }
 
-int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_stream_t stream) {
-  const char* fn = "bcm_scan_bwd_rows";
+// bcm_scan_bwd_rows' argument checks; *fused: whether it runs as one kernel.
+static int rows_plan(const bcm_scan_args* args, const bcm_scan_rows* rows, const char* fn, bool* fused) {
   if (!args || !rows) return bcm::set_error(BCM_EINVAL, "%s: null argument", fn);
   const bcm_scan_rows& r = *rows;
   if (r.seqlen < 0 || r.mask_row_div < 1) return bcm::set_error(BCM_EINVAL, "%s: invalid seqlen / mask_row_div", fn);
@@ -1174,8 +1176,25 @@ int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_
     if ((reinterpret_cast<uintptr_t>(r.bitmask) & 7) != 0)
       return bcm::set_error(BCM_EINVAL, "%s: bitmask must be 8-byte aligned", fn);
   }
-  if (args->n_channels < 1 || r.seqlen == 0 || !bcm::dtype_ok(args->dtype) || !bcm::rows_fusable(*args, r)) {
+  *fused = args->n_channels >= 1 && r.seqlen > 0 && bcm::dtype_ok(args->dtype) && bcm::rows_fusable(*args, r);
+  return BCM_OK;
+}
+
+int bcm_scan_bwd_rows_fused(const bcm_scan_args* args, const bcm_scan_rows* rows) {
+  bool fused = false;
+  const int rc = rows_plan(args, rows, "bcm_scan_bwd_rows_fused", &fused);
+  return rc ? -rc : (fused ? 1 : 0);
+}
+
+int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_stream_t stream) {
+  const char* fn = "bcm_scan_bwd_rows";
+  bool fused = false;
+  if (const int rc = rows_plan(args, rows, fn, &fused)) return rc;
+  const bcm_scan_rows& r = *rows;
+  if (!fused) {
     // two steps: the scan backward, then the rows from du
+    if (args->n_events > 0 && !args->du)
+      return bcm::set_error(BCM_EINVAL, "%s: du required where the rows are written from it in a second pass", fn);
     int rc = bcm::scan_entry<true>(args, stream, fn);
     if (rc) return rc;
     return bcm_gather_bwd_rows(args->du, args->dtype, r.bitmask, r.mask_row_div, r.tile_start, args->n_channels,

@@ -592,7 +592,7 @@ __device__ __forceinline__ void sl_bwd_body(const bcm_scan_args& a, const ScanRo
 
   const int64_t E = a.n_events;
   const __amdgpu_buffer_rsrc_t ru = buf_rsrc(a.u, E * SZ), rk = buf_rsrc(a.k, E * 4);
-  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, E * SZ);
+  const __amdgpu_buffer_rsrc_t rdo = buf_rsrc(a.dout, E * SZ), rdu = buf_rsrc(a.du, a.du ? E * SZ : 0);  // no du: the dense rows alone (stores dropped)
   const __amdgpu_buffer_rsrc_t rz = buf_rsrc(a.z, HAS_Z ? E * SZ : 0), ros = buf_rsrc(a.out_saved, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rdz = buf_rsrc(a.dz, HAS_Z ? E * SZ : 0);
   const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.chunk_g, a.chunk_g ? a.chunk_g_bytes : 0);

@@ -152,12 +152,14 @@ def _event_scan_bwd(ctx, saved, dout, rows=None):
     """(du, dt_idle, dt_active, dA, dW_B, dW_C, dD) of the fused block's scan
     from the tensors _event_scan_fwd saved; with rows = (bitmask, expand,
     tile_start, dx) the scan kernel also writes the dense gather backward
-    into dx."""
+    into dx, and du (which then has no other use) is None where that kernel
+    writes the rows itself."""
     x_ev, k_flat, cu_seqlens, dt_idle, dt_active, A, W_B, W_C, xs = saved[:9]
     D = saved[9] if ctx.has_D else None
     res = selective_scan_cuda.bwd_flat_ch(x_ev, k_flat, cu_seqlens, ctx.max_seqlen, dt_idle, dt_active, A, W_B, W_C,
                                           dout.contiguous(), xs, D, is_depthwise_bc=True, _chunk_g=ctx.chunk_g,
-                                          _rows=rows, _trusted_seqlen=True, _acc=ctx.acc)
+                                          _rows=rows, _trusted_seqlen=True, _acc=ctx.acc,
+                                          _discard_du=rows is not None)
     du, dA, dW_B, dW_C, ddt_idle, ddt_active = res[:6]
     return du, ddt_idle, ddt_active, dA, dW_B, dW_C, (res[6] if D is not None else None)
 

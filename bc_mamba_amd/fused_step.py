@@ -43,20 +43,25 @@ class FusedStep:
 
     KERNELS = ["count", "fill", "scan_fwd", "restore_fwd", "restore_bwd", "scan_bwd"]
 
-    def __init__(self, w, dev, restore_bwd="auto"):
+    def __init__(self, w, dev, restore_bwd="auto", keep_du=True):
         """restore_bwd: "chained" (one kernel, bcm_restore_bwd_chained),
         "two_pass" (tile pass + fix-up pass, bcm_restore_bwd) or "auto": the
         chained form where its tile grid fits one launch (at most 4 blocks
         of 4 waves per CU; configs 1 and 2), else the two-pass form (the
         chained form's later launches cannot overlap the earlier ones:
-        config 3, 54 against 40 us)."""
+        config 3, 54 against 40 us).
+        keep_du=False: the step's gradient output is dx (the path's input
+        gradient); where the scan backward writes dx's rows itself it then
+        stores no separate du stream (dx holds the same values at the
+        events), as the model's backward does. self.du is then not
+        written."""
         if restore_bwd not in ("auto", "chained", "two_pass"):
             raise ValueError(f"restore_bwd must be 'auto', 'chained' or 'two_pass', not {restore_bwd!r}")
         if restore_bwd == "auto":
             waves = w.B * nat.tile_count(w.L) * -(-w.D // 64)
             cus = torch.cuda.get_device_properties(dev).multi_processor_count
             restore_bwd = "chained" if waves <= 16 * cus else "two_pass"
-        self.w, self.dev, self.restore_bwd = w, dev, restore_bwd
+        self.w, self.dev, self.restore_bwd, self.keep_du = w, dev, restore_bwd, keep_du
         B, D, L = w.B, w.D, w.L
         self.NC = B * D
         i32 = dict(dtype=torch.int32, device=dev)
@@ -170,6 +175,9 @@ class FusedStep:
             self.split_ws = torch.empty(max(nb, 4) // 4, dtype=torch.float32, device=self.dev) if nb else None
             a.split_ws = self.split_ws.data_ptr() if nb else None
             a.split_ws_bytes = nb
+            a.du = self.du_buf.data_ptr()
+            if not self.keep_du and nat.lib().bcm_scan_bwd_rows_fused(a, self.rows) == 1:
+                a.du = None
         mark("scan_fwd", lambda: nat.call("bcm_scan_fwd", self.args, s))
         mark("restore_fwd", lambda: nat.call("bcm_restore_fwd", P(self.y_buf), dt, E, P(self.bitmask), 1,
                                              P(self.tile_start), self.NC, D, L, P(self.dense), dt, s))

@@ -267,7 +267,8 @@ def fwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
 
 def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B, C, dout_flat, x,
                 D=None, z=None, out=None, tile_offsets=None, tile_chunk_size=0, is_depthwise_bc=False,
-                pw_B=None, pw_C=None, _chunk_g=None, _rows=None, _trusted_seqlen=False, _acc=None):
+                pw_B=None, pw_C=None, _chunk_g=None, _rows=None, _trusted_seqlen=False, _acc=None,
+                _discard_du=False):
     """Flat per-channel scan backward -> [du, dA, dB, dC, ddt_idle,
     ddt_active, (dD), (dz), (dpw_B, dpw_C)] (selective_scan.cpp:890-1153).
     dB / dC are dW_B / dW_C [dim, dstate] in depthwise mode and have the
@@ -279,6 +280,9 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
     receives the gather backward of du (du at the events, 0 elsewhere).
     `_acc`: the per-event state sums a fwd_flat_ch(_acc=...) of the same
     inputs wrote (depthwise mode), read instead of rebuilt.
+    `_discard_du` (with `_rows`): a caller that needs only dx; where the
+    scan kernel writes the rows itself, du is not stored and the result's
+    du slot is None (dx holds the same values at the events).
     As fwd_flat_ch, raises RuntimeError when a channel holds more than
     max_seqlen events (unless `_trusted_seqlen`)."""
     fn = "selective_scan_bwd_flat_ch"
@@ -366,6 +370,8 @@ def bwd_flat_ch(u_flat, k_flat, cu_seqlens, max_seqlen, dt_idle, dt_active, A, B
                 r = _nat.ScanRows()
                 r.bitmask, r.mask_row_div, r.tile_start = bitmask.data_ptr(), int(mrd), tile_start.data_ptr()
                 r.seqlen, r.dx = int(dx.size(1)), dx.data_ptr()
+                if _discard_du and _nat.lib().bcm_scan_bwd_rows_fused(a, r) == 1:
+                    a.du, du = None, None
                 _nat.call("bcm_scan_bwd_rows", a, r, s)
             status.check()
             if pw_B is not None:  # dB, dC hold dW_eff here

@@ -64,27 +64,31 @@ def algorithmic_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, expand=1):
     }
 
 
-def own_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o):
+def own_bytes(B, D, L, N, E, max_seqlen, s_m, s_u, s_o, dy_direct=False, du_stream=True):
     """Compulsory traffic of this build's own kernel interfaces for the same
     step (each tensor once): the fill writes k and u but no ch / t streams;
     restore and the gather backward read the event index (a bitmask of one
     bit per step and a tile table of one int32 per 64 steps) instead of t
-    and ch; dy is fp32 and, for 16-bit u, copied once to u's dtype for the
-    scan backward. The reference interface's figure (algorithmic_bytes) is
-    the metric's numerator; this one says how close the kernels run to
-    their own floor."""
+    and ch; dy is written in u's dtype by the one-kernel restore backward
+    (dy_direct), else as fp32 and, for 16-bit u, copied once to u's dtype
+    for the scan backward; the scan backward stores du only with du_stream
+    (else dx's rows are its only copy). The reference interface's figure
+    (algorithmic_bytes) is the metric's numerator; this one says how close
+    the kernels run to their own floor."""
     M, NC = B * D * L, B * D
     n_ch = max(1, -(-max_seqlen // 2048))
     st = NC * n_ch * N * 8
     index = M // 8 + NC * (-(-L // 64) + 1) * 4  # bitmask + tile table
-    dy_copy = 0 if s_u == 4 else E * 4 + E * s_u
+    dy_w = E * s_u if dy_direct else E * 4
+    dy_copy = 0 if (s_u == 4 or dy_direct) else E * 4 + E * s_u
     return {
         "count": M * s_m + M // 8 + NC * 4,
         "fill": M // 8 + NC * 4 + M * s_u + E * 4 + E * s_u + index - M // 8 + 4 * (NC + 1),
         "scan_fwd": E * s_u + E * 4 + E * s_u + st,
         "restore_fwd": E * s_u + index + M * s_o,
-        "restore_bwd": M * s_o + index + E * 4,
-        "scan_bwd": E * s_u + E * 4 + E * s_u + st + E * s_u + index + M * s_u + dy_copy,
+        "restore_bwd": M * s_o + index + dy_w,
+        "scan_bwd": (E * s_u + E * 4 + E * s_u + st + (E * s_u if du_stream else 0) + index + M * s_u
+                     + dy_copy),
     }
 
 
@@ -204,6 +208,9 @@ def main():
     ap.add_argument("--restore-bwd", choices=["auto", "chained", "two_pass"], default="auto",
                     help="restore backward form: one kernel with look-back, tile pass + fix-up pass, or the "
                          "first where its tile grid fits one launch")
+    ap.add_argument("--du-stream", action="store_true",
+                    help="also store the scan backward's du stream (the step's input gradient is dx, whose rows "
+                         "the scan backward writes itself; du is the reference's intermediate before its scatter)")
     ap.add_argument("--no-peak", action="store_true",
                     help="config 4: skip the peak-memory steps (fused and reference composition) after timing")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
@@ -223,7 +230,7 @@ def main():
         print(json.dumps(model_step_bench(args, dev)), flush=True)
         return
     w = make_workload(args.cfg).to(dev)
-    path = FusedStep(w, dev, restore_bwd=args.restore_bwd)
+    path = FusedStep(w, dev, restore_bwd=args.restore_bwd, keep_du=args.du_stream)
 
     if args.pmc_child:  # a few steps and the calibration copy, run under rocprofv3 --pmc by the parent
         for _ in range(3):
@@ -267,7 +274,8 @@ def main():
     su = torch.tensor([], dtype=w.dtype).element_size()
     alg = algorithmic_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su)
     total_bytes = sum(alg.values())
-    own_total = sum(own_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su).values())
+    own_total = sum(own_bytes(w.B, w.D, w.L, w.N, E, ms, 4, su, su, dy_direct=path.restore_bwd == "chained",
+                              du_stream=path.args.du is not None).values())
     # algorithmic bytes of one launch of each kernel (its share of the API-contract traffic)
     kernel_bytes = {"count": w.B * w.D * w.L * 4 + 4 * path.NC,
                     "fill": alg["fwd_extract_gather"] - w.B * w.D * w.L * 4, "scan_fwd": alg["fwd_scan"],
@@ -293,6 +301,9 @@ def main():
                    "B": w.B, "D": w.D, "L": w.L, "N": w.N, "events": E, "density": E / (w.B * w.D * w.L),
                    "max_seqlen": ms},
         "restore_bwd_form": path.restore_bwd,
+        # whether the scan backward also stored du (the reference's
+        # intermediate before its scatter into dx); dx is written either way
+        "du_stream": path.args.du is not None,
         "achieved_gbs": total_bytes / (ms_per_step * 1e-3) / 1e9,
         "algorithmic_bytes": total_bytes,
         # the same time against this build's own compulsory traffic (no ch /
@@ -361,7 +372,7 @@ def towers_bench(w, dev, args):
     """Cold and warm step time of the two-call encoding (same protocol as
     the headline figure)."""
     import torch
-    two = TwoTowers(w, dev, restore_bwd=args.restore_bwd)
+    two = TwoTowers(w, dev, restore_bwd=args.restore_bwd, keep_du=args.du_stream)
     for _ in range(args.warmup):
         two.step()
     cold = cold_steps_ms(two, dev, args.steps)

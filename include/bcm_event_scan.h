@@ -320,7 +320,11 @@ int bcm_scan_bwd(const bcm_scan_args* args, bcm_stream_t stream);
  * on du. bitmask / tile_start are the extraction's event index
  * (bcm_extract_indexed) and must describe the events of cu_seqlens. One
  * kernel for single-pass 16-lane shapes without z and seqlen % 4 == 0
- * (dx aligned to 4 elements); otherwise the two steps run in turn. */
+ * (dx aligned to 4 elements); otherwise the two steps run in turn. When it
+ * runs as one kernel (bcm_scan_bwd_rows_fused), args->du may be NULL: dx
+ * then holds the only copy of du (a caller that needs only dx, as the
+ * model's backward, skips the du stream); in the two-step case a NULL du
+ * is BCM_EINVAL. */
 typedef struct bcm_scan_rows {
   const uint32_t* bitmask;    /* [n_channels / mask_row_div, words], 8-byte aligned */
   int64_t mask_row_div;       /* channel ch reads bitmask row ch / mask_row_div */
@@ -329,6 +333,10 @@ typedef struct bcm_scan_rows {
   void* dx;                   /* [n_channels, L] */
 } bcm_scan_rows;
 int bcm_scan_bwd_rows(const bcm_scan_args* args, const bcm_scan_rows* rows, bcm_stream_t stream);
+/* 1 when bcm_scan_bwd_rows(args, rows) runs as one kernel (and so accepts a
+ * NULL args->du), 0 when it runs the two steps, negative for invalid
+ * arguments. Enqueues nothing. No counterpart in the reference. */
+int bcm_scan_bwd_rows_fused(const bcm_scan_args* args, const bcm_scan_rows* rows);
 
 /* B and C of the non-depthwise modes of fwd_flat_ch / bwd_flat_ch
  * (selective_scan.cpp:760-776, 840-848, 969-990, 1085-1090):

@@ -74,6 +74,13 @@ def test_scan_rows_arguments_are_rejected_before_launch(lib):
     assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "null index" in lib.bcm_last_error().decode()
     r.bitmask, r.tile_start, r.dx = 20, 16, 16  # never dereferenced: rejected first
     assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "8-byte aligned" in lib.bcm_last_error().decode()
+    assert lib.bcm_scan_bwd_rows_fused(a, r) < 0 and "8-byte aligned" in lib.bcm_last_error().decode()
+    # a shape the one kernel does not take (seqlen % 4 != 0): the rows come
+    # from du in a second pass, so du cannot be left out
+    r.bitmask, r.seqlen = 16, 63
+    a.n_events, a.dout = 10, 16
+    assert lib.bcm_scan_bwd_rows_fused(a, r) == 0
+    assert lib.bcm_scan_bwd_rows(a, r, None) == 1 and "du required" in lib.bcm_last_error().decode()
 
 
 def test_header_constants_match_binding():
