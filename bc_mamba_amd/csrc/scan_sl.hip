@@ -326,14 +326,22 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
   const float al = sl_table_al<NL>(a, d);  // the table build waits for this load alone
   const float dti = a.dt_idle[d], dta = a.dt_active[d];
   const float Dv = a.D ? a.D[d] : 0.0f;
-  float Al[NL], wb[NL], cw[NL];  // the lane's states s + 16j
+  float Al[NL], wb[NL], cw[NL], rwc[NL];  // the lane's states s + 16j
 #pragma unroll
   for (int j = 0; j < NL; ++j) {
     const int64_t ix = (int64_t)d * N + s + kSLN * j;
     Al[j] = a.A[ix] * kLog2e;
     wb[j] = a.W_B[ix];
-    cw[j] = wb[j] * a.W_C[ix];  // one state per lane: W_B W_C of the lane's own state
+    const float wc = a.W_C[ix];
+    cw[j] = wb[j] * wc;  // one state per lane: W_B W_C of the lane's own state
+    rwc[j] = 1.0f / wc;
   }
+  // One state per lane: the recurrence runs on the state's share of y,
+  // q = W_B W_C g (q = a q + W_B W_C Δu², one DPP multiply and one fma per
+  // event instead of a DPP move, an fma and a multiply), the saved states
+  // being q / W_C. Only where every W_B W_C of the model channel is far
+  // from zero and W_C inverts (uniform over the workgroup); else on g.
+  const bool scaled = NL == 1 && __all(fabsf(cw[0]) >= 1e-30f && fabsf(rwc[0]) <= 1e30f);
   const uint32_t rowb = sl_tab_lane(s, grp);
 
   // the loads of a channel's block round r
@@ -356,8 +364,11 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
   sl_build_table<NL>(sT, al, dti, dta, nw);
   __syncthreads();
 
-  auto run = [&](auto exact_tag) {
+  auto run = [&](auto exact_tag, auto scaled_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
+    constexpr bool SC = decltype(scaled_tag)::value && NL == 1;
+    // the lane's saved state h = W_B g from its recurrence variable
+    auto state = [&](int j, float v) { return SC ? v * rwc[j] : v * wb[j]; };
     for (int r0 = 0; r0 + sp < n_per_d; r0 += nslots * S) {
       const int b = chan_at(r0);
       const bool act = b < n_per_d;
@@ -399,7 +410,11 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
         float wq[kSLN];  // one state per lane: W_B W_C g of the lane's state after each event
         for16([&](auto q) {
           constexpr int Q = decltype(q)::value;
-          if constexpr (NL == 1) {
+          if constexpr (SC) {
+            g[0] = fmaf(av[0][Q], g[0], cw[0] * bcast_f<Q>(du2));  // g holds W_B W_C g
+            if (EXACT) P[0] *= av[0][Q];
+            wq[Q] = g[0];
+          } else if constexpr (NL == 1) {
             g[0] = fmaf(av[0][Q], g[0], bcast_f<Q>(du2));
             if (EXACT) P[0] *= av[0][Q];
             wq[Q] = cw[0] * g[0];
@@ -435,14 +450,14 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
 #pragma unroll
             for (int j = 0; j < NL; ++j) {
               const float Pn = EXACT ? P[j] : decay(sd * Al[j]);
-              reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s + kSLN * j] = make_float2(Pn, g[j] * wb[j]);
+              reinterpret_cast<float2*>(a.x + (ch * nck + xc) * 2 * N)[s + kSLN * j] = make_float2(Pn, state(j, g[j]));
             }
           }
         }
         const int pend = (bk + 1) * kSLB;  // events before the next pass start, when it is one
         if (a.chunk_g && pend % Sh::Pass == 0 && pend < n && pend / Sh::Pass < g_rows) {
 #pragma unroll
-          for (int j = 0; j < NL; ++j) a.chunk_g[(ch * g_rows + pend / Sh::Pass) * N + s + kSLN * j] = g[j] * wb[j];
+          for (int j = 0; j < NL; ++j) a.chunk_g[(ch * g_rows + pend / Sh::Pass) * N + s + kSLN * j] = state(j, g[j]);
         }
       };
       for (int r = 0; r * kSLPF < wblk; ++r) {
@@ -468,8 +483,13 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
       }
     }
   };
-  if (exact) run(std::true_type{});
-  else run(std::false_type{});
+  if (scaled) {
+    if (exact) run(std::true_type{}, std::true_type{});
+    else run(std::false_type{}, std::true_type{});
+  } else {
+    if (exact) run(std::true_type{}, std::false_type{});
+    else run(std::false_type{}, std::false_type{});
+  }
 }
 
 // nw: waves per workgroup, S: workgroups per model channel (the launch's
