@@ -339,9 +339,10 @@ __device__ __forceinline__ void sl_fwd_body(const bcm_scan_args& a, float* sT, i
   // One state per lane: the recurrence runs on the state's share of y,
   // q = W_B W_C g (q = a q + W_B W_C Δu², one DPP multiply and one fma per
   // event instead of a DPP move, an fma and a multiply), the saved states
-  // being q / W_C. Only where every W_B W_C of the model channel is far
-  // from zero and W_C inverts (uniform over the workgroup); else on g.
-  const bool scaled = NL == 1 && __all(fabsf(cw[0]) >= 1e-30f && fabsf(rwc[0]) <= 1e30f);
+  // being q / W_C. Only where every W_B W_C of the model channel and every
+  // 1 / W_C lie within [1e-20, 1e20] in magnitude (finite, far from
+  // underflow and overflow; uniform over the workgroup); else on g.
+  const bool scaled = NL == 1 && __all(fabsf(cw[0]) >= 1e-20f && fabsf(cw[0]) <= 1e20f && fabsf(rwc[0]) <= 1e20f);
   const uint32_t rowb = sl_tab_lane(s, grp);
 
   // the loads of a channel's block round r

@@ -149,16 +149,18 @@ def test_scan_clamped_decays(cuda_device):
 
 @pytest.mark.parametrize("use_acc", [False, True])
 def test_scan_zero_and_tiny_weights(cuda_device, use_acc):
-    """Model channels whose W_B W_C has a zero or denormal-sized entry (or a
-    W_C too small to invert): the one-state-per-lane forward runs its
-    recurrence on W_B W_C g only where every entry of the model channel is
-    far from zero, and on g elsewhere; both against the oracle, with long
-    channels (two 2048-event chunks of x, many passes of chunk_g)."""
+    """Model channels whose W_B W_C has a zero or tiny entry (or a W_C too
+    small to invert, or a huge one): the one-state-per-lane forward runs
+    its recurrence on W_B W_C g only where every entry of the model channel
+    and every 1 / W_C lie within [1e-20, 1e20], and on g elsewhere; both
+    against the oracle, with long channels (two 2048-event chunks of x,
+    many passes of chunk_g)."""
     c = _case(2, 8, 3000, 0.8, 16, torch.float32, seed=11)
     c["WC"][0, 3] = 0.0      # one zero: that model channel falls back
     c["WB"][1, 5] = 0.0
-    c["WC"][2, :] = 1e-36    # W_B W_C ~ 1e-37: falls back
-    c["WC"][3, 7] = 2e-31    # 1 / W_C overflows the bound: falls back
+    c["WC"][2, :] = 1e-30    # W_B W_C ~ 1e-31: falls back
+    c["WC"][3, 7] = 2e-21    # 1 / W_C beyond the bound: falls back
+    c["WB"][5, 2] = 1e21     # W_B W_C beyond the bound: falls back
     c["WB"][4, :] *= 1e-3    # small but far from the bounds: scaled
     _run_and_check(c, torch.float32, cuda_device, use_acc=use_acc)
 
