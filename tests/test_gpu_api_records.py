@@ -87,3 +87,18 @@ def test_understated_max_seqlen_still_reported(cuda_device):
     with pytest.raises(RuntimeError, match="more than max_seqlen"):
         selective_scan_flat_ch_fn(u, k, cu, int(ms) - 1, w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, D=w.D_skip,
                                   is_depthwise_bc=True)
+
+
+def test_restore_backward_sync_area_reuse(cuda_device):
+    """The one-kernel restore backward's per-stream sync area is reused and
+    grown across calls of other sizes (each call leaves it zero): small,
+    large, small again, each against the two-pass form on copies."""
+    for cfg, B in ((0, None), (1, 8), (0, None), (1, 4)):
+        w = make_workload(cfg, **({} if B is None else {"B": B})).to(cuda_device)
+        ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+        assert prov.event_index_for(t, cu, w.L) is not None
+        got = rdc.restore_dense_bwd(w.dout, t, cu, w.D, w.L)
+        ref = rdc.restore_dense_bwd(w.dout, t.clone(), cu.clone(), w.D, w.L)
+        assert_close(got.cpu(), ref.cpu().numpy(), 1e-5, 1e-6, f"dy config {cfg} B={B}")
+    areas = [a for (dev, _), a in rdc._sync_areas.items() if dev == cuda_device.index]
+    assert areas and all(int(a.abs().sum()) == 0 for a in areas)  # left zero
