@@ -11,12 +11,14 @@ them so that later calls of the drop-in API need not recompute it.
 
 Both are Python attributes of the returned tensors, valid only while those
 tensors are unchanged: a record keeps the data pointer, size and version
-counter of every tensor it depends on, and holds a reference to each one
-other than its holder, so a match cannot come from another tensor that
-reuses the memory (the holder's own memory lives as long as the record).
-A call whose tensors do not match computes what it needs, as for any other
-input.
+counter of every tensor it depends on, and a weak reference to each one
+other than its holder. A dependency that has been freed voids the record,
+so a match cannot come from another tensor that reuses the memory (the
+holder's own memory lives as long as the record), and a record keeps no
+tensor alive. A call whose tensors do not match computes what it needs, as
+for any other input.
 """
+import weakref
 
 _INDEX = "_bcm_event_index"
 _MAXLEN = "_bcm_max_seqlen"
@@ -34,18 +36,25 @@ class EventIndex:
 
     def __init__(self, bitmask, tile_start, seqlen, time_steps, channel_ids, cu_seqlens):
         self.bitmask, self.tile_start, self.seqlen = bitmask, tile_start, int(seqlen)
-        self.ch, self.cu = channel_ids, cu_seqlens
+        self.ch, self.cu = weakref.ref(channel_ids), weakref.ref(cu_seqlens)
         self.sigs = (_sig(time_steps), _sig(channel_ids), _sig(cu_seqlens))
         self.bm_ver = (bitmask._version, tile_start._version)
+
+    @staticmethod
+    def _same(ref, given, sig):
+        """given describes the data the record was made for: the recorded
+        tensor is still alive and unchanged, and given shares its data."""
+        rec = ref()
+        return rec is not None and _sig(rec) == sig and _sig(given) == sig
 
     def matches(self, time_steps, cu_seqlens, seqlen, channel_ids=None):
         if int(seqlen) != self.seqlen or (self.bitmask._version, self.tile_start._version) != self.bm_ver:
             return False
         if _sig(time_steps) != self.sigs[0]:
             return False
-        if cu_seqlens is not None and (_sig(cu_seqlens) != self.sigs[2] or _sig(self.cu) != self.sigs[2]):
+        if cu_seqlens is not None and not self._same(self.cu, cu_seqlens, self.sigs[2]):
             return False
-        if channel_ids is not None and (_sig(channel_ids) != self.sigs[1] or _sig(self.ch) != self.sigs[1]):
+        if channel_ids is not None and not self._same(self.ch, channel_ids, self.sigs[1]):
             return False
         return True
 

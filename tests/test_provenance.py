@@ -57,6 +57,23 @@ def test_max_seqlen_record():
     assert prov.max_seqlen_of(cu) is None and not prov.covers_max_seqlen(cu, 100)
 
 
+def test_freed_dependency_voids_the_record():
+    """A record keeps its channel_ids and cu_seqlens only weakly: once
+    either is freed, nothing can match it (its memory may hold another
+    tensor by then)."""
+    import gc
+    t, ch, cu, _, _ = _streams()
+    assert prov.event_index_for(t, None, 8, ch) is not None
+    del ch
+    gc.collect()
+    other = torch.zeros(4, dtype=torch.int32)  # may reuse the freed memory
+    assert prov.event_index_for(t, None, 8, other) is None
+    assert prov.event_index_for(t, cu, 8) is not None  # cu is still alive
+    del cu
+    gc.collect()
+    assert prov.event_index_for(t, torch.tensor([0, 2, 4], dtype=torch.int32), 8) is None
+
+
 def test_records_hold_no_reference_to_their_holder():
     import gc
     import weakref
@@ -66,8 +83,8 @@ def test_records_hold_no_reference_to_their_holder():
     gc.disable()
     try:
         del t, cu
-        # freed by reference counting alone (no cycle through a record): t,
-        # then cu, which only t's record still held
+        # freed by reference counting alone: no record keeps a tensor alive
+        # or forms a cycle
         assert rt() is None and rcu() is None
     finally:
         gc.enable()
