@@ -102,3 +102,22 @@ def test_restore_backward_sync_area_reuse(cuda_device):
         assert_close(got.cpu(), ref.cpu().numpy(), 1e-5, 1e-6, f"dy config {cfg} B={B}")
     areas = [a for (dev, _), a in rdc._sync_areas.items() if dev == cuda_device.index]
     assert areas and all(int(a.abs().sum()) == 0 for a in areas)  # left zero
+
+
+def test_api_path_without_events(cuda_device):
+    """A membrane with no event: the extraction records its (zero) longest
+    channel and no index; the API path runs and gives a zero output and
+    zero input gradient."""
+    w = make_workload(0).to(cuda_device)
+    w.membrane = torch.zeros_like(w.membrane)
+    ch, t, k, cu, counts, ms = ee.extract_base_events(w.membrane, w.threshold)
+    assert ch.numel() == 0 and int(ms.max()) == 0 and prov.max_seqlen_of(cu) == 0
+    x_conv = w.x_conv.detach().clone().requires_grad_(True)
+    params = [p.detach().clone().requires_grad_(True) for p in (w.dt_idle, w.dt_active, w.A, w.W_B, w.W_C, w.D_skip)]
+    u = e_model.GatherEventsFn.apply(x_conv, ch, t)
+    y, _ = selective_scan_flat_ch_fn(u, k, cu, int(ms.max()), *params[:5], D=params[5], is_depthwise_bc=True)
+    out = e_model.restore_dense_fn(y, t, cu, w.D, w.L)
+    out.backward(w.dout)
+    torch.cuda.synchronize()
+    assert out.shape == (w.B, w.L, w.D) and int(torch.count_nonzero(out)) == 0
+    assert x_conv.grad is not None and int(torch.count_nonzero(x_conv.grad)) == 0
