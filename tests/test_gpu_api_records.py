@@ -121,3 +121,18 @@ def test_api_path_without_events(cuda_device):
     torch.cuda.synchronize()
     assert out.shape == (w.B, w.L, w.D) and int(torch.count_nonzero(out)) == 0
     assert x_conv.grad is not None and int(torch.count_nonzero(x_conv.grad)) == 0
+
+
+@pytest.mark.parametrize("expand", [2, 3])
+def test_expanded_offsets_carry_the_maximum(cuda_device, expand):
+    """expand_base_events copies the base offsets' recorded maximum to the
+    logical offsets (every logical channel holds its base channel's events),
+    and the scan over them needs no length report."""
+    w = make_workload(0).to(cuda_device)
+    B, Dm = w.B, w.D
+    bch, bt, bk, bcu, _, bms = ee.extract_base_events(w.membrane, w.threshold)
+    ch, t, k, cu, ms = ee.expand_base_events(bch, bt, bk, bcu, B, Dm, expand)
+    assert prov.max_seqlen_of(cu) == int(ms) == int(bms)
+    assert prov.event_index_for(t, cu, w.L) is None  # the expanded streams carry no index
+    lens = (cu[1:] - cu[:-1]).max()
+    assert int(lens) == int(ms)
